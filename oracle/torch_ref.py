@@ -1,0 +1,66 @@
+"""TEST INFRASTRUCTURE -- numerical oracles (fp32 on CPU), never used by the product.
+
+Follows the reference's checks:
+* GEMM: ``torch.mm(A.float(), B.float())`` (``tests/test_modal_gpu.py:115``).
+* attention: ``softmax(q @ k^T / sqrt(d)) @ v`` in fp32
+  (``tests/test_modal_attention.py:92-98``), chunked over (batch, head)
+  to bound the score matrix, with an optional causal mask
+  (``kernel_examples/attention/mha_h100.cu:160-176``) and the natural-log
+  log-sum-exp of the scaled scores.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+
+def seeded_normal(shape, seed: int, scale: float = 1.0) -> torch.Tensor:
+    """``N(0,1) * scale`` from ``torch.Generator().manual_seed(seed)`` on CPU, as bf16."""
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g, dtype=torch.float32) * scale).to(torch.bfloat16)
+
+
+def gemm_ref(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """fp32 ``A @ B`` of bf16 inputs (``tests/test_modal_gpu.py:115``)."""
+    return torch.matmul(a.float(), b.float())
+
+
+def attention_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
+                  causal: bool = False, heads: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Naive fp32 attention over ``[..., S, D]``; returns ``(O, LSE)``.
+
+    ``LSE[..., s] = logsumexp_j(q_s . k_j * scale)`` (natural log).  With
+    ``heads`` set, only the first ``heads`` of the flattened (batch, head)
+    rows are computed (a bounded CPU sample).
+    """
+    d = q.shape[-1]
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    lead = q.shape[:-2]
+    qf = q.reshape(-1, q.shape[-2], d)
+    kf = k.reshape(-1, k.shape[-2], d)
+    vf = v.reshape(-1, v.shape[-2], v.shape[-1])
+    n = qf.shape[0] if heads is None else min(heads, qf.shape[0])
+    outs, lses = [], []
+    for h in range(n):
+        s = (qf[h].float() @ kf[h].float().t()) * scale
+        if causal:
+            sq, sk = s.shape
+            mask = torch.ones(sq, sk, dtype=torch.bool).tril_(diagonal=sk - sq)
+            s = s.masked_fill(~mask, float("-inf"))
+        lses.append(torch.logsumexp(s, dim=-1))
+        outs.append(torch.softmax(s, dim=-1) @ vf[h].float())
+    o = torch.stack(outs)
+    lse = torch.stack(lses)
+    if heads is None:
+        o = o.reshape(*lead, q.shape[-2], v.shape[-1])
+        lse = lse.reshape(*lead, q.shape[-2])
+    return o, lse
+
+
+def rel_err(out: torch.Tensor, ref: torch.Tensor) -> float:
+    """``max|out - ref| / max|ref|`` -- the acceptance metric (bar: 1e-2)."""
+    out, ref = out.float(), ref.float()
+    denom = ref.abs().max().item()
+    return (out - ref).abs().max().item() / (denom if denom > 0 else 1.0)

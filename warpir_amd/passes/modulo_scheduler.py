@@ -1,0 +1,259 @@
+"""Modulo scheduling of tile loops into a multi-buffered pipeline.
+
+Public API as in the reference (``warpir/passes/modulo_scheduler.py``):
+``MSInstructionEdge``, ``MSInstruction``, ``MSInstructionManager.solve``
+and ``kernel_pass``.  The model is the same; the solver is this
+package's own exact search (``_modsched_search``) instead of OR-Tools
+CP-SAT, which is not available on MI355X hosts here.
+
+``kernel_pass`` rewrites every top-level unit-step ``ForOp`` whose body
+is made of loads and MMAs into the buffer form: a ring of
+``num_stages`` shared slots per loaded tile, ``num_stages - 1`` prologue
+load steps, a steady-state loop that waits on the slot the MMA reads,
+refills the slot just freed and runs the MMA, and ``num_stages - 1``
+drain steps (``modulo_scheduler.py:233-358``).  On CDNA4 the ring
+becomes LDS slots filled by ``global_load_lds`` DMA and the waits become
+``s_waitcnt vmcnt`` + ``s_barrier``; see ``warpir_amd.lowering``.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Tuple
+
+from warpir_amd.ir.ops import (
+    AllocSharedOp,
+    BufSlotExpr,
+    ForOp,
+    Kernel,
+    MMABufOp,
+    MMAOp,
+    Op,
+    TMALoadBufOp,
+    TMALoadOp,
+    TMAStoreOp,
+    Value,
+    WaitBufOp,
+    YieldOp,
+)
+from warpir_amd.ir.types import SharedBufferType
+
+from . import _modsched_search
+
+# Cost model of the reference pass (modulo_scheduler.py:169-172, 186-190).
+RESOURCE_COUNTS = {"tma": 4, "tc": 1}
+MAX_CYCLES = 100
+DEPTH = 5
+LATENCY = {TMALoadOp: ("tma", 12), MMAOp: ("tc", 4), TMAStoreOp: ("tma", 12)}
+
+
+@dataclass
+class MSInstructionEdge:
+    """Dependence ``source -> dest`` across ``distance`` iterations (``:25-29``)."""
+
+    source: "MSInstruction"
+    dest: "MSInstruction"
+    distance: int
+
+
+@dataclass
+class MSInstruction:
+    """One schedulable instruction of the loop body (``:31-37``)."""
+
+    resource: str
+    latency: int
+    name: str
+    parent_edges: List[MSInstructionEdge]
+
+
+class PipelineError(KeyError):
+    """The loop cannot be rewritten into buffer form.
+
+    Raised where the reference pass fails with a ``KeyError``
+    (``modulo_scheduler.py:309``): an MMA operand that is not produced by
+    a load inside the loop, or a loop without an MMA.
+    """
+
+
+class MSInstructionManager:
+    """Collects instructions and solves the modulo schedule (``:40-166``)."""
+
+    def __init__(self) -> None:
+        self.instructions: List[MSInstruction] = []
+        self.child_edges: Dict[str, List[MSInstructionEdge]] = {}
+        # (depth, name) -> (start, end) of the solved schedule.
+        self.intervals: Dict[Tuple[int, str], Tuple[int, int]] = {}
+
+    def add_instruction(self, instruction: MSInstruction) -> None:
+        self.instructions.append(instruction)
+        for edge in instruction.parent_edges:
+            self.child_edges.setdefault(edge.source.name, []).append(edge)
+
+    def solve(self, max_cycles: int, depth: int, resource_counts: Dict[str, int],
+              use_verbose: bool = False):
+        """Solve for the minimum-makespan schedule.
+
+        Returns ``(prologue, steady_state, epilogue, ii, num_stages,
+        stage_of)`` as the reference does (``:108-162``), or six ``None``
+        when no schedule fits in ``max_cycles``:
+
+        * ``prologue[i]``     -- ``(logical_iter, name)`` pairs issued in fill step ``i``;
+        * ``steady_state[j]`` -- ``(name, buffer_offset)`` pairs of unrolled copy
+          ``num_stages - 1 + j``;
+        * ``epilogue[i]``     -- ``(name, stage - (i + 1))`` pairs of drain step ``i``;
+        * ``stage_of[name]``  -- ``start // ii`` of the instruction's first copy.
+        """
+        index = {ins.name: k for k, ins in enumerate(self.instructions)}
+        edges = []
+        for k, ins in enumerate(self.instructions):
+            for e in ins.parent_edges:
+                if e.source.name not in index:
+                    raise KeyError(e.source.name)
+                edges.append((index[e.source.name], k, e.distance))
+        problem = _modsched_search.Problem(
+            latencies=[ins.latency for ins in self.instructions],
+            resources=[ins.resource for ins in self.instructions],
+            edges=edges, depth=depth, max_cycles=max_cycles, capacity=resource_counts,
+        )
+        found = _modsched_search.solve(problem)
+        if found is None:
+            if use_verbose:
+                print("modulo schedule: no solution within", max_cycles, "cycles")
+            return None, None, None, None, None, None
+        ii, offsets, makespan = found
+        self.intervals = {}
+        for d in range(depth):
+            for ins, s in zip(self.instructions, offsets):
+                self.intervals[(d, ins.name)] = (s + d * ii, s + d * ii + ins.latency)
+        if use_verbose:
+            print(f"modulo schedule: ii={ii} makespan={makespan} offsets={offsets}")
+        return _shape_schedule(self.instructions, offsets, ii, depth)
+
+
+def _shape_schedule(instructions: List[MSInstruction], offsets: List[int], ii: int, depth: int):
+    names = [ins.name for ins in instructions]
+    # ii == 0 places every copy at the same cycle; everything is stage 0.
+    stage_of = {n: (s // ii if ii else 0) for n, s in zip(names, offsets)}
+    num_stages = max(stage_of.values()) + 1
+    prologue = [[(i - stage_of[n], n) for n in names if stage_of[n] <= i]
+                for i in range(num_stages - 1)]
+    steady_state = [[(n, k - stage_of[n]) for n in names] for k in range(num_stages - 1, depth)]
+    epilogue = [[(n, stage_of[n] - i) for n in names if stage_of[n] >= i]
+                for i in range(1, num_stages)]
+    return prologue, steady_state, epilogue, ii, num_stages, stage_of
+
+
+def _loop_instructions(loop: ForOp) -> Dict[str, MSInstruction]:
+    """One ``MSInstruction`` per load / MMA / store, keyed by the op's text (``:183-217``)."""
+    instrs: Dict[str, MSInstruction] = {}
+    for op in loop.body:
+        kind = LATENCY.get(type(op))
+        if kind is not None:
+            instrs[str(op)] = MSInstruction(resource=kind[0], latency=kind[1], name=str(op),
+                                            parent_edges=[])
+    producer: Dict[Value, MSInstruction] = {
+        op.result: instrs[str(op)] for op in loop.body if type(op) in (TMALoadOp, MMAOp)
+    }
+    carried = {ia.block_arg for ia in loop.iter_args}
+    yld = next(op for op in loop.body if isinstance(op, YieldOp))
+    next_value = {ia.block_arg: yld.values[k] for k, ia in enumerate(loop.iter_args)}
+    for op in loop.body:
+        ins = instrs.get(str(op))
+        if ins is None:
+            continue
+        # Only bare Value operands carry dependences; coordinate tuples do not.
+        for name, operand in vars(op).items():
+            if name == "result" or not isinstance(operand, Value):
+                continue
+            distance = 1 if operand in carried else 0
+            src = producer.get(next_value.get(operand, operand))
+            if src is not None:
+                ins.parent_edges.append(MSInstructionEdge(source=src, dest=ins, distance=distance))
+    return instrs
+
+
+def _pipeline_loop(loop: ForOp) -> Optional[List[Op]]:
+    instrs = _loop_instructions(loop)
+    manager = MSInstructionManager()
+    for ins in instrs.values():
+        manager.add_instruction(ins)
+    prologue, steady, epilogue, _ii, stages, stage_of = manager.solve(
+        max_cycles=MAX_CYCLES, depth=DEPTH, resource_counts=RESOURCE_COUNTS)
+    if prologue is None:
+        return None
+
+    by_name: Dict[str, Op] = {str(op): op for op in loop.body}
+    loads = [op for op in loop.body if isinstance(op, TMALoadOp)]
+    mmas = [op for op in loop.body if isinstance(op, MMAOp)]
+    if not mmas:
+        raise PipelineError("loop has no MMA to pipeline")
+    ring = {ld.result: Value(f"{ld.source.name.lower()}_bufs",
+                             SharedBufferType(tile_type=ld.result.type, count=stages))
+            for ld in loads}
+    for mma in mmas:
+        for operand in (mma.a, mma.b):
+            if operand not in ring:
+                raise PipelineError(f"MMA operand {operand!r} is not loaded inside the loop")
+    all_rings = tuple(ring[ld.result] for ld in loads)
+
+    out: List[Op] = [AllocSharedOp(result=ring[ld.result]) for ld in loads]
+    # Fill: prologue step i loads logical iteration i - stage into slot i (:255-269).
+    for step, items in enumerate(prologue):
+        for logical, name in items:
+            op = by_name[name]
+            if isinstance(op, TMALoadOp):
+                fixed = op.substitute({loop.induction_var: logical})
+                out.append(TMALoadBufOp(buf=ring[op.result], slot=step, source=op.source,
+                                        coords=fixed.coords))
+
+    def slot_of(stage: int) -> BufSlotExpr:
+        return BufSlotExpr(value=loop.induction_var, offset=-stage, modulus=stages)
+
+    body: List[Op] = [WaitBufOp(bufs=all_rings, slot=slot_of(stage_of[str(mmas[0])]))]
+    for name, _offset in steady[0]:
+        op = by_name[name]
+        slot = slot_of(stage_of[name])
+        if isinstance(op, TMALoadOp):
+            body.append(TMALoadBufOp(buf=ring[op.result], slot=slot, source=op.source,
+                                     coords=op.coords))
+        elif isinstance(op, MMAOp):
+            body.append(MMABufOp(result=op.result, a_buf=ring[op.a], a_slot=slot,
+                                 b_buf=ring[op.b], b_slot=slot, accum=op.accum))
+    body.append(next(op for op in loop.body if isinstance(op, YieldOp)))
+    out.append(ForOp(induction_var=loop.induction_var, start=stages - 1, stop=loop.stop,
+                     step=loop.step, tile_size=loop.tile_size, iter_args=loop.iter_args,
+                     body=tuple(body), results=loop.results))
+
+    # Drain: step e waits on drain slot e and runs the MMAs still in flight (:329-356).
+    for e, items in enumerate(epilogue):
+        slot = BufSlotExpr(value=None, offset=e, modulus=stages)
+        out.append(WaitBufOp(bufs=all_rings, slot=slot))
+        for name, _offset in items:
+            op = by_name[name]
+            if not isinstance(op, MMAOp):
+                continue
+            k = next(j for j, ia in enumerate(loop.iter_args) if ia.block_arg == op.accum)
+            out.append(MMABufOp(result=Value(f"{op.result.name}_ep{e}", op.result.type),
+                                a_buf=ring[op.a], a_slot=slot, b_buf=ring[op.b], b_slot=slot,
+                                accum=loop.results[k]))
+    return out
+
+
+def kernel_pass(kernel: Kernel) -> Kernel:
+    """Pipeline every top-level unit-step loop of *kernel* (``:168-358``).
+
+    Loops whose schedule has no solution are kept unchanged, as in the
+    reference.  Raises ``PipelineError`` (a ``KeyError``) on a loop whose
+    MMA reads a tile that is not loaded inside the loop.
+    """
+    body: List[Op] = []
+    for op in kernel.body:
+        if not isinstance(op, ForOp) or op.step != 1:
+            body.append(op)
+            continue
+        rewritten = _pipeline_loop(op)
+        body.extend([op] if rewritten is None else rewritten)
+    return Kernel(name=kernel.name, inputs=kernel.inputs, outputs=kernel.outputs, body=tuple(body))
+
+
+__all__ = ["MSInstructionEdge", "MSInstruction", "MSInstructionManager", "PipelineError",
+           "kernel_pass"]

@@ -1,0 +1,248 @@
+"""IR builders for the GEMM and FlashAttention-forward workloads.
+
+``build_gemm_kernel`` and ``build_attention_kernel`` with their default
+arguments construct the same IR as the reference's builder scripts
+(``tests/gemm_baseline_v2.py:31-88`` and
+``tests/attention_baseline.py:46-186``): same value names, types and op
+order (checked against the reference printer's text in the tests).  The
+keyword arguments widen them to the MI355X configurations -- block tiles
+of 256x256x64, per-wavefront accumulator slices, multi-head
+``[B, H, S, D]`` attention with a log-sum-exp output and causal block
+skipping -- using only additive ops.
+"""
+from __future__ import annotations
+
+import math
+
+from warpir_amd.ir import (
+    AddOp,
+    CausalMaskOp,
+    ColVecType,
+    CopyOp,
+    DivRowOp,
+    Exp2Op,
+    ForOp,
+    GPUType,
+    GlobalType,
+    IntAffineOp,
+    IntType,
+    IterArg,
+    Kernel,
+    Log2Op,
+    MMAOp,
+    MulOp,
+    MulRowOp,
+    MulScalarOp,
+    NegInftyOp,
+    RegTileType,
+    RowMaxOp,
+    RowSumOp,
+    SharedTileType,
+    SubOp,
+    SubRowOp,
+    TMALoadOp,
+    TMAStoreOp,
+    Value,
+    WaitOp,
+    YieldOp,
+    ZeroOp,
+)
+
+LOG2E = math.log2(math.e)
+LN2 = math.log(2.0)
+
+# The reference attention builder's exp2 scale for D=64 (tests/attention_baseline.py:42-43).
+REFERENCE_ATTENTION_SCALE = 0.125 * 1.44269504089
+
+
+def _bf16_global(tile: SharedTileType, batch: int = 1, depth: int = 1) -> GlobalType:
+    return GlobalType(data_type=GPUType.bf16, sub_tile_type=tile, batch=batch, depth=depth,
+                      rows=-1, cols=-1)
+
+
+def build_gemm_kernel(block_m: int = 64, block_n: int = 64, block_k: int = 64,
+                      wave_m: int = 16, wave_n: int = 64, name: str = "gemm") -> Kernel:
+    """``C[M, N] = A[M, K] @ B[K, N]``, bf16 in, fp32 accumulate, bf16 out.
+
+    One program per ``block_m x block_n`` tile of C at
+    ``(blockIdx.y, blockIdx.x)``; the loop walks ``ceil(N / block_k)``
+    K-tiles, where the loop bound input is named ``N`` as in the
+    reference (it is the reduction extent).  The accumulator type is the
+    per-wavefront slice ``wave_m x wave_n``, so a block runs
+    ``(block_m / wave_m) * (block_n / wave_n)`` wavefronts.
+
+    Defaults reproduce ``tests/gemm_baseline_v2.py:31-88``.
+    """
+    a_tile = SharedTileType(GPUType.bf16, block_m, block_k)
+    b_tile = SharedTileType(GPUType.bf16, block_k, block_n)
+    c_tile = SharedTileType(GPUType.bf16, block_m, block_n)
+    a_glob, b_glob, c_glob = _bf16_global(a_tile), _bf16_global(b_tile), _bf16_global(c_tile)
+    acc = RegTileType(GPUType.fp32, wave_m, wave_n)
+
+    A, B, C = Value("A", a_glob), Value("B", b_glob), Value("C_global", c_glob)
+    n_red = Value("N", IntType())
+    row, col = Value("blockIdx.y", IntType()), Value("blockIdx.x", IntType())
+    i = Value("i", IntType())
+    c_init, c_accum, c_final, c_new = (Value(n, acc) for n in ("c_init", "c_accum", "c_final", "c_new"))
+    a_sh, b_sh = Value("a_shared", a_tile), Value("b_shared", b_tile)
+
+    loop = ForOp(
+        induction_var=i, start=0, stop=n_red, step=1, tile_size=block_k,
+        iter_args=(IterArg(block_arg=c_accum, init=c_init),),
+        body=(
+            TMALoadOp(result=a_sh, source=A, coords=(0, 0, row, i)),
+            TMALoadOp(result=b_sh, source=B, coords=(0, 0, i, col)),
+            WaitOp(values=(a_sh, b_sh)),
+            MMAOp(result=c_new, a=a_sh, b=b_sh, accum=c_accum),
+            YieldOp(values=(c_new,)),
+        ),
+        results=(c_final,),
+    )
+    return Kernel(
+        name=name, inputs=(A, B, n_red), outputs=(C,),
+        body=(ZeroOp(result=c_init), loop,
+              TMAStoreOp(source=c_final, dest=C, coords=(0, 0, row, col))),
+    )
+
+
+def build_attention_kernel(d: int = 64, block: int = 64, warp_rows: int = 16,
+                           scale: float = REFERENCE_ATTENTION_SCALE) -> Kernel:
+    """Single-head FlashAttention forward in exp2 form.
+
+    Defaults reproduce ``tests/attention_baseline.py:46-186``: Q tile
+    resident, loop over K/V tiles with ``S = Q K^T``, online softmax in the
+    exp2 domain with ``scale = log2(e) / sqrt(d)``, ``O += bf16(P) V``,
+    final ``O / l``.
+    """
+    return _attention(name="attention_fwd", d=d, block_q=block, block_kv=block,
+                      wave_rows=warp_rows, scale=scale, multi_head=False, causal=False,
+                      with_lse=False)
+
+
+def build_mha_forward_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64,
+                             wave_rows: int = 32, causal: bool = False, with_lse: bool = True,
+                             name: str = "mha_fwd") -> Kernel:
+    """Multi-head FlashAttention forward over ``[B, H, S, D]`` tensors.
+
+    Program ``(blockIdx.x, blockIdx.y, blockIdx.z)`` = (query tile, head,
+    batch).  Outputs O ``[B, H, S, D]`` bf16 and, with ``with_lse``, the
+    natural-log log-sum-exp ``L[B, H, S]`` fp32 (as the plain
+    ``logsumexp(S * scale)``; the reference TK kernel stores a
+    ``-sqrt(D)``-scaled variant, ``mha_h100.cu:216-221``).  With ``causal``
+    the KV loop stops at the query tile's last row
+    (``IntAffineOp``) and the score tile is masked (``CausalMaskOp``).
+    """
+    return _attention(name=name, d=d, block_q=block_q, block_kv=block_kv, wave_rows=wave_rows,
+                      scale=LOG2E / math.sqrt(d), multi_head=True, causal=causal,
+                      with_lse=with_lse)
+
+
+def _attention(*, name, d, block_q, block_kv, wave_rows, scale, multi_head, causal, with_lse):
+    q_tile = SharedTileType(GPUType.bf16, block_q, d)
+    kv_tile = SharedTileType(GPUType.bf16, block_kv, d)
+    if multi_head:
+        q_glob = GlobalType(GPUType.bf16, q_tile)
+        kv_glob = GlobalType(GPUType.bf16, kv_tile)
+    else:
+        q_glob = kv_glob = _bf16_global(q_tile)
+    att_f = RegTileType(GPUType.fp32, wave_rows, block_kv)
+    att_b = RegTileType(GPUType.bf16, wave_rows, block_kv)
+    o_reg = RegTileType(GPUType.fp32, wave_rows, d)
+    cvec = ColVecType(GPUType.fp32, wave_rows, block_kv)
+
+    Q, K, V, O = Value("Q", q_glob), Value("K", kv_glob), Value("V", kv_glob), Value("O", q_glob)
+    n_kv = Value("N", IntType())
+    q_idx = Value("blockIdx.x", IntType())
+    if multi_head:
+        head, batch = Value("blockIdx.y", IntType()), Value("blockIdx.z", IntType())
+        bh = (batch, head)
+    else:
+        bh = (0, 0)
+
+    def v(n, t):
+        return Value(n, t)
+
+    q_sh = v("q_shared", q_tile)
+    o_init, max_init, norm_init = v("o_init", o_reg), v("max_init", cvec), v("norm_init", cvec)
+    i = v("i", IntType())
+    o_acc, max_vec, norm_vec = v("o_accum", o_reg), v("max_vec", cvec), v("norm_vec", cvec)
+    k_sh, v_sh = v("k_shared", kv_tile), v("v_shared", kv_tile)
+    att_zero, att = v("att_zero", att_f), v("att", att_f)
+    max_prev, max_new = v("max_prev", cvec), v("max_new", cvec)
+    att_scaled, max_new_sc, max_prev_sc = v("att_scaled", att_f), v("max_new_sc", cvec), v("max_prev_sc", cvec)
+    att_shifted, p_f = v("att_shifted", att_f), v("P_fp32", att_f)
+    corr_diff, corr = v("corr_diff", cvec), v("correction", cvec)
+    norm_rescaled, norm_new = v("norm_rescaled", cvec), v("norm_new", cvec)
+    o_rescaled, p_b, o_new = v("o_rescaled", o_reg), v("P_bf16", att_b), v("o_new", o_reg)
+    o_final, max_final, norm_final, o_norm = (v("o_final", o_reg), v("max_final", cvec),
+                                              v("norm_final", cvec), v("o_norm", o_reg))
+
+    scores = att
+    body = [
+        TMALoadOp(result=k_sh, source=K, coords=(*bh, i, 0)),
+        TMALoadOp(result=v_sh, source=V, coords=(*bh, i, 0)),
+        WaitOp(values=(k_sh, v_sh)),
+        ZeroOp(result=att_zero),
+        MMAOp(result=att, a=q_sh, b=k_sh, accum=att_zero, transpose_b=True),
+    ]
+    if causal:
+        scores = v("att_masked", att_f)
+        body.append(CausalMaskOp(result=scores, tile=att, row_tile=q_idx, col_tile=i))
+    body += [
+        CopyOp(result=max_prev, input=max_vec),
+        RowMaxOp(result=max_new, tile=scores, prev=max_vec),
+        MulScalarOp(result=att_scaled, input=scores, scalar=scale),
+        MulScalarOp(result=max_new_sc, input=max_new, scalar=scale),
+        MulScalarOp(result=max_prev_sc, input=max_prev, scalar=scale),
+        SubRowOp(result=att_shifted, tile=att_scaled, vec=max_new_sc),
+        Exp2Op(result=p_f, input=att_shifted),
+        SubOp(result=corr_diff, a=max_prev_sc, b=max_new_sc),
+        Exp2Op(result=corr, input=corr_diff),
+        MulOp(result=norm_rescaled, a=norm_vec, b=corr),
+        RowSumOp(result=norm_new, tile=p_f, prev=norm_rescaled),
+        MulRowOp(result=o_rescaled, tile=o_acc, vec=corr),
+        CopyOp(result=p_b, input=p_f),
+        MMAOp(result=o_new, a=p_b, b=v_sh, accum=o_rescaled),
+        YieldOp(values=(o_new, max_new, norm_new)),
+    ]
+
+    prologue = []
+    stop = n_kv
+    if causal:
+        stop = v("kv_stop", IntType())
+        prologue.append(IntAffineOp(result=stop, input=q_idx, mul=block_q, add=block_q))
+
+    loop = ForOp(
+        induction_var=i, start=0, stop=stop, step=1, tile_size=block_kv,
+        iter_args=(IterArg(block_arg=o_acc, init=o_init),
+                   IterArg(block_arg=max_vec, init=max_init),
+                   IterArg(block_arg=norm_vec, init=norm_init)),
+        body=tuple(body),
+        results=(o_final, max_final, norm_final),
+    )
+    kernel_body = [
+        TMALoadOp(result=q_sh, source=Q, coords=(*bh, q_idx, 0)),
+        WaitOp(values=(q_sh,)),
+        ZeroOp(result=o_init),
+        NegInftyOp(result=max_init),
+        ZeroOp(result=norm_init),
+        *prologue,
+        loop,
+        DivRowOp(result=o_norm, tile=o_final, vec=norm_final),
+        TMAStoreOp(source=o_norm, dest=O, coords=(*bh, q_idx, 0)),
+    ]
+    outputs = [O]
+    if with_lse:
+        lse_tile = SharedTileType(GPUType.fp32, block_q, 1)
+        L = Value("L", GlobalType(GPUType.fp32, lse_tile, cols=1))
+        m_sc, l2, lse2, lse = (v("max_final_sc", cvec), v("norm_log2", cvec),
+                               v("lse_log2", cvec), v("lse", cvec))
+        kernel_body += [
+            MulScalarOp(result=m_sc, input=max_final, scalar=scale),
+            Log2Op(result=l2, input=norm_final),
+            AddOp(result=lse2, a=m_sc, b=l2),
+            MulScalarOp(result=lse, input=lse2, scalar=LN2),
+            TMAStoreOp(source=lse, dest=L, coords=(*bh, q_idx, 0)),
+        ]
+        outputs.append(L)
+    return Kernel(name=name, inputs=(Q, K, V, n_kv), outputs=tuple(outputs), body=tuple(kernel_body))
