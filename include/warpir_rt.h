@@ -1,0 +1,90 @@
+/*
+ * warpir_rt -- the C-ABI launcher of the WarpIR MI355X (gfx950) backend.
+ *
+ * The reference has no native launcher of its own: its harness JIT-builds a
+ * pybind wrapper around each generated kernel and launches it with the
+ * triple-chevron syntax on the default stream
+ * (reference tests/test_modal_gpu.py:24-50, tests/test_modal_attention.py:25-39,
+ * built by tests/test_modal_gpu.py:80-99).  This library replaces that
+ * wrapper with a fixed, kernel-independent C ABI: a code object produced by
+ * the CDNA4 lowering is loaded once, its kernel looked up by the IR kernel's
+ * name, and launched with a packed kernel-argument buffer whose layout is the
+ * kernel's globals struct (inputs then outputs, in IR order; the reference's
+ * `global_vars`, warpir/lowering/lowering.py:291-298).
+ *
+ * Conventions
+ *   - Every function returns 0 on success or a hipError_t code; the message of
+ *     any code is available from wir_error_string().
+ *   - Plain pointers and sizes only.  Device buffers are owned by the caller
+ *     (PyTorch in the Python host); the library allocates no user memory.
+ *   - Streams are passed as opaque `void*` (a hipStream_t; NULL = the null
+ *     stream).  Launches are asynchronous on that stream.
+ */
+#ifndef WARPIR_RT_H
+#define WARPIR_RT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* wir_module_t;   /* a loaded code object (hipModule_t)      */
+typedef void* wir_function_t; /* a kernel inside a module (hipFunction_t) */
+typedef void* wir_event_t;    /* a timing event (hipEvent_t)              */
+
+/* ABI version of this header; bumped on any signature change. */
+#define WIR_RT_ABI_VERSION 1
+int wir_abi_version(void);
+
+/* Make `device` current for the calling thread. */
+int wir_set_device(int device);
+
+/* Device facts used by the lowering and by roofline reporting:
+ * compute-unit count, peak shader clock (kHz), LDS bytes per workgroup and
+ * the gfx architecture name (NUL-terminated, truncated to arch_len). */
+int wir_device_info(int device, int* num_cus, int* clock_khz, int* lds_per_block,
+                    char* arch, size_t arch_len);
+
+/* Load a code object image (an ELF .hsaco as bytes).  Replaces the
+ * reference's load_inline build-and-dlopen step (tests/test_modal_gpu.py:80-99). */
+int wir_module_load(const void* image, size_t size, wir_module_t* module);
+int wir_module_unload(wir_module_t module);
+
+/* Look up the kernel named `name` (the IR Kernel.name) in a loaded module. */
+int wir_module_get_function(wir_module_t module, const char* name, wir_function_t* function);
+
+/* Launch `function` on `stream` with grid (gx, gy, gz) of workgroups of
+ * (bx, by, bz) work-items and `dyn_lds` bytes of dynamic LDS.  `kernarg`
+ * points at `kernarg_size` bytes laid out as the kernel's globals struct.
+ * Replaces the reference launch wrappers (`gemm<<<grid, 128[, smem]>>>(g)`,
+ * tests/test_modal_gpu.py:24-50). */
+int wir_launch(wir_function_t function, unsigned gx, unsigned gy, unsigned gz,
+               unsigned bx, unsigned by, unsigned bz, unsigned dyn_lds, void* stream,
+               const void* kernarg, size_t kernarg_size);
+
+/* Kernel resource facts (from the code object's metadata): registers per
+ * work-item, static LDS bytes and the maximum work-group size. */
+int wir_function_attrs(wir_function_t function, int* num_regs, int* static_lds,
+                       int* max_threads);
+
+/* Wait for all work queued on `stream`, or on the whole device. */
+int wir_stream_sync(void* stream);
+int wir_device_sync(void);
+
+/* Timing events on a stream (the reference times with CUDA events,
+ * tests/test_modal_gpu.py:138-151). */
+int wir_event_create(wir_event_t* event);
+int wir_event_destroy(wir_event_t event);
+int wir_event_record(wir_event_t event, void* stream);
+int wir_event_elapsed_ms(wir_event_t start, wir_event_t end, float* ms);
+
+/* Human-readable message for a code returned by any function above. */
+const char* wir_error_string(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WARPIR_RT_H */

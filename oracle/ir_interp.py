@@ -35,14 +35,18 @@ import torch
 from warpir_amd.ir import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, ColVecType, CopyOp, DivRowOp, Exp2Op,
     ForOp, GPUType, IntAffineOp, Kernel, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp,
-    NegInftyOp, RegTileType, RowMaxOp, RowSumOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp,
+    NegInftyOp, RegTileType, RowMaxOp, RowSumOp, SlotViewOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp,
     TMAStoreOp, Value, WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
 
 BUILTINS = ("blockIdx.x", "blockIdx.y", "blockIdx.z")
 
 
-def _as4d(t: torch.Tensor) -> torch.Tensor:
+def _as4d(t: torch.Tensor, gtype=None) -> torch.Tensor:
+    """View a tensor as [batch, depth, rows, cols]; a global typed with
+    ``cols == 1`` gets its unit column appended (e.g. LSE ``[B, H, S]``)."""
+    if gtype is not None and getattr(gtype, "cols", -1) == 1 and t.shape[-1] != 1:
+        t = t.unsqueeze(-1)
     while t.dim() < 4:
         t = t.unsqueeze(0)
     return t
@@ -68,7 +72,7 @@ def grid_of(kernel: Kernel, tensors: Dict[str, torch.Tensor]) -> Tuple[int, int,
     for op in kernel.body:
         if not isinstance(op, TMAStoreOp):
             continue
-        t = _as4d(tensors[op.dest.name])
+        t = _as4d(tensors[op.dest.name], op.dest.type)
         sub = op.dest.type.sub_tile_type
         units = (1, 1, sub.rows, sub.cols)
         for p, c in enumerate(op.coords):
@@ -111,7 +115,7 @@ class Interpreter:
         return (self._int(slot.value) + slot.offset) % slot.modulus
 
     def _load(self, src: Value, coords, rows: int, cols: int) -> torch.Tensor:
-        g = _as4d(self.tensors[src.name])
+        g = _as4d(self.tensors[src.name], src.type)
         sub = src.type.sub_tile_type
         b, d, rt, ct = (self._int(c) for c in coords)
         r0, c0 = rt * sub.rows, ct * sub.cols
@@ -122,7 +126,7 @@ class Interpreter:
         return tile
 
     def _store(self, val, dest: Value, coords) -> None:
-        g = _as4d(self.tensors[dest.name])
+        g = _as4d(self.tensors[dest.name], dest.type)
         sub = dest.type.sub_tile_type
         b, d, rt, ct = (self._int(c) for c in coords)
         tile = val if val.dim() == 2 else val.reshape(-1, 1)
@@ -160,6 +164,8 @@ class Interpreter:
             s(op.result, self._load(op.source, op.coords, t.rows, t.cols))
         elif isinstance(op, AllocSharedOp):
             s(op.result, [None] * op.result.type.count)
+        elif isinstance(op, SlotViewOp):
+            s(op.result, g(op.buf)[self._slot(op.slot)])
         elif isinstance(op, TMALoadBufOp):
             t = op.buf.type.tile_type
             g(op.buf)[self._slot(op.slot)] = self._load(op.source, op.coords, t.rows, t.cols)

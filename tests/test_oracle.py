@@ -1,0 +1,101 @@
+"""The CPU oracle itself (CPU): interpreter vs torch closed forms.
+
+Config 1 of the benchmark set: the reference GEMM IR at M=N=K=1024,
+through ``kernel_pass``, printed, interpreted on the CPU and checked
+against ``torch.matmul`` (no GPU).  The interpreter follows the
+reference lowering's storage semantics (aliasing, in-place MMA
+accumulation, drain counter), so SSA and buffer forms must agree bit for
+bit.  Closed forms pin ``oracle.torch_ref``: identity B, one-hot V,
+constant K, and the log-sum-exp of constant scores.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle.ir_interp import run_kernel
+from oracle.torch_ref import attention_ref, gemm_ref, rel_err, seeded_normal
+from warpir_amd.passes.modulo_scheduler import GFX950_COST_MODEL, kernel_pass
+from warpir_amd.printing import format_kernel
+from warpir_amd.workloads import build_attention_kernel, build_gemm_kernel, build_mha_forward_kernel
+
+
+def _gemm(kernel, a, b):
+    c = torch.zeros(a.shape[0], b.shape[1], dtype=torch.bfloat16)
+    run_kernel(kernel, {"A": a, "B": b, "C_global": c}, {"N": a.shape[1]})
+    return c
+
+
+def test_config1_gemm_1024_through_pass_and_printer():
+    a = seeded_normal((1024, 1024), 0, 0.1)
+    b = seeded_normal((1024, 1024), 1, 0.1)
+    piped = kernel_pass(build_gemm_kernel())
+    assert "mma_buf" in format_kernel(piped)
+    c = _gemm(piped, a, b)
+    assert rel_err(c, gemm_ref(a, b)) <= 1e-2
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 64, 64), (128, 192, 64), (100, 72, 136), (64, 64, 200)])
+def test_ssa_and_buffer_forms_agree_bitwise(m, n, k):
+    a = seeded_normal((m, k), 5, 0.1)
+    b = seeded_normal((k, n), 6, 0.1)
+    ssa = _gemm(build_gemm_kernel(), a, b)
+    piped = _gemm(kernel_pass(build_gemm_kernel()), a, b)
+    assert torch.equal(ssa, piped)
+    assert rel_err(ssa, gemm_ref(a, b)) <= 1e-2
+
+
+def test_mi355x_gemm_ir_interpreted():
+    a = seeded_normal((300, 520), 2, 0.1)
+    b = seeded_normal((520, 264), 3, 0.1)
+    k = kernel_pass(build_gemm_kernel(256, 256, 32, 128, 128), cost_model=GFX950_COST_MODEL)
+    assert rel_err(_gemm(k, a, b), gemm_ref(a, b)) <= 1e-2
+
+
+def test_gemm_ref_identity_closed_form():
+    a = seeded_normal((64, 64), 9, 0.1)
+    assert torch.equal(gemm_ref(a, torch.eye(64, dtype=torch.bfloat16)), a.float())
+
+
+@pytest.mark.parametrize("n", [64, 256])
+def test_reference_attention_ir_interpreted(n):
+    q, k, v = (seeded_normal((n, 64), s) for s in (0, 1, 2))
+    o = torch.zeros(n, 64, dtype=torch.bfloat16)
+    run_kernel(build_attention_kernel(), {"Q": q, "K": k, "V": v, "O": o}, {"N": n})
+    ref, _ = attention_ref(q, k, v, scale=1 / math.sqrt(64))
+    assert rel_err(o, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_mha_ir_interpreted_with_lse(causal):
+    b, h, s, d = 1, 2, 256, 64
+    q, k, v = (seeded_normal((b, h, s, d), sd) for sd in (3, 4, 5))
+    o = torch.zeros(b, h, s, d, dtype=torch.bfloat16)
+    lse = torch.zeros(b, h, s, dtype=torch.float32)
+    kern = build_mha_forward_kernel(d=d, block_q=128, block_kv=64, wave_rows=32, causal=causal)
+    run_kernel(kern, {"Q": q, "K": k, "V": v, "O": o, "L": lse}, {"N": s})
+    ref, ref_lse = attention_ref(q, k, v, causal=causal)
+    assert rel_err(o, ref) <= 1e-2
+    assert (lse - ref_lse).abs().max().item() <= 1e-3
+
+
+def test_attention_ref_closed_forms():
+    s, d = 64, 64
+    q = seeded_normal((s, d), 1)
+    k = torch.zeros(s, d, dtype=torch.bfloat16)  # constant scores -> uniform softmax
+    v = seeded_normal((s, d), 2)
+    o, lse = attention_ref(q, k, v)
+    assert torch.allclose(o, v.float().mean(0, keepdim=True).expand(s, d), atol=1e-6)
+    assert torch.allclose(lse, torch.full((s,), math.log(s)), atol=1e-6)
+    # one-hot V columns return the probability matrix itself
+    v1 = torch.eye(s, dtype=torch.bfloat16)
+    k1 = seeded_normal((s, d), 3)
+    o1, _ = attention_ref(q, k1, v1)
+    p = torch.softmax((q.float() @ k1.float().t()) / math.sqrt(d), dim=-1)
+    assert torch.allclose(o1, p, atol=1e-6)
+
+
+def test_causal_first_row_attends_only_to_first_key():
+    q, k, v = (seeded_normal((1, 1, 64, 64), s) for s in (7, 8, 9))
+    o, _ = attention_ref(q, k, v, causal=True)
+    assert torch.allclose(o[0, 0, 0], v[0, 0, 0].float(), atol=1e-6)

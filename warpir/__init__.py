@@ -13,8 +13,8 @@ import sys
 _ALIASED = (
     "ir", "ir.ops", "ir.types",
     "printing", "printing.printer",
-    "passes", "passes.modulo_scheduler", "passes.warp_assigner",
-    "lowering",
+    "passes", "passes.modulo_scheduler",
+    "lowering", "runtime",
 )
 
 for _name in _ALIASED:

@@ -1,0 +1,574 @@
+// wir_cdna4.h -- device tile library of the WarpIR gfx950 (CDNA4) lowering.
+//
+// Every kernel emitted by warpir_amd.lowering.CDNA4Lowerer is this header
+// followed by one `extern "C" __global__` function whose body is a sequence
+// of calls into the templates below, one group per IR op.  The header is
+// pasted into the emitted source, so a generated .hip file is
+// self-contained (no other include than the HIP runtime header).
+//
+// Execution model (wave64):
+//   * A workgroup is NW wavefronts of 64 lanes.  Block-level tiles live in
+//     LDS; register tiles are per-wavefront slices.
+//   * Register tiles use the "lane = row" layout: the fp32 result of
+//     v_mfma_f32_{32x32x16,16x16x32}_bf16 is computed for the transposed
+//     product, so lane l owns logical row (l % MS) of each MS-row block and
+//     the accumulator registers run along the columns.  Row reductions of
+//     the online softmax are then lane-local plus one cross-lane step, and
+//     4 consecutive registers hold 4 consecutive columns (8-byte stores).
+//   * MFMA lane layouts on gfx950 (measured on the device):
+//       32x32x16: operand lane l -> row/col l%32, k = 8*(l/32) + j (j<8);
+//                 C reg i -> row 8*(i/4) + 4*(l/32) + i%4, col l%32.
+//       16x16x32: operand lane l -> row/col l%16, k = 8*(l/16) + j;
+//                 C reg i -> row 4*(l/16) + i, col l%16.
+//   * global_load_lds_dwordx4 writes lane l's 16 bytes at M0 + 16*l, so a
+//     tile load is 64 physical 16-byte LDS chunks per instruction and the
+//     LDS swizzle is expressed by choosing each lane's global address.
+//   * ds_read_b64_tr_b16: in each 16-lane group, lane s supplies row
+//     (s/4) and columns 4*(s%4)..+3 of a 4x16 bf16 block; afterwards lane s
+//     holds column s, rows 0..3.  It feeds MFMA operands from row-major
+//     [K][N] tiles without a transpose pass.
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace wir {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_char;
+
+// A 4-D row-major tensor [b, d, r, c] in HBM; the column stride is 1.
+// Mirrors the host-side ctypes structure of warpir_amd.runtime.
+template <typename T>
+struct gl {
+  T* data;
+  int b, d, r, c;
+  long long sb, sd, sr;
+};
+
+// Zero-filled source for out-of-bounds tile chunks (TMA zero-fill semantics).
+__device__ __attribute__((aligned(256))) unsigned int zero_page[64] = {0};
+
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+__device__ __forceinline__ lds_char* lds(char* generic) { return (lds_char*)(generic); }
+
+// ---------------------------------------------------------------------------
+// MFMA shape traits.
+template <int MS> struct MF;
+template <> struct MF<32> {
+  static constexpr int LG = 2;      // lane groups (64 / MS)
+  static constexpr int CREGS = 16;  // fp32 C registers per lane
+  static constexpr int KSTEP = 16;  // k per MFMA
+  typedef f32x16 cvec;
+  static __device__ __forceinline__ cvec mma(bf16x8 a, bf16x8 b, cvec c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct MF<16> {
+  static constexpr int LG = 4;
+  static constexpr int CREGS = 4;
+  static constexpr int KSTEP = 32;
+  typedef f32x4 cvec;
+  static __device__ __forceinline__ cvec mma(bf16x8 a, bf16x8 b, cvec c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Column (within an MS-column block) held by C register i of a lane in
+// lane group lh, in the lane = row layout.
+template <int MS>
+__device__ __forceinline__ int ccol(int i, int lh) {
+  return (i / 4) * (4 * MF<MS>::LG) + 4 * lh + (i % 4);
+}
+
+// ---------------------------------------------------------------------------
+// LDS tiles.  ROWS x COLS bf16, row-major, in 16-byte chunks (CPR per row)
+// with an XOR swizzle of the chunk index chosen by how the tile is read:
+//   ROWREAD -- ds_read_b128 of one row per lane (8 consecutive rows per
+//              phase): chunk ^ f(row) spreads 8 rows over 8 bank groups;
+//   TRREAD  -- ds_read_b64_tr_b16 (4 rows x 32 bytes per 16-lane group):
+//              chunk ^ 2*(row%4) spreads the 4 rows over 4 bank ranges.
+enum Role { ROWREAD = 0, TRREAD = 1 };
+
+template <int CPR, int ROLE>
+__device__ __forceinline__ int swz(int row) {
+  if (ROLE == ROWREAD) {
+    if (CPR >= 8) return row & 7;
+    if (CPR == 4) return (row >> 1) & 3;
+    if (CPR == 2) return (row >> 2) & 1;
+    return 0;
+  } else {
+    if (CPR >= 8) return (row & 3) << 1;
+    if (CPR == 4) return ((row >> 1) & 1) << 1;
+    return 0;
+  }
+}
+
+template <int ROWS_, int COLS_, int ROLE_>
+struct STile {
+  static constexpr int ROWS = ROWS_, COLS = COLS_, ROLE = ROLE_;
+  static constexpr int CPR = COLS / 8;
+  static constexpr int BYTES = ROWS * COLS * 2;
+  static_assert(COLS % 8 == 0, "tile columns must be a multiple of 8 bf16");
+  // Byte offset of the 16-byte chunk holding columns 8*chunk..8*chunk+7 of `row`.
+  static __device__ __forceinline__ int chunk_off(int row, int chunk) {
+    return (row * CPR + (chunk ^ swz<CPR, ROLE>(row))) * 16;
+  }
+  // Byte offset of element (row, col) (col need not be chunk aligned).
+  static __device__ __forceinline__ int elem_off(int row, int col) {
+    return chunk_off(row, col >> 3) + (col & 7) * 2;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Asynchronous global -> LDS tile load (the IR's tma_load / tma_load_buf).
+// The tile's rows start at global row `row0`, its columns at `col0`
+// (elements).  Chunks outside [0, r) x [0, c) or an out-of-range (b, d)
+// read the zero page.  Every wave issues exactly INSTR_PER_WAVE
+// global_load_lds_dwordx4 instructions, the count the lowering uses for
+// its vmcnt waits.
+template <class Tile, int NW>
+struct Loader {
+  static constexpr int CHUNKS = Tile::ROWS * Tile::CPR;
+  static constexpr int INSTR = CHUNKS / 64;
+  static_assert(CHUNKS % 64 == 0, "tile must be a multiple of 1 KiB");
+  static_assert(INSTR % NW == 0, "tile chunks must split evenly over the wavefronts");
+  static constexpr int INSTR_PER_WAVE = INSTR / NW;
+
+  static __device__ __forceinline__ void load(char* tile_base, const gl<bf16>& g, int b, int d,
+                                              int row0, int col0) {
+    const int lane = lane_id();
+    const int wave = wave_id();
+    const bool bd_ok = (unsigned)b < (unsigned)g.b && (unsigned)d < (unsigned)g.d;
+    const bf16* base = g.data + (long long)b * g.sb + (long long)d * g.sd;
+#pragma unroll
+    for (int j = 0; j < INSTR_PER_WAVE; ++j) {
+      const int ins = wave + j * NW;
+      const int p = ins * 64 + lane;  // physical chunk
+      const int row = p / Tile::CPR;
+      const int c = (p % Tile::CPR) ^ swz<Tile::CPR, Tile::ROLE>(row);
+      const int gr = row0 + row, gc = col0 + c * 8;
+      const bool ok = bd_ok && (unsigned)gr < (unsigned)g.r && (unsigned)gc < (unsigned)g.c;
+      const void* src = ok ? (const void*)(base + (long long)gr * g.sr + gc) : (const void*)zero_page;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(tile_base + ins * 1024),
+                                       16, 0, 0);
+    }
+  }
+};
+
+// Wait until at most N of this wave's vector-memory instructions are
+// outstanding (s_waitcnt vmcnt(N)), then synchronise the workgroup so every
+// wave's LDS-DMA writes are visible.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  __builtin_amdgcn_s_barrier();
+}
+
+__device__ __forceinline__ void barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS reads of this wave are done
+  __builtin_amdgcn_s_barrier();
+}
+
+// ---------------------------------------------------------------------------
+// Register tiles (per wave), lane = row layout.
+//   RTile<MS, R, C>: logical R x C fp32; f[cb][rb] is the MFMA C fragment
+//   of column block cb and row block rb.  Lane l owns row rb*MS + l%MS and,
+//   in register i, column cb*MS + ccol<MS>(i, l/MS).
+template <int MS, int R, int C>
+struct RTile {
+  static constexpr int RB = R / MS, CB = C / MS;
+  static_assert(R % MS == 0 && C % MS == 0, "register tile must be a multiple of the MFMA shape");
+  typename MF<MS>::cvec f[CB][RB];
+};
+
+// bf16 copy of an RTile: each group of 4 C registers packed as bf16x4.
+template <int MS, int R, int C>
+struct BTile {
+  static constexpr int RB = R / MS, CB = C / MS;
+  static constexpr int G = MF<MS>::CREGS / 4;
+  bf16x4 f[CB][RB][G];
+};
+
+// Column vector of a lane = row tile: one value per row block.
+template <int MS, int R>
+struct RVec {
+  static constexpr int RB = R / MS;
+  float v[RB];
+};
+
+template <int MS, int R, int C>
+__device__ __forceinline__ void fill(RTile<MS, R, C>& t, float x) {
+#pragma unroll
+  for (int cb = 0; cb < t.CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < t.RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < MF<MS>::CREGS; ++i) t.f[cb][rb][i] = x;
+}
+
+template <int MS, int R>
+__device__ __forceinline__ void fill(RVec<MS, R>& t, float x) {
+#pragma unroll
+  for (int rb = 0; rb < t.RB; ++rb) t.v[rb] = x;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA operands.
+//
+// "Row operand": 8 bf16 along k of one row per lane, from a ROWREAD LDS
+// tile (ds_read_b128).  Used for the IR's `a` operand of every MMA and for
+// `b` of a transpose_b MMA.
+template <class Tile, int MS>
+__device__ __forceinline__ bf16x8 row_operand(char* tile_base, int row_base, int kstep) {
+  const int lane = lane_id();
+  const int row = row_base + lane % MS;
+  const int chunk = kstep * MF<MS>::LG + lane / MS;
+  return *(const __attribute__((address_space(3))) bf16x8*)(lds(tile_base) + Tile::chunk_off(row, chunk));
+}
+
+// 4 consecutive k of one column per lane from a TRREAD [K][N] LDS tile via
+// ds_read_b64_tr_b16.  `k0` is this lane's first k (uniform per 16-lane
+// group), `n0` the group's first column.
+template <class Tile>
+__device__ __forceinline__ bf16x4 tr_operand4(char* tile_base, int k0, int n0) {
+  const int s = lane_id() & 15;
+  const int row = k0 + (s >> 2);
+  const int col = n0 + 4 * (s & 3);
+  i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(lds(tile_base) + Tile::elem_off(row, col)));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+__device__ __forceinline__ bf16x8 cat(bf16x4 lo, bf16x4 hi) {
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// 4 consecutive k of one row per lane from a ROWREAD tile (ds_read_b64).
+template <class Tile>
+__device__ __forceinline__ bf16x4 row_operand4(char* tile_base, int row, int k0) {
+  return *(const __attribute__((address_space(3))) bf16x4*)(lds(tile_base) + Tile::elem_off(row, k0));
+}
+
+// Hoisted row operands of a loop-invariant LDS tile (e.g. the resident Q
+// tile): RB row blocks x KS k-steps per wave.
+template <int MS, int RB, int KS>
+struct RowFrags {
+  bf16x8 f[RB][KS];
+};
+
+template <class Tile, int MS, int RB, int KS>
+__device__ __forceinline__ void load_row_frags(RowFrags<MS, RB, KS>& fr, char* tile_base, int row0) {
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) fr.f[rb][ks] = row_operand<Tile, MS>(tile_base, row0 + rb * MS, ks);
+}
+
+// ---------------------------------------------------------------------------
+// MMA, lane = row result layout.  Result rows = the IR operand `a`'s rows
+// [a_row0, a_row0 + R), result cols = `b`'s columns (or rows when
+// transposed) [b_col0, b_col0 + C).  The MFMA computes result^T =
+// b^T a^T: its A operand comes from `b`, its B operand from `a`.
+
+// acc += a @ b; a: ROWREAD LDS [.][K]; b: TRREAD LDS [K][.].
+template <int MS, int R, int C, class TA, class TB>
+__device__ __forceinline__ void mma_AB(RTile<MS, R, C>& acc, char* a_base, int a_row0, char* b_base,
+                                       int b_col0) {
+  static_assert(TA::COLS == TB::ROWS, "inner dimensions differ");
+  constexpr int K = TA::COLS;
+  constexpr int KS = K / MF<MS>::KSTEP;
+  static_assert(K % MF<MS>::KSTEP == 0, "k tile must be a multiple of the MFMA k");
+  const int lane = lane_id();
+  const int lh = lane / MS;
+  const int ngrp = (lane % MS) & ~15;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    bf16x8 bop[RTile<MS, R, C>::RB];
+#pragma unroll
+    for (int rb = 0; rb < acc.RB; ++rb) bop[rb] = row_operand<TA, MS>(a_base, a_row0 + rb * MS, ks);
+#pragma unroll
+    for (int cb = 0; cb < acc.CB; ++cb) {
+      const int k0 = ks * MF<MS>::KSTEP + 8 * lh;
+      const int n0 = b_col0 + cb * MS + ngrp;
+      const bf16x8 aop = cat(tr_operand4<TB>(b_base, k0, n0), tr_operand4<TB>(b_base, k0 + 4, n0));
+#pragma unroll
+      for (int rb = 0; rb < acc.RB; ++rb) acc.f[cb][rb] = MF<MS>::mma(aop, bop[rb], acc.f[cb][rb]);
+    }
+  }
+}
+
+// acc = a @ b^T with `a` from hoisted register fragments or LDS; b: ROWREAD LDS [.][K].
+template <int MS, int R, int C, class TB, int KS>
+__device__ __forceinline__ void mma_ABt_frags(RTile<MS, R, C>& acc, const RowFrags<MS, R / MS, KS>& a,
+                                              char* b_base, int b_row0) {
+  static_assert(TB::COLS == KS * MF<MS>::KSTEP, "inner dimensions differ");
+  fill(acc, 0.f);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+    for (int cb = 0; cb < acc.CB; ++cb) {
+      const bf16x8 aop = row_operand<TB, MS>(b_base, b_row0 + cb * MS, ks);
+#pragma unroll
+      for (int rb = 0; rb < acc.RB; ++rb) acc.f[cb][rb] = MF<MS>::mma(aop, a.f[rb][ks], acc.f[cb][rb]);
+    }
+  }
+}
+
+template <int MS, int R, int C, class TA, class TB>
+__device__ __forceinline__ void mma_ABt(RTile<MS, R, C>& acc, char* a_base, int a_row0, char* b_base,
+                                        int b_row0) {
+  static_assert(TA::COLS == TB::COLS, "inner dimensions differ");
+  constexpr int KS = TA::COLS / MF<MS>::KSTEP;
+  fill(acc, 0.f);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    bf16x8 bop[RTile<MS, R, C>::RB];
+#pragma unroll
+    for (int rb = 0; rb < acc.RB; ++rb) bop[rb] = row_operand<TA, MS>(a_base, a_row0 + rb * MS, ks);
+#pragma unroll
+    for (int cb = 0; cb < acc.CB; ++cb) {
+      const bf16x8 aop = row_operand<TB, MS>(b_base, b_row0 + cb * MS, ks);
+#pragma unroll
+      for (int rb = 0; rb < acc.RB; ++rb) acc.f[cb][rb] = MF<MS>::mma(aop, bop[rb], acc.f[cb][rb]);
+    }
+  }
+}
+
+// acc += a @ b with `a` a bf16 register tile (lane = row, k along its
+// columns) and b: TRREAD LDS [K][.].  The k order inside each MFMA follows
+// the register layout of `a`: its 4-register group g of column block kb
+// covers k = kb*MS + g*4*LG + 4*lh + (0..3).
+template <int MS, int R, int K, int C, class TB>
+__device__ __forceinline__ void mma_rAB(RTile<MS, R, C>& acc, const BTile<MS, R, K>& a, char* b_base,
+                                        int b_col0) {
+  static_assert(TB::ROWS == K, "inner dimensions differ");
+  constexpr int G = BTile<MS, R, K>::G;      // 4-register groups per C fragment
+  constexpr int NG = (K / MS) * G;            // groups along k
+  static_assert(NG % 2 == 0, "k extent must fill whole MFMAs");
+  const int lane = lane_id();
+  const int lh = lane / MS;
+  const int ngrp = (lane % MS) & ~15;
+#pragma unroll
+  for (int q = 0; q < NG; q += 2) {
+    const int kb0 = q / G, g0 = q % G, kb1 = (q + 1) / G, g1 = (q + 1) % G;
+    const int k0 = kb0 * MS + g0 * 4 * MF<MS>::LG + 4 * lh;
+    const int k1 = kb1 * MS + g1 * 4 * MF<MS>::LG + 4 * lh;
+#pragma unroll
+    for (int cb = 0; cb < acc.CB; ++cb) {
+      const int n0 = b_col0 + cb * MS + ngrp;
+      const bf16x8 aop = cat(tr_operand4<TB>(b_base, k0, n0), tr_operand4<TB>(b_base, k1, n0));
+#pragma unroll
+      for (int rb = 0; rb < acc.RB; ++rb)
+        acc.f[cb][rb] = MF<MS>::mma(aop, cat(a.f[kb0][rb][g0], a.f[kb1][rb][g1]), acc.f[cb][rb]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Element-wise and row operations on lane = row tiles.
+template <int MS, int R, int C, class F>
+__device__ __forceinline__ void map(RTile<MS, R, C>& out, const RTile<MS, R, C>& in, F fn) {
+#pragma unroll
+  for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < out.RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < MF<MS>::CREGS; ++i) out.f[cb][rb][i] = fn(in.f[cb][rb][i], rb);
+}
+
+template <int MS, int R, int C, class F>
+__device__ __forceinline__ void map2(RTile<MS, R, C>& out, const RTile<MS, R, C>& a,
+                                     const RTile<MS, R, C>& b, F fn) {
+#pragma unroll
+  for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < out.RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < MF<MS>::CREGS; ++i) out.f[cb][rb][i] = fn(a.f[cb][rb][i], b.f[cb][rb][i]);
+}
+
+template <int MS, int R, class F>
+__device__ __forceinline__ void vmap(RVec<MS, R>& out, const RVec<MS, R>& in, F fn) {
+#pragma unroll
+  for (int rb = 0; rb < out.RB; ++rb) out.v[rb] = fn(in.v[rb]);
+}
+
+template <int MS, int R, class F>
+__device__ __forceinline__ void vmap2(RVec<MS, R>& out, const RVec<MS, R>& a, const RVec<MS, R>& b, F fn) {
+#pragma unroll
+  for (int rb = 0; rb < out.RB; ++rb) out.v[rb] = fn(a.v[rb], b.v[rb]);
+}
+
+// Combine a value across the lanes that hold the same row (lane groups).
+template <int MS, class F>
+__device__ __forceinline__ float lane_group_reduce(float x, F op) {
+  if (MS == 32) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  } else {
+    x = op(x, __shfl_xor(x, 16));
+    return op(x, __shfl_xor(x, 32));
+  }
+}
+
+struct OpMax { __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct OpAdd { __device__ __forceinline__ float operator()(float a, float b) const { return a + b; } };
+
+// out[r] = op(op_c tile[r, c], prev[r]).
+template <int MS, int R, int C, class F>
+__device__ __forceinline__ void row_reduce(RVec<MS, R>& out, const RTile<MS, R, C>& t, const RVec<MS, R>& prev,
+                                           F op) {
+#pragma unroll
+  for (int rb = 0; rb < out.RB; ++rb) {
+    float x = t.f[0][rb][0];
+#pragma unroll
+    for (int cb = 0; cb < t.CB; ++cb)
+#pragma unroll
+      for (int i = (cb == 0 ? 1 : 0); i < MF<MS>::CREGS; ++i) x = op(x, t.f[cb][rb][i]);
+    x = lane_group_reduce<MS>(x, op);
+    out.v[rb] = op(x, prev.v[rb]);
+  }
+}
+
+template <int MS, int R, int C, class F>
+__device__ __forceinline__ void row_apply(RTile<MS, R, C>& out, const RTile<MS, R, C>& t, const RVec<MS, R>& v,
+                                          F fn) {
+#pragma unroll
+  for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < out.RB; ++rb) {
+      const float s = v.v[rb];
+#pragma unroll
+      for (int i = 0; i < MF<MS>::CREGS; ++i) out.f[cb][rb][i] = fn(t.f[cb][rb][i], s);
+    }
+}
+
+template <int MS, int R, int C>
+__device__ __forceinline__ void to_bf16(BTile<MS, R, C>& out, const RTile<MS, R, C>& in) {
+#pragma unroll
+  for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < out.RB; ++rb)
+#pragma unroll
+      for (int g = 0; g < out.G; ++g) {
+        bf16x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (bf16)in.f[cb][rb][4 * g + j];
+        out.f[cb][rb][g] = v;
+      }
+}
+
+// Lower-triangular mask: keep (row, col) when col_g <= row_g with
+// row_g = row_tile*BR + row0 + r and col_g = col_tile*BC + c.
+template <int MS, int R, int C>
+__device__ __forceinline__ void causal_mask(RTile<MS, R, C>& out, const RTile<MS, R, C>& t, int row_g0,
+                                            int col_g0) {
+  const int lane = lane_id();
+  const int lr = lane % MS, lh = lane / MS;
+  const float ninf = -__builtin_inff();
+#pragma unroll
+  for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < out.RB; ++rb) {
+      const int row = row_g0 + rb * MS + lr;
+#pragma unroll
+      for (int i = 0; i < MF<MS>::CREGS; ++i) {
+        const int col = col_g0 + cb * MS + ccol<MS>(i, lh);
+        out.f[cb][rb][i] = col <= row ? t.f[cb][rb][i] : ninf;
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Stores (the IR's tma_store) with TMA bounds semantics: elements outside
+// the tensor are dropped.
+
+// Register tile -> bf16 or fp32 global; rows from row0, cols from col0.
+template <typename T, int MS, int R, int C>
+__device__ __forceinline__ void store_tile(const gl<T>& g, const RTile<MS, R, C>& t, int b, int d, int row0,
+                                           int col0) {
+  if ((unsigned)b >= (unsigned)g.b || (unsigned)d >= (unsigned)g.d) return;
+  const int lane = lane_id();
+  const int lr = lane % MS, lh = lane / MS;
+  T* base = g.data + (long long)b * g.sb + (long long)d * g.sd;
+  const bool full_cols = (col0 + C <= g.c) && ((g.c & 3) == 0);
+#pragma unroll
+  for (int rb = 0; rb < t.RB; ++rb) {
+    const int row = row0 + rb * MS + lr;
+    if (row >= g.r) continue;
+    T* prow = base + (long long)row * g.sr;
+#pragma unroll
+    for (int cb = 0; cb < t.CB; ++cb)
+#pragma unroll
+      for (int q = 0; q < MF<MS>::CREGS / 4; ++q) {
+        const int col = col0 + cb * MS + ccol<MS>(4 * q, lh);
+        if (full_cols) {
+          if constexpr (sizeof(T) == 2) {
+            bf16x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = (bf16)t.f[cb][rb][4 * q + j];
+            *(bf16x4*)(prow + col) = v;
+          } else {
+            f32x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = t.f[cb][rb][4 * q + j];
+            *(f32x4*)(prow + col) = v;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (col + j < g.c) prow[col + j] = (T)t.f[cb][rb][4 * q + j];
+        }
+      }
+  }
+}
+
+// Column vector -> global column `col0` of rows row0.. (one writer lane per row).
+template <typename T, int MS, int R>
+__device__ __forceinline__ void store_vec(const gl<T>& g, const RVec<MS, R>& v, int b, int d, int row0, int col0) {
+  if ((unsigned)b >= (unsigned)g.b || (unsigned)d >= (unsigned)g.d || col0 >= g.c) return;
+  const int lane = lane_id();
+  if (lane >= MS) return;
+  T* base = g.data + (long long)b * g.sb + (long long)d * g.sd;
+#pragma unroll
+  for (int rb = 0; rb < v.RB; ++rb) {
+    const int row = row0 + rb * MS + lane;
+    if (row < g.r) base[(long long)row * g.sr + col0] = (T)v.v[rb];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Program-id remapping.  Workgroups are dispatched round-robin over the 8
+// XCDs (each with its own L2).  remap_xcd turns the hardware linear id into
+// a logical one such that each XCD walks a contiguous range of logical ids,
+// so neighbouring tiles (same A row panel / same attention head) share an
+// L2.  Any bijection is valid because programs are independent.
+__device__ __forceinline__ int remap_xcd(int hw_id, int total) {
+  constexpr int NXCD = 8;
+  const int per = total / NXCD;  // ids that split evenly
+  if (hw_id >= per * NXCD) return hw_id;
+  return (hw_id % NXCD) * per + hw_id / NXCD;
+}
+
+// Grouped tile order over a (tiles_y x tiles_x) grid: GROUP rows of tiles
+// are walked column by column, so consecutive ids reuse B column panels
+// while A row panels stay hot.
+template <int GROUP>
+__device__ __forceinline__ void grouped_tile(int id, int tiles_x, int tiles_y, int& tx, int& ty) {
+  const int per_group = GROUP * tiles_x;
+  const int grp = id / per_group;
+  const int first_y = grp * GROUP;
+  const int gsize = min(tiles_y - first_y, GROUP);
+  const int in = id % per_group;
+  ty = first_y + in % gsize;
+  tx = in / gsize;
+}
+
+}  // namespace wir

@@ -317,6 +317,20 @@ class MMABufOp(Op):
     accum: Value
 
 
+@dataclass(frozen=True)
+class SlotViewOp(Op):
+    """*Additive.* ``result`` names the shared tile held in ring slot ``slot`` of ``buf``.
+
+    Lets an ``MMAOp`` (with its ``transpose_b`` flag and register
+    operands) read a ring slot in the buffer form of a loop whose body is
+    more than loads and MMAs -- the pipelined FlashAttention loop.
+    """
+
+    result: Value
+    buf: Value
+    slot: BufIdx
+
+
 # --- control flow -----------------------------------------------------------
 
 @dataclass(frozen=True)

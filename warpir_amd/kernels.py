@@ -1,0 +1,63 @@
+"""Named kernel variants used by the tests, the benchmark and the smoke check.
+
+Each entry builds a WarpIR ``Kernel`` (through the front end and, where
+named, ``kernel_pass``).  ``__graft_entry__.build()`` lowers and compiles
+every entry into the code-object cache, so GPU runs load prebuilt
+``.hsaco`` files and never invoke hipcc.
+"""
+from __future__ import annotations
+
+from typing import Callable, Dict
+
+from warpir_amd.ir import Kernel
+from warpir_amd.passes.modulo_scheduler import GFX950_COST_MODEL, kernel_pass
+from warpir_amd.workloads import build_attention_kernel, build_gemm_kernel, build_mha_forward_kernel
+
+
+def _gemm_mi355x(block_k: int = 32, cost=GFX950_COST_MODEL) -> Kernel:
+    return kernel_pass(build_gemm_kernel(block_m=256, block_n=256, block_k=block_k, wave_m=128, wave_n=128,
+                                         name="gemm"), cost_model=cost)
+
+
+VARIANTS: Dict[str, Callable[[], Kernel]] = {
+    # The reference's own GEMM IR (tests/gemm_baseline_v2.py:31-88): SSA and pipelined.
+    "gemm_ref_ssa": lambda: build_gemm_kernel(),
+    "gemm_ref_piped": lambda: kernel_pass(build_gemm_kernel()),
+    # MI355X GEMM: 256x256 block tile, 4 wavefronts of 128x128, 3-stage LDS ring.
+    "gemm_256_k32": lambda: _gemm_mi355x(32),
+    # The reference's single-head attention IR (tests/attention_baseline.py:46-186).
+    "attn_ref_ssa": lambda: build_attention_kernel(),
+    # Multi-head FlashAttention forward, [B, H, S, D] with LSE.
+    "mha_d128": lambda: build_mha_forward_kernel(d=128, block_q=128, block_kv=64, wave_rows=32),
+    "mha_d64_causal": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
+                                                       causal=True, name="mha_fwd_causal"),
+}
+
+_handles: Dict[str, object] = {}
+
+
+def kernel(name: str) -> Kernel:
+    return VARIANTS[name]()
+
+
+def handle(name: str):
+    """A compiled, launchable ``KernelHandle`` for variant *name* (memoised)."""
+    from warpir_amd.runtime import compile_kernel
+
+    if name not in _handles:
+        _handles[name] = compile_kernel(VARIANTS[name]())
+    return _handles[name]
+
+
+def build_all(verbose: bool = False) -> Dict[str, str]:
+    """Lower and compile every variant; returns name -> code-object path."""
+    from warpir_amd.lowering import CDNA4Lowerer
+    from warpir_amd.runtime import compile_source
+
+    out = {}
+    for name, make in VARIANTS.items():
+        src = CDNA4Lowerer().lower(make())
+        out[name] = compile_source(src, force=True)
+        if verbose:
+            print(f"built {name}: {out[name]}", flush=True)
+    return out

@@ -1,0 +1,872 @@
+"""WarpIR tile IR -> gfx950 (CDNA4) HIP source.
+
+``CDNA4Lowerer().lower(kernel) -> str`` is the drop-in counterpart of the
+reference's ``ThunderKittensLowerer().lower(kernel) -> str``
+(``warpir/lowering/lowering.py:44,67-81``).  It keeps the reference
+lowering's behavioural contract (``lowering.py:87-113,196-207,454-488,
+572-606``):
+
+* a loop's iter_arg ``init``, its ``results`` and the yielded values name
+  the block argument's storage;
+* ``MMAOp`` without ``transpose_b`` accumulates in place into its result
+  (after copying ``accum`` there when the storages differ); with
+  ``transpose_b`` it computes ``a @ b^T`` and does not read ``accum``;
+* ``MMABufOp`` accumulates in place into ``accum`` and advances the drain
+  counter, which every ``drain(...)`` slot reads;
+* a ``tile_size`` loop runs ``ceil(stop / tile_size)`` trips;
+* kernel arguments are ``inputs`` then ``outputs`` in IR order.
+
+What differs is the machine mapping, which is CDNA4's own:
+
+* tile loads are LDS-DMA (``global_load_lds_dwordx4``) into swizzled LDS
+  tiles; out-of-bounds chunks read a zero page (TMA zero-fill);
+* ``WaitOp`` / ``WaitBufOp`` become ``s_waitcnt vmcnt(N)`` + ``s_barrier``
+  where ``N`` -- the loads this wave may keep in flight -- comes from a
+  concrete simulation of the IR's load/wait order (``_schedule``), and a
+  barrier is inserted before any load that would overwrite a tile another
+  wave may still be reading (write-after-read);
+* MMAs are ``v_mfma_f32_32x32x16_bf16`` (or ``16x16x32`` for 16-row
+  wavefront slices) computed for the transposed product so that every
+  register tile has the lane = row layout (see ``csrc/wir_cdna4.h``);
+* row reductions use one ``v_permlane32_swap`` after the lane-local part;
+* program ids are remapped so each XCD walks a contiguous, grouped range
+  of output tiles (L2 locality).
+
+``launch_config`` returns grid / block / LDS for concrete tensors, the
+information the reference keeps in its harness strings
+(``tests/test_modal_gpu.py:24-50``).
+"""
+from __future__ import annotations
+
+import math
+import os
+import re
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence, Tuple, Union
+
+from warpir_amd.ir.ops import (
+    AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, CopyOp, DivRowOp, Exp2Op, ForOp,
+    IntAffineOp, Kernel, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp, NegInftyOp,
+    Op, RowMaxOp, RowSumOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
+    WaitBufOp, WaitOp, YieldOp, ZeroOp,
+)
+from warpir_amd.ir.ops import SlotViewOp
+from warpir_amd.ir.types import (
+    ColVecType, GPUType, GlobalType, IntType, RegTileType, ScalarType, SharedBufferType,
+    SharedTileType,
+)
+
+BUILTINS = ("blockIdx.x", "blockIdx.y", "blockIdx.z")
+HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "csrc",
+                           "wir_cdna4.h")
+ROWREAD, TRREAD = 0, 1
+
+
+class LoweringError(ValueError):
+    """The kernel uses a shape or op combination this target cannot lower."""
+
+
+@dataclass
+class CDNA4Target:
+    """Machine parameters and code-generation choices for gfx950.
+
+    ``waves_per_eu`` = None picks 1 when a wavefront's accumulators exceed
+    128 registers per lane and 2 otherwise.  ``mfma`` = None picks the
+    32x32x16 MFMA when every register tile is a multiple of 32 rows and
+    columns, else 16x16x32.
+    """
+
+    arch: str = "gfx950"
+    lds_bytes: int = 160 * 1024
+    num_xcds: int = 8
+    waves_per_eu: Optional[int] = None
+    mfma: Optional[int] = None
+    xcd_remap: bool = True
+    group_m: int = 8
+
+
+@dataclass
+class LaunchConfig:
+    grid: Tuple[int, int, int]
+    block: Tuple[int, int, int]
+    dyn_lds: int = 0
+
+
+@dataclass
+class _Geometry:
+    nw: int            # wavefronts per workgroup
+    nw_c: int          # wavefronts along the result columns
+    ms: int            # MFMA shape (32 or 16)
+    waves_per_eu: int
+
+
+def _cname(name: str) -> str:
+    return "v_" + re.sub(r"[^0-9A-Za-z_]", "_", name)
+
+
+def _ceil_div(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+class CDNA4Lowerer:
+    """Lower a WarpIR ``Kernel`` to one self-contained gfx950 HIP source."""
+
+    def __init__(self, target: Optional[CDNA4Target] = None):
+        self.target = target or CDNA4Target()
+        self._reset()
+
+    # ------------------------------------------------------------------
+    # public API
+    # ------------------------------------------------------------------
+    def lower(self, kernel: Kernel) -> str:
+        """Return HIP C++ for *kernel* (``lowering.py:67-81``)."""
+        self._reset()
+        self.kernel = kernel
+        self._build_aliases(kernel.body)
+        self._classify(kernel)
+        self.geo = self._geometry(kernel)
+        self._assign_roles(kernel.body)
+        self._allocate_lds()
+        self.wait_n, self.war_barrier = _schedule(kernel, self)
+        self._pending_hoist = self._hoistable()
+        body: List[str] = []
+        self._emit_ops(kernel.body, body, 1)
+        return self._assemble(kernel, body)
+
+    def launch_config(self, kernel: Kernel, tensors: Dict[str, Sequence[int]]) -> LaunchConfig:
+        """Grid / block for concrete output shapes (``tensors``: name -> shape)."""
+        if self.kernel is not kernel:
+            self.lower(kernel)
+        grid = [1, 1, 1]
+        for op in _walk(kernel.body):
+            if not isinstance(op, TMAStoreOp):
+                continue
+            shape = _as4d(tensors[op.dest.name])
+            sub = op.dest.type.sub_tile_type
+            units = (1, 1, sub.rows, sub.cols)
+            for pos, c in enumerate(op.coords):
+                if isinstance(c, Value) and c.name in BUILTINS:
+                    axis = BUILTINS.index(c.name)
+                    grid[axis] = max(grid[axis], _ceil_div(shape[pos], units[pos]))
+        return LaunchConfig(grid=tuple(grid), block=(self.geo.nw * 64, 1, 1), dyn_lds=0)
+
+    @property
+    def num_threads(self) -> int:
+        return self.geo.nw * 64
+
+    def lds_bytes(self) -> int:
+        return self.lds_total
+
+    # ------------------------------------------------------------------
+    # analysis
+    # ------------------------------------------------------------------
+    def _reset(self) -> None:
+        self.kernel = None
+        self._aliases: Dict[str, str] = {}
+        self.values: Dict[str, Value] = {}
+        self.roles: Dict[str, int] = {}
+        self.lds_off: Dict[str, int] = {}
+        self.lds_total = 0
+        self.globals: List[Value] = []
+        self.drain_modulus: Optional[int] = None
+        self._loop_of_yield: Dict[int, ForOp] = {}
+        self._hoisted: Dict[str, Tuple[str, int]] = {}
+        self._pending_hoist: Dict[str, tuple] = {}
+        self._view_cache: Dict[str, SlotViewOp] = {}
+        self._view_kernel = None
+
+    def _build_aliases(self, ops) -> None:
+        """iter_arg init / loop results / yielded values -> block arg (``lowering.py:87-100``)."""
+        for op in ops:
+            if not isinstance(op, ForOp):
+                continue
+            for k, ia in enumerate(op.iter_args):
+                self._aliases[ia.init.name] = ia.block_arg.name
+                if k < len(op.results):
+                    self._aliases[op.results[k].name] = ia.block_arg.name
+            for inner in op.body:
+                if isinstance(inner, YieldOp):
+                    for k, y in enumerate(inner.values):
+                        if k < len(op.iter_args):
+                            self._aliases[y.name] = op.iter_args[k].block_arg.name
+            self._build_aliases(op.body)
+
+    def resolve(self, name: str) -> str:
+        seen = set()
+        while name in self._aliases and name not in seen:
+            seen.add(name)
+            name = self._aliases[name]
+        return name
+
+    def _classify(self, kernel: Kernel) -> None:
+        self.globals = list(kernel.inputs) + list(kernel.outputs)
+        for v in self.globals:
+            if not isinstance(v.type, (GlobalType, ScalarType)):
+                raise LoweringError(f"kernel argument {v!r} must be a global or an int")
+        for op in _walk(kernel.body):
+            for f in vars(op).values():
+                for v in _values_in(f):
+                    self.values.setdefault(self.resolve(v.name), v)
+
+    def _rtype(self, v: Value):
+        return self.values[self.resolve(v.name)].type
+
+    def _is_shared(self, v: Value) -> bool:
+        return isinstance(v.type, SharedTileType)
+
+    def _geometry(self, kernel: Kernel) -> _Geometry:
+        mmas = [op for op in _walk(kernel.body) if isinstance(op, (MMAOp, MMABufOp))]
+        if not mmas:
+            raise LoweringError("kernel has no MMA: nothing sets the wavefront layout")
+        nw = nw_c = None
+        dims = []
+        for op in mmas:
+            res_t = op.result.type if isinstance(op.result.type, RegTileType) else self._rtype(op.accum)
+            if not isinstance(res_t, RegTileType):
+                raise LoweringError(f"MMA result {op.result!r} is not a register tile")
+            r, c = res_t.rows, res_t.cols
+            dims += [r, c]
+            a_t, b_t, tb = _mma_operand_types(op)
+            block_c = b_t.rows if tb else b_t.cols
+            if block_c % c:
+                raise LoweringError(f"MMA {op.result.name}: {block_c} columns do not split into {c}")
+            this_c = block_c // c
+            if isinstance(a_t, SharedTileType):
+                if a_t.rows % r:
+                    raise LoweringError(f"MMA {op.result.name}: {a_t.rows} rows do not split into {r}")
+                this_nw = (a_t.rows // r) * this_c
+                if nw is not None and this_nw != nw:
+                    raise LoweringError("MMAs disagree on the wavefront count")
+                nw = this_nw
+            else:
+                dims += [a_t.rows, a_t.cols]
+            if nw_c is not None and this_c != nw_c:
+                raise LoweringError("MMAs disagree on the wavefront column split")
+            nw_c = this_c
+        if nw is None:
+            raise LoweringError("no MMA reads a shared tile as `a`: wavefront count unknown")
+        for op in _walk(kernel.body):
+            for v in _values_in(vars(op).get("result")):
+                if isinstance(v.type, RegTileType):
+                    dims += [v.type.rows, v.type.cols]
+        ms = self.target.mfma
+        if ms is None:
+            ms = 32 if all(d % 32 == 0 for d in dims) else 16
+        if any(d % ms for d in dims):
+            raise LoweringError(f"register tiles {sorted(set(dims))} are not multiples of the MFMA shape {ms}")
+        if nw * 64 > 1024:
+            raise LoweringError(f"{nw} wavefronts exceed the 1024-thread workgroup limit")
+        wpe = self.target.waves_per_eu
+        if wpe is None:
+            acc_regs = max((v.type.rows * v.type.cols // 64
+                            for op in _walk(kernel.body) for v in _values_in(vars(op).get("result"))
+                            if isinstance(v.type, RegTileType) and v.type.data_type == GPUType.fp32),
+                           default=0)
+            wpe = 1 if acc_regs > 64 else 2
+        return _Geometry(nw=nw, nw_c=nw_c, ms=ms, waves_per_eu=wpe)
+
+    def _assign_roles(self, ops) -> None:
+        """ROWREAD for tiles read along k by rows, TRREAD for [K][N] tiles read across k."""
+        def use(v: Value, role: int) -> None:
+            key = self._lds_key(v)
+            if key is None:
+                return
+            if self.roles.setdefault(key, role) != role:
+                raise LoweringError(f"shared tile {v.name} is read both by rows and transposed")
+
+        for op in _walk(ops):
+            if isinstance(op, MMAOp):
+                use(op.a, ROWREAD)
+                use(op.b, ROWREAD if op.transpose_b else TRREAD)
+            elif isinstance(op, MMABufOp):
+                use(op.a_buf, ROWREAD)
+                use(op.b_buf, TRREAD)
+
+    def _lds_key(self, v: Value) -> Optional[str]:
+        """Name of the LDS allocation behind a shared tile / ring / slot view."""
+        name = self.resolve(v.name)
+        view = self._views().get(name)
+        if view is not None:
+            return self.resolve(view.buf.name)
+        t = self.values[name].type if name in self.values else v.type
+        if isinstance(t, (SharedTileType, SharedBufferType)):
+            return name
+        return None
+
+    def _views(self) -> Dict[str, SlotViewOp]:
+        if self._view_kernel is not self.kernel:
+            self._view_cache = {self.resolve(op.result.name): op for op in _walk(self.kernel.body)
+                                if isinstance(op, SlotViewOp)}
+            self._view_kernel = self.kernel
+        return self._view_cache
+
+    def _allocate_lds(self) -> None:
+        off = 0
+        for op in _walk(self.kernel.body):
+            if isinstance(op, TMALoadOp):
+                key, t, count = self.resolve(op.result.name), op.result.type, 1
+            elif isinstance(op, AllocSharedOp):
+                key, t = self.resolve(op.result.name), op.result.type.tile_type
+                count = op.result.type.count
+            else:
+                continue
+            if key in self.lds_off:
+                continue
+            if t.data_type != GPUType.bf16:
+                raise LoweringError(f"shared tile {key} must be bf16")
+            self.roles.setdefault(key, ROWREAD)
+            self.lds_off[key] = off
+            off += _align(t.rows * t.cols * 2, 1024) * count
+        self.lds_total = off
+        if off > self.target.lds_bytes:
+            raise LoweringError(f"LDS use {off} B exceeds the {self.target.lds_bytes} B per workgroup")
+
+    # ------------------------------------------------------------------
+    # emission helpers
+    # ------------------------------------------------------------------
+    def tile_type_of(self, key: str) -> SharedTileType:
+        t = self.values[key].type
+        return t.tile_type if isinstance(t, SharedBufferType) else t
+
+    def stile(self, key: str) -> str:
+        t = self.tile_type_of(key)
+        return f"wir::STile<{t.rows}, {t.cols}, {self.roles.get(key, ROWREAD)}>"
+
+    def loads_per_wave(self, tile: SharedTileType) -> int:
+        chunks = tile.rows * tile.cols * 2 // 16
+        if chunks % 64:
+            raise LoweringError(f"tile {tile} is not a multiple of 1 KiB (64 LDS-DMA chunks)")
+        instr = chunks // 64
+        if instr % self.geo.nw:
+            raise LoweringError(f"tile {tile}: {instr} DMA instructions do not split over {self.geo.nw} wavefronts")
+        return instr // self.geo.nw
+
+    def _int(self, x) -> str:
+        if isinstance(x, int):
+            return str(x)
+        name = self.resolve(x.name)
+        if name in BUILTINS:
+            return "pid_" + name[-1]
+        if any(g.name == name for g in self.globals):
+            return f"globals.{_cname(name)[2:]}"
+        return _cname(name)
+
+    def _slot(self, slot) -> str:
+        if isinstance(slot, int):
+            return str(slot)
+        if slot.value is None:
+            return "wir_drain"
+        m = slot.modulus
+        return f"((({self._int(slot.value)}) + {slot.offset % m}) % {m})"
+
+    def _tile_ptr(self, v: Value) -> Tuple[str, str]:
+        """(LDS pointer expression, LDS key) of a shared tile or slot view."""
+        name = self.resolve(v.name)
+        view = self._views().get(name)
+        if view is not None:
+            key = self.resolve(view.buf.name)
+            t = self.tile_type_of(key)
+            stride = _align(t.rows * t.cols * 2, 1024)
+            return f"(smem + {self.lds_off[key]} + {self._slot(view.slot)} * {stride})", key
+        if name not in self.lds_off:
+            raise LoweringError(f"{v.name} is not a shared tile")
+        return f"(smem + {self.lds_off[name]})", name
+
+    def _buf_ptr(self, buf: Value, slot) -> Tuple[str, str]:
+        key = self.resolve(buf.name)
+        t = self.tile_type_of(key)
+        stride = _align(t.rows * t.cols * 2, 1024)
+        return f"(smem + {self.lds_off[key]} + {self._slot(slot)} * {stride})", key
+
+    def _var(self, v: Value) -> str:
+        return _cname(self.resolve(v.name))
+
+    def _reg_decl(self, v: Value) -> Optional[str]:
+        t = v.type
+        ms = self.geo.ms
+        if isinstance(t, RegTileType):
+            kind = "RTile" if t.data_type == GPUType.fp32 else "BTile"
+            return f"wir::{kind}<{ms}, {t.rows}, {t.cols}>"
+        if isinstance(t, ColVecType):
+            return f"wir::RVec<{ms}, {t.rows}>"
+        return None
+
+    # ------------------------------------------------------------------
+    # op emission
+    # ------------------------------------------------------------------
+    def _emit_ops(self, ops, out: List[str], depth: int) -> None:
+        for op in ops:
+            self._emit_op(op, out, depth)
+
+    def _emit_op(self, op: Op, out: List[str], depth: int) -> None:  # noqa: C901
+        pad = "  " * depth
+        ms = self.geo.ms
+        w = out.append
+        if isinstance(op, (AllocSharedOp, YieldOp)):
+            if isinstance(op, YieldOp):
+                self._emit_yield(op, out, depth)
+            return
+        if isinstance(op, ZeroOp) or isinstance(op, NegInftyOp):
+            val = "0.f" if isinstance(op, ZeroOp) else "-__builtin_inff()"
+            if isinstance(op.result.type, (RegTileType, ColVecType)):
+                w(f"{pad}wir::fill({self._var(op.result)}, {val});")
+                return
+            raise LoweringError(f"{type(op).__name__} on {op.result.type}")
+        if isinstance(op, (TMALoadOp, TMALoadBufOp)):
+            if id(op) in self.war_barrier:
+                w(f"{pad}wir::barrier();")
+            if isinstance(op, TMALoadOp):
+                ptr, key = self._tile_ptr(op.result)
+            else:
+                ptr, key = self._buf_ptr(op.buf, op.slot)
+            src = op.source
+            sub = src.type.sub_tile_type
+            b, d, rt, ct = (self._int(c) for c in op.coords)
+            w(f"{pad}wir::Loader<{self.stile(key)}, {self.geo.nw}>::load({ptr}, globals.{_cname(src.name)[2:]}, "
+              f"{b}, {d}, ({rt}) * {sub.rows}, ({ct}) * {sub.cols});")
+            return
+        if isinstance(op, (WaitOp, WaitBufOp)):
+            n = self.wait_n.get(id(op), 0)
+            w(f"{pad}wir::wait_vm_barrier<{n}>();")
+            return
+        if isinstance(op, SlotViewOp):
+            return  # views are resolved to LDS pointers where they are read
+        if isinstance(op, MMAOp):
+            self._emit_mma(op, out, depth)
+            return
+        if isinstance(op, MMABufOp):
+            a_ptr, a_key = self._buf_ptr(op.a_buf, op.a_slot)
+            b_ptr, b_key = self._buf_ptr(op.b_buf, op.b_slot)
+            t = self._rtype(op.accum)
+            acc = self._var(op.accum)
+            w(f"{pad}wir::mma_AB<{ms}, {t.rows}, {t.cols}, {self.stile(a_key)}, {self.stile(b_key)}>"
+              f"({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0);")
+            if self._var(op.result) != acc:
+                w(f"{pad}{self._var(op.result)} = {acc};")
+            if isinstance(op.a_slot, BufSlotExpr):
+                self.drain_modulus = op.a_slot.modulus
+                w(f"{pad}wir_drain = (wir_drain + 1) % {op.a_slot.modulus};")
+            return
+        if isinstance(op, CopyOp):
+            rt, it = op.result.type, op.input.type
+            if isinstance(rt, RegTileType) and isinstance(it, RegTileType) and rt.data_type != it.data_type:
+                if it.data_type != GPUType.fp32:
+                    raise LoweringError("only fp32 -> bf16 register conversion is supported")
+                w(f"{pad}wir::to_bf16({self._var(op.result)}, {self._var(op.input)});")
+            elif self._var(op.result) != self._var(op.input):
+                w(f"{pad}{self._var(op.result)} = {self._var(op.input)};")
+            return
+        if isinstance(op, (MulScalarOp, Exp2Op, Log2Op)):
+            fn = {MulScalarOp: f"x * {_flt(getattr(op, 'scalar', 0.0))}",
+                  Exp2Op: "__builtin_amdgcn_exp2f(x)", Log2Op: "__builtin_amdgcn_logf(x)"}[type(op)]
+            if isinstance(op.result.type, RegTileType):
+                w(f"{pad}wir::map({self._var(op.result)}, {self._var(op.input)}, "
+                  f"[](float x, int) {{ return {fn}; }});")
+            else:
+                w(f"{pad}wir::vmap({self._var(op.result)}, {self._var(op.input)}, [](float x) {{ return {fn}; }});")
+            return
+        if isinstance(op, (SubOp, MulOp, AddOp)):
+            sym = {SubOp: "-", MulOp: "*", AddOp: "+"}[type(op)]
+            fn = "map2" if isinstance(op.result.type, RegTileType) else "vmap2"
+            w(f"{pad}wir::{fn}({self._var(op.result)}, {self._var(op.a)}, {self._var(op.b)}, "
+              f"[](float a, float b) {{ return a {sym} b; }});")
+            return
+        if isinstance(op, (RowMaxOp, RowSumOp)):
+            red = "wir::OpMax()" if isinstance(op, RowMaxOp) else "wir::OpAdd()"
+            w(f"{pad}wir::row_reduce({self._var(op.result)}, {self._var(op.tile)}, {self._var(op.prev)}, {red});")
+            return
+        if isinstance(op, (SubRowOp, MulRowOp, DivRowOp)):
+            if isinstance(op, DivRowOp):
+                w(f"{pad}{{ wir::RVec<{ms}, {op.vec.type.rows}> rcp_; "
+                  f"wir::vmap(rcp_, {self._var(op.vec)}, [](float x) {{ return 1.0f / x; }});")
+                w(f"{pad}  wir::row_apply({self._var(op.result)}, {self._var(op.tile)}, rcp_, "
+                  f"[](float x, float s) {{ return x * s; }}); }}")
+                return
+            sym = "-" if isinstance(op, SubRowOp) else "*"
+            w(f"{pad}wir::row_apply({self._var(op.result)}, {self._var(op.tile)}, {self._var(op.vec)}, "
+              f"[](float x, float s) {{ return x {sym} s; }});")
+            return
+        if isinstance(op, CausalMaskOp):
+            t = op.tile.type
+            br, bc = t.rows * (self.geo.nw // self.geo.nw_c), t.cols * self.geo.nw_c
+            w(f"{pad}wir::causal_mask({self._var(op.result)}, {self._var(op.tile)}, "
+              f"({self._int(op.row_tile)}) * {br} + wave_row0, ({self._int(op.col_tile)}) * {bc} + wave_col0);")
+            return
+        if isinstance(op, IntAffineOp):
+            w(f"{pad}const int {self._var(op.result)} = ({self._int(op.input)}) * {op.mul} + {op.add};")
+            return
+        if isinstance(op, TMAStoreOp):
+            self._emit_store(op, out, depth)
+            return
+        if isinstance(op, ForOp):
+            self._emit_for(op, out, depth)
+            return
+        raise LoweringError(f"no CDNA4 lowering for {type(op).__name__}")
+
+    def _emit_yield(self, op: YieldOp, out: List[str], depth: int) -> None:
+        pad = "  " * depth
+        loop = self._loop_of_yield[id(op)]
+        for k, v in enumerate(op.values):
+            dst = self._var(loop.iter_args[k].block_arg)
+            if self._var(v) != dst:
+                out.append(f"{pad}{dst} = {self._var(v)};")
+
+    def _emit_mma(self, op: MMAOp, out: List[str], depth: int) -> None:
+        pad = "  " * depth
+        ms = self.geo.ms
+        res_t = op.result.type
+        res = self._var(op.result)
+        b_ptr, b_key = self._tile_ptr(op.b)
+        if op.transpose_b:
+            hoisted = self._hoisted.get(self.resolve(op.a.name))
+            if hoisted is not None:
+                out.append(f"{pad}wir::mma_ABt_frags<{ms}, {res_t.rows}, {res_t.cols}, {self.stile(b_key)}, "
+                           f"{hoisted[1]}>({res}, {hoisted[0]}, {b_ptr}, wave_col0);")
+                return
+            a_ptr, a_key = self._tile_ptr(op.a)
+            out.append(f"{pad}wir::mma_ABt<{ms}, {res_t.rows}, {res_t.cols}, {self.stile(a_key)}, "
+                       f"{self.stile(b_key)}>({res}, {a_ptr}, wave_row0, {b_ptr}, wave_col0);")
+            return
+        acc = self._var(op.accum)
+        if acc != res:
+            out.append(f"{pad}{res} = {acc};")
+        if self._is_shared(op.a) or self._lds_key(op.a) is not None:
+            a_ptr, a_key = self._tile_ptr(op.a)
+            out.append(f"{pad}wir::mma_AB<{ms}, {res_t.rows}, {res_t.cols}, {self.stile(a_key)}, "
+                       f"{self.stile(b_key)}>({res}, {a_ptr}, wave_row0, {b_ptr}, wave_col0);")
+            return
+        a_t = op.a.type
+        if not (isinstance(a_t, RegTileType) and a_t.data_type == GPUType.bf16):
+            raise LoweringError(f"MMA operand {op.a!r} must be a shared tile or a bf16 register tile")
+        out.append(f"{pad}wir::mma_rAB<{ms}, {a_t.rows}, {a_t.cols}, {res_t.cols}, {self.stile(b_key)}>"
+                   f"({res}, {self._var(op.a)}, {b_ptr}, wave_col0);")
+
+    def _emit_store(self, op: TMAStoreOp, out: List[str], depth: int) -> None:
+        pad = "  " * depth
+        dest = op.dest
+        if not isinstance(dest.type, GlobalType):
+            raise LoweringError("tma_store destination must be a global")
+        sub = dest.type.sub_tile_type
+        b, d, rt, ct = (self._int(c) for c in op.coords)
+        g = f"globals.{_cname(dest.name)[2:]}"
+        st = self._rtype(op.source)
+        if isinstance(st, RegTileType):
+            out.append(f"{pad}wir::store_tile({g}, {self._var(op.source)}, {b}, {d}, "
+                       f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols} + wave_col0);")
+        elif isinstance(st, ColVecType):
+            out.append(f"{pad}if (wave_col0 == 0) wir::store_vec({g}, {self._var(op.source)}, {b}, {d}, "
+                       f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols});")
+        else:
+            raise LoweringError("tma_store of a shared tile is not supported by the CDNA4 target")
+
+    def _emit_for(self, op: ForOp, out: List[str], depth: int) -> None:
+        pad = "  " * depth
+        for name, (var, ks, rows, loop) in self._pending_hoist.items():
+            if loop is op:
+                ptr, key = self._tile_ptr(self.values[name])
+                out.append(f"{pad}wir::RowFrags<{self.geo.ms}, {rows // self.geo.ms}, {ks}> {var};")
+                out.append(f"{pad}wir::load_row_frags<{self.stile(key)}>({var}, {ptr}, wave_row0);")
+                self._hoisted[name] = (var, ks)
+        for inner in op.body:
+            if isinstance(inner, YieldOp):
+                self._loop_of_yield[id(inner)] = op
+        stop = self._int(op.stop)
+        if op.tile_size:
+            stop = f"(({stop}) + {op.tile_size - 1}) / {op.tile_size}"
+        iv = self._var(op.induction_var)
+        out.append(f"{pad}for (int {iv} = {self._int(op.start)}; {iv} < {stop}; {iv} += {self._int(op.step)}) {{")
+        self._emit_ops(op.body, out, depth + 1)
+        out.append(f"{pad}}}")
+
+    # ------------------------------------------------------------------
+    # assembly
+    # ------------------------------------------------------------------
+    def _hoistable(self) -> Dict[str, tuple]:
+        """Shared tiles read as the row operand of a transpose_b MMA inside a
+        loop that never reloads them (e.g. the resident Q tile): their MFMA
+        fragments are read from LDS once, before the loop."""
+        hoist: Dict[str, tuple] = {}
+        for loop in _walk(self.kernel.body):
+            if not isinstance(loop, ForOp):
+                continue
+            written = {self.resolve(o.result.name) for o in _walk(loop.body) if isinstance(o, TMALoadOp)}
+            for o in _walk(loop.body):
+                if isinstance(o, MMAOp) and o.transpose_b:
+                    key = self._lds_key(o.a)
+                    name = self.resolve(o.a.name)
+                    if key is not None and key == name and name not in written and name not in hoist:
+                        t = self.tile_type_of(key)
+                        ks = t.cols // (16 if self.geo.ms == 32 else 32)
+                        res_t = o.result.type
+                        hoist[name] = (f"hf_{_cname(name)[2:]}", ks, res_t.rows, loop)
+        return hoist
+
+    def _assemble(self, kernel: Kernel, body: List[str]) -> str:
+        ms = self.geo.ms
+        # registers: one declaration per resolved value
+        decls = []
+        seen = set()
+        for op in _walk(kernel.body):
+            for v in _values_in(vars(op).get("result")):
+                name = self.resolve(v.name)
+                if name in seen:
+                    continue
+                seen.add(name)
+                typ = self._reg_decl(self.values.get(name, v))
+                if typ:
+                    decls.append(f"  {typ} {_cname(name)};")
+            if isinstance(op, ForOp):
+                for ia in op.iter_args:
+                    name = self.resolve(ia.block_arg.name)
+                    if name not in seen:
+                        seen.add(name)
+                        typ = self._reg_decl(ia.block_arg)
+                        if typ:
+                            decls.append(f"  {typ} {_cname(name)};")
+        fields = []
+        for v in self.globals:
+            if isinstance(v.type, GlobalType):
+                ctype = "wir::bf16" if v.type.data_type == GPUType.bf16 else "float"
+                fields.append(f"  wir::gl<{ctype}> {_cname(v.name)[2:]};")
+            else:
+                fields.append(f"  int {_cname(v.name)[2:]};")
+        uses = {c.name for op in _walk(kernel.body) for f in vars(op).values() for c in _values_in(f)}
+        dims = 3 if "blockIdx.z" in uses else 2
+        causal_x = any(isinstance(op, IntAffineOp) and isinstance(op.input, Value)
+                       and op.input.name == "blockIdx.x" for op in _walk(kernel.body))
+        wpe = self.geo.waves_per_eu
+        nt = self.geo.nw * 64
+        pid = _pid_code(dims, self.target, reverse_x=causal_x)
+        src = [
+            "// Generated by warpir_amd.lowering.CDNA4Lowerer for gfx950 -- do not edit.",
+            _header_text(),
+            "",
+            f"struct {kernel.name}_globals {{",
+            *fields,
+            "};",
+            "",
+            f'extern "C" __global__ void __attribute__((amdgpu_flat_work_group_size({nt}, {nt}), '
+            f"amdgpu_waves_per_eu({wpe}, {wpe})))",
+            f"{kernel.name}(const {kernel.name}_globals globals) {{",
+            f"  __shared__ __attribute__((aligned(1024))) char smem[{max(self.lds_total, 1024)}];",
+            *pid,
+            f"  const int wir_wave = wir::wave_id();",
+            f"  const int wave_row0 = (wir_wave / {self.geo.nw_c}) * {self._wave_rows()};",
+            f"  const int wave_col0 = (wir_wave % {self.geo.nw_c}) * {self._wave_cols()};",
+            "  int wir_drain = 0;",
+            "  (void)wave_row0; (void)wave_col0; (void)wir_drain;",
+            *decls,
+        ]
+        return "\n".join(src + body + ["}", ""])
+
+    def _wave_rows(self) -> int:
+        for op in _walk(self.kernel.body):
+            if isinstance(op, (MMAOp, MMABufOp)):
+                t = op.result.type if isinstance(op.result.type, RegTileType) else self._rtype(op.accum)
+                return t.rows
+        raise LoweringError("no MMA")
+
+    def _wave_cols(self) -> int:
+        for op in _walk(self.kernel.body):
+            if isinstance(op, (MMAOp, MMABufOp)):
+                t = op.result.type if isinstance(op.result.type, RegTileType) else self._rtype(op.accum)
+                return t.cols
+        raise LoweringError("no MMA")
+
+
+# ----------------------------------------------------------------------
+# schedule analysis: vmcnt per wait, write-after-read barriers
+# ----------------------------------------------------------------------
+def _schedule(kernel: Kernel, low: CDNA4Lowerer):
+    """Simulate the kernel's load / wait / MMA order with concrete trip counts.
+
+    Returns ``(wait_n, war)``: ``wait_n[id(wait_op)]`` is the number of this
+    wave's LDS-DMA instructions that may stay in flight at the wait (the
+    minimum over every simulated instance), and ``war`` the ids of load ops
+    that must be preceded by a workgroup barrier because a tile they
+    overwrite was read since the last barrier.
+    """
+    wait_n: Dict[int, int] = {}
+    war: set = set()
+    for trips in (0, 1, 2, 3, 5, 8):
+        sim = _Sim(low, trips)
+        sim.run(kernel.body)
+        for k, n in sim.wait_n.items():
+            wait_n[k] = min(wait_n.get(k, n), n)
+        war |= sim.war
+    return wait_n, war
+
+
+class _Sim:
+    def __init__(self, low: CDNA4Lowerer, trips: int):
+        self.low = low
+        self.trips = trips
+        self.env: Dict[str, int] = {}
+        self.drain = 0
+        self.issued: List[Tuple[Tuple[str, int], int]] = []   # (key, instructions)
+        self.read_since_barrier: set = set()
+        self.wait_n: Dict[int, int] = {}
+        self.war: set = set()
+        self.landed: set = set()
+
+    def val(self, x) -> int:
+        if isinstance(x, int):
+            return x
+        name = self.low.resolve(x.name)
+        return self.env.get(name, 0)
+
+    def slot(self, s) -> int:
+        if isinstance(s, int):
+            return s
+        if s.value is None:
+            return self.drain
+        return (self.val(s.value) + s.offset) % s.modulus
+
+    def key_of_tile(self, v: Value) -> Tuple[str, int]:
+        low = self.low
+        name = low.resolve(v.name)
+        view = low._views().get(name)
+        if view is not None:
+            return (low.resolve(view.buf.name), self.slot(view.slot))
+        return (name, 0)
+
+    def load(self, op, key, tile) -> None:
+        if key in self.read_since_barrier:
+            self.war.add(id(op))
+            self.read_since_barrier.clear()
+        self.landed.discard(key)
+        self.issued.append((key, self.low.loads_per_wave(tile)))
+
+    def wait(self, op, keys) -> None:
+        last = -1
+        for k, (key, _n) in enumerate(self.issued):
+            if key in keys:
+                last = k
+        n_after = sum(n for _k, n in self.issued[last + 1:]) if last >= 0 else sum(n for _k, n in self.issued)
+        self.wait_n[id(op)] = min(self.wait_n.get(id(op), n_after), n_after)
+        for key, _n in self.issued[:last + 1]:
+            self.landed.add(key)
+        self.issued = self.issued[last + 1:]
+        self.read_since_barrier.clear()
+
+    def read(self, key) -> None:
+        self.read_since_barrier.add(key)
+
+    def run(self, ops) -> None:
+        low = self.low
+        for op in ops:
+            if isinstance(op, TMALoadOp):
+                self.load(op, (low.resolve(op.result.name), 0), op.result.type)
+            elif isinstance(op, TMALoadBufOp):
+                key = (low.resolve(op.buf.name), self.slot(op.slot))
+                self.load(op, key, op.buf.type.tile_type)
+            elif isinstance(op, WaitOp):
+                self.wait(op, {self.key_of_tile(v) for v in op.values})
+            elif isinstance(op, WaitBufOp):
+                s = self.slot(op.slot)
+                self.wait(op, {(low.resolve(b.name), s) for b in op.bufs})
+            elif isinstance(op, MMAOp):
+                for v in (op.a, op.b):
+                    if low._lds_key(v) is not None:
+                        self.read(self.key_of_tile(v))
+            elif isinstance(op, MMABufOp):
+                self.read((low.resolve(op.a_buf.name), self.slot(op.a_slot)))
+                self.read((low.resolve(op.b_buf.name), self.slot(op.b_slot)))
+                if isinstance(op.a_slot, BufSlotExpr):
+                    self.drain = (self.drain + 1) % op.a_slot.modulus
+            elif isinstance(op, IntAffineOp):
+                self.env[low.resolve(op.result.name)] = self.val(op.input) * op.mul + op.add
+            elif isinstance(op, ForOp):
+                start = self.val(op.start)
+                step = self.val(op.step) or 1
+                iv = low.resolve(op.induction_var.name)
+                for t in range(self.trips):
+                    self.env[iv] = start + t * step
+                    self.run(op.body)
+                self.env[iv] = start + self.trips * step
+
+
+# ----------------------------------------------------------------------
+# helpers
+# ----------------------------------------------------------------------
+def _walk(ops):
+    for op in ops:
+        yield op
+        if isinstance(op, ForOp):
+            yield from _walk(op.body)
+
+
+def _values_in(x):
+    if isinstance(x, Value):
+        yield x
+    elif isinstance(x, (tuple, list)):
+        for y in x:
+            yield from _values_in(y)
+    elif isinstance(x, BufSlotExpr) and x.value is not None:
+        yield x.value
+
+
+def _mma_operand_types(op):
+    if isinstance(op, MMAOp):
+        a_t, b_t = op.a.type, op.b.type
+        if isinstance(b_t, SharedBufferType):
+            b_t = b_t.tile_type
+        if isinstance(a_t, SharedBufferType):
+            a_t = a_t.tile_type
+        return a_t, b_t, op.transpose_b
+    return op.a_buf.type.tile_type, op.b_buf.type.tile_type, False
+
+
+def _as4d(shape) -> Tuple[int, int, int, int]:
+    s = tuple(int(x) for x in shape)
+    while len(s) < 4:
+        s = (1,) + s
+    return s
+
+
+def _align(x: int, a: int) -> int:
+    return _ceil_div(x, a) * a
+
+
+def _flt(x: float) -> str:
+    return repr(float(x)) + "f"
+
+
+def _pid_code(dims: int, target: CDNA4Target, reverse_x: bool) -> List[str]:
+    lines = [
+        "  const int nx_ = gridDim.x, ny_ = gridDim.y, nz_ = gridDim.z;",
+        "  const int hw_ = blockIdx.x + nx_ * (blockIdx.y + ny_ * blockIdx.z);",
+    ]
+    if target.xcd_remap:
+        lines.append("  const int lid_ = wir::remap_xcd(hw_, nx_ * ny_ * nz_);")
+    else:
+        lines.append("  const int lid_ = hw_;")
+    if dims == 2:
+        lines += [
+            "  int pid_x, pid_y;",
+            f"  wir::grouped_tile<{target.group_m}>(lid_, nx_, ny_, pid_x, pid_y);",
+            "  const int pid_z = 0;",
+        ]
+    else:
+        lines += [
+            "  int pid_x = lid_ % nx_;",
+            "  const int pid_y = (lid_ / nx_) % ny_;",
+            "  const int pid_z = lid_ / (nx_ * ny_);",
+        ]
+    if reverse_x:
+        lines.append("  pid_x = nx_ - 1 - pid_x;  // longest causal rows first")
+    lines.append("  (void)pid_x; (void)pid_y; (void)pid_z;")
+    return lines
+
+
+_HEADER_CACHE: Dict[str, str] = {}
+
+
+def _header_text() -> str:
+    if "h" not in _HEADER_CACHE:
+        with open(HEADER_PATH, "r") as f:
+            _HEADER_CACHE["h"] = f.read()
+    return _HEADER_CACHE["h"]
+
+
+__all__ = ["CDNA4Lowerer", "CDNA4Target", "LaunchConfig", "LoweringError"]

@@ -17,7 +17,7 @@ becomes LDS slots filled by ``global_load_lds`` DMA and the waits become
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Tuple
 
 from warpir_amd.ir.ops import (
@@ -44,6 +44,28 @@ RESOURCE_COUNTS = {"tma": 4, "tc": 1}
 MAX_CYCLES = 100
 DEPTH = 5
 LATENCY = {TMALoadOp: ("tma", 12), MMAOp: ("tc", 4), TMAStoreOp: ("tma", 12)}
+
+
+@dataclass
+class CostModel:
+    """Latencies (resource, cycles) per op type, resource capacities and the
+    solver horizon.  ``kernel_pass`` uses the reference's constants unless
+    given another model."""
+
+    latency: Dict[type, Tuple[str, int]]
+    resources: Dict[str, int]
+    max_cycles: int = MAX_CYCLES
+    depth: int = DEPTH
+
+
+REFERENCE_COST_MODEL = CostModel(latency=dict(LATENCY), resources=dict(RESOURCE_COUNTS))
+
+# gfx950, in units of 256 cycles for a 256x256x32 block step: one K-step of
+# MFMAs on a SIMD is 4 units (32 v_mfma_f32_32x32x16_bf16 of 32 cycles),
+# an LDS-DMA tile load under load is ~8 units from issue to landing.  The
+# optimum is ii=4 with the MMA two stages behind its loads: a 3-slot ring.
+GFX950_COST_MODEL = CostModel(latency={TMALoadOp: ("tma", 8), MMAOp: ("tc", 4), TMAStoreOp: ("tma", 8)},
+                              resources={"tma": 4, "tc": 1})
 
 
 @dataclass
@@ -142,11 +164,11 @@ def _shape_schedule(instructions: List[MSInstruction], offsets: List[int], ii: i
     return prologue, steady_state, epilogue, ii, num_stages, stage_of
 
 
-def _loop_instructions(loop: ForOp) -> Dict[str, MSInstruction]:
+def _loop_instructions(loop: ForOp, cost: CostModel) -> Dict[str, MSInstruction]:
     """One ``MSInstruction`` per load / MMA / store, keyed by the op's text (``:183-217``)."""
     instrs: Dict[str, MSInstruction] = {}
     for op in loop.body:
-        kind = LATENCY.get(type(op))
+        kind = cost.latency.get(type(op))
         if kind is not None:
             instrs[str(op)] = MSInstruction(resource=kind[0], latency=kind[1], name=str(op),
                                             parent_edges=[])
@@ -171,13 +193,13 @@ def _loop_instructions(loop: ForOp) -> Dict[str, MSInstruction]:
     return instrs
 
 
-def _pipeline_loop(loop: ForOp) -> Optional[List[Op]]:
-    instrs = _loop_instructions(loop)
+def _pipeline_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
+    instrs = _loop_instructions(loop, cost)
     manager = MSInstructionManager()
     for ins in instrs.values():
         manager.add_instruction(ins)
     prologue, steady, epilogue, _ii, stages, stage_of = manager.solve(
-        max_cycles=MAX_CYCLES, depth=DEPTH, resource_counts=RESOURCE_COUNTS)
+        max_cycles=cost.max_cycles, depth=cost.depth, resource_counts=cost.resources)
     if prologue is None:
         return None
 
@@ -238,22 +260,24 @@ def _pipeline_loop(loop: ForOp) -> Optional[List[Op]]:
     return out
 
 
-def kernel_pass(kernel: Kernel) -> Kernel:
+def kernel_pass(kernel: Kernel, cost_model: Optional[CostModel] = None) -> Kernel:
     """Pipeline every top-level unit-step loop of *kernel* (``:168-358``).
 
     Loops whose schedule has no solution are kept unchanged, as in the
     reference.  Raises ``PipelineError`` (a ``KeyError``) on a loop whose
-    MMA reads a tile that is not loaded inside the loop.
+    MMA reads a tile that is not loaded inside the loop.  ``cost_model``
+    defaults to the reference's constants.
     """
+    cost = cost_model or REFERENCE_COST_MODEL
     body: List[Op] = []
     for op in kernel.body:
         if not isinstance(op, ForOp) or op.step != 1:
             body.append(op)
             continue
-        rewritten = _pipeline_loop(op)
+        rewritten = _pipeline_loop(op, cost)
         body.extend([op] if rewritten is None else rewritten)
     return Kernel(name=kernel.name, inputs=kernel.inputs, outputs=kernel.outputs, body=tuple(body))
 
 
 __all__ = ["MSInstructionEdge", "MSInstruction", "MSInstructionManager", "PipelineError",
-           "kernel_pass"]
+           "CostModel", "REFERENCE_COST_MODEL", "GFX950_COST_MODEL", "kernel_pass"]

@@ -30,6 +30,7 @@ from warpir_amd.ir.ops import (
     Op,
     RowMaxOp,
     RowSumOp,
+    SlotViewOp,
     SubOp,
     SubRowOp,
     TMALoadBufOp,
@@ -119,6 +120,7 @@ _LINE: Dict[type, Callable[[Op], str]] = {
     CausalMaskOp: lambda op: (
         f"{op.result!r} = causal_mask({op.tile!r}, {_coord(op.row_tile)}, {_coord(op.col_tile)})"
     ),
+    SlotViewOp: lambda op: f"{op.result!r} = slot_view({op.buf.name}[{_slot(op.slot)}])",
     IntAffineOp: lambda op: (
         f"{op.result!r} = int_affine({_coord(op.input)}, {op.mul}, {op.add})"
     ),
