@@ -1,0 +1,213 @@
+"""Benchmark of the WarpIR MI355X backend's hot path (one JSON line).
+
+Headline (``value``): bf16 GEMM C = A @ B at M = N = K = 8192, the
+WarpIR-generated, modulo-scheduled HIP kernel, TFLOP/s on one MI355X.
+The same line carries FlashAttention forward, non-causal,
+B16 H16 S4096 D128 (``fa_fwd``), the second workload the metric names.
+
+A "step" is one launch of the generated kernel over one batch of
+synthetic, seeded inputs already resident in HBM.  Timing: ``--warmup``
+untimed launches, then ``--steps`` launches bracketed by device
+synchronisation and HIP events recorded through the C ABI on the
+stream the kernels are launched on.
+
+``roofline``: algorithmic FLOPs per launch (2MNK for GEMM, 4BHS^2D for
+attention) over the average launch duration, against MI355X's dense
+bf16 MFMA peak (2.5 PFLOP/s).  ``cpu_baseline``: the reference's oracle
+path (``torch.matmul`` on fp32, naive fp32 attention) on the host cores,
+on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (AMD published)
+PEAK_HBM_GBS = 8000.0
+METRIC = "bf16 TFLOP/s + % MFMA peak: GEMM 8192³ and FA-fwd B16 H16 S4096 D128"
+
+
+def _time_launches(launch, steps: int, warmup: int, stream):
+    import torch
+
+    from warpir_amd.runtime import Event
+
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    e0, e1 = Event(), Event()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_ms(e1) / steps, wall * 1e3 / steps
+
+
+def _traffic_from_profiles(kernel: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    return None
+
+
+def bench_gemm(steps, warmup, cpu: bool):
+    import torch
+
+    from oracle.torch_ref import gemm_ref, seeded_normal
+    from warpir_amd import kernels
+
+    m = n = k = 8192
+    a = seeded_normal((m, k), 0, 0.1).cuda()
+    b = seeded_normal((k, n), 1, 0.1).cuda()
+    c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    h = kernels.handle("gemm_256_k64")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():
+        h(A=a, B=b, N=k, C_global=c)
+
+    ms, wall_ms = _time_launches(launch, steps, warmup, stream)
+    flops = 2.0 * m * n * k
+    tflops = flops / (ms * 1e-3) / 1e12
+    res = {
+        "value": tflops, "ms_per_step": ms, "wall_ms_per_step": wall_ms,
+        "config": {"workload": "gemm_bf16_8192x8192x8192", "M": m, "N": n, "K": k,
+                   "kernel": "gemm_256_k64", "block_tile": [256, 256, 64], "lds_stages": 2,
+                   "wavefronts": 4},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / PEAK_BF16_TFLOPS,
+                     "traffic": _traffic_from_profiles("gemm_256_k64")},
+    }
+    if cpu:
+        res["cpu_baseline"] = _cpu_gemm(a.cpu(), b.cpu(), gemm_ref)
+    return res
+
+
+def _cpu_gemm(a, b, gemm_ref):
+    import torch
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    rows = 512
+    sa = a[:rows]
+    gemm_ref(sa, b)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        gemm_ref(sa, b)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    flops = 2.0 * rows * b.shape[0] * b.shape[1]
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port", "os_cpu_count": os.cpu_count(),
+            "sample": f"torch.matmul fp32 on {rows} of 8192 rows of A (x 8192x8192 B), median of 3"}
+
+
+def bench_fa(steps, warmup, cpu: bool):
+    import torch
+
+    from oracle.torch_ref import attention_ref, seeded_normal
+    from warpir_amd import api, kernels
+
+    bsz, heads, seq, d = 16, 16, 4096, 128
+    q, k, v = (seeded_normal((bsz, heads, seq, d), s).cuda() for s in (0, 1, 2))
+    o = torch.empty_like(q)
+    lse = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
+    h = kernels.handle("mha_d128")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():
+        h(Q=q, K=k, V=v, N=seq, O=o, L=lse)
+
+    ms, wall_ms = _time_launches(launch, steps, warmup, stream)
+    flops = api.attention_flops(bsz, heads, seq, d)
+    tflops = flops / (ms * 1e-3) / 1e12
+    ref_flops = flops + 4.0 * bsz * heads * seq * seq   # the reference's formula adds softmax
+    res = {
+        "value": tflops, "unit": "TFLOP/s", "ms_per_step": ms, "wall_ms_per_step": wall_ms,
+        "tflops_with_softmax_term": ref_flops / (ms * 1e-3) / 1e12,
+        "config": {"workload": "fa_fwd_bf16_B16_H16_S4096_D128_noncausal", "B": bsz, "H": heads, "S": seq,
+                   "D": d, "kernel": "mha_d128", "outputs": "O bf16 + LSE fp32"},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / PEAK_BF16_TFLOPS, "traffic": _traffic_from_profiles("mha_d128")},
+    }
+    if cpu:
+        torch.set_num_threads(os.cpu_count() or 1)
+        qs, ks, vs = (x[0, :2].cpu() for x in (q, k, v))
+        attention_ref(qs[:1], ks[:1], vs[:1])
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            attention_ref(qs, ks, vs)
+            times.append(time.perf_counter() - t0)
+        t = sorted(times)[1]
+        cflops = api.attention_flops(1, 2, seq, d)
+        res["cpu_baseline"] = {"value": cflops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+                               "kind": "port", "os_cpu_count": os.cpu_count(),
+                               "sample": "naive fp32 softmax(q k^T/sqrt(d)) v on 2 of 256 (b,h) heads, "
+                                         "S=4096 D=128, median of 3"}
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["gemm", "fa"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "both workloads shard with no communication (see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from warpir_amd.runtime import device_info
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    info = device_info(0)
+    gemm = fa = None
+    if args.only in (None, "gemm"):
+        print("[bench] gemm 8192^3", file=sys.stderr, flush=True)
+        gemm = bench_gemm(args.steps, args.warmup, not args.no_cpu)
+    if args.only in (None, "fa"):
+        print("[bench] fa-fwd B16 H16 S4096 D128", file=sys.stderr, flush=True)
+        fa = bench_fa(args.steps, args.warmup, not args.no_cpu)
+    head = gemm or fa
+    line = {
+        "metric": METRIC, "value": head["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1), GEMM x0.1)",
+        "config": head["config"], "roofline": head["roofline"],
+    }
+    if "cpu_baseline" in head:
+        line["cpu_baseline"] = head["cpu_baseline"]
+    if gemm is not None and fa is not None:
+        line["fa_fwd"] = fa
+    line["device"] = info
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,128 @@
+"""CDNA4 lowering and the C-ABI boundary (CPU only: no kernel is launched).
+
+Checks the emitted HIP's structure (self-contained, one extern "C"
+kernel named after the IR kernel, globals struct in IR argument order),
+the wait/barrier analysis that replaces the reference's semaphores, the
+kernel-argument layout seen from the host, the error paths, and that
+``libwarpir_rt.so`` loads and exports every entry point that
+``include/warpir_rt.h`` declares.
+"""
+import ctypes
+import os
+import re
+import shutil
+
+import pytest
+
+from warpir_amd import kernels
+from warpir_amd.lowering import CDNA4Lowerer, CDNA4Target, LoweringError
+from warpir_amd.passes.modulo_scheduler import GFX950_COST_MODEL, kernel_pass
+from warpir_amd.runtime import GL, LIB_PATH, kernarg_struct
+from warpir_amd.workloads import build_gemm_kernel, build_mha_forward_kernel
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.mark.parametrize("name", sorted(kernels.VARIANTS))
+def test_every_variant_lowers_to_self_contained_hip(name):
+    k = kernels.kernel(name)
+    src = CDNA4Lowerer().lower(k)
+    assert f'extern "C" __global__' in src and f"\n{k.name}(const {k.name}_globals globals)" in src
+    includes = re.findall(r"#include\s*[<\"]([^>\"]+)", src)
+    assert includes == ["hip/hip_runtime.h"]
+    for banned in ("kittens", "cuda_runtime", "__nv_", "HIP_PLATFORM", "hipify"):
+        assert banned not in src
+
+
+def _waits(src):
+    return [int(x) for x in re.findall(r"wait_vm_barrier<(\d+)>", src)]
+
+
+def test_pipelined_gemm_waits_keep_one_stage_in_flight():
+    src = CDNA4Lowerer().lower(kernels.kernel("gemm_256_k32"))
+    # 256x32 A tile and 32x256 B tile: 16 KiB each = 16 DMA instructions / 4 waves = 4 + 4 per stage
+    assert _waits(src) == [8, 8, 0]
+    assert "wir::barrier()" not in src  # the ring's waits already order every slot reuse
+
+
+def test_ssa_gemm_waits_for_everything_and_guards_reuse():
+    src = CDNA4Lowerer().lower(build_gemm_kernel())
+    assert _waits(src) == [0]
+    body = src[src.index("for (int v_i"):]
+    assert body.index("wir::barrier()") < body.index("Loader")
+
+
+def test_attention_hoists_resident_q_fragments():
+    src = CDNA4Lowerer().lower(kernels.kernel("mha_d128"))
+    loop = src.index("for (int v_i")
+    assert src.index("load_row_frags") < loop
+    assert "mma_ABt_frags" in src and "mma_rAB" in src
+
+
+def test_kernarg_layout_matches_globals_struct():
+    assert ctypes.sizeof(GL) == 48
+    s = kernarg_struct(build_gemm_kernel())
+    assert [f[0] for f in s._fields_] == ["A", "B", "N", "C_global"]
+    assert s.C_global.offset == 104 and ctypes.sizeof(s) == 152
+
+
+def test_lds_budget_is_enforced():
+    k = kernel_pass(build_gemm_kernel(256, 256, 64, 128, 128), cost_model=GFX950_COST_MODEL)
+    with pytest.raises(LoweringError, match="LDS"):
+        CDNA4Lowerer().lower(k)
+
+
+def test_uneven_wave_split_is_rejected():
+    k = build_gemm_kernel(block_m=64, block_n=64, block_k=64, wave_m=16, wave_n=16)
+    with pytest.raises(LoweringError):
+        CDNA4Lowerer().lower(k)
+
+
+def test_mfma_shape_choice():
+    assert "wir::RTile<32, 128, 128>" in CDNA4Lowerer().lower(kernels.kernel("gemm_256_k32"))
+    assert "wir::RTile<16, 16, 64>" in CDNA4Lowerer().lower(build_gemm_kernel())
+    forced = CDNA4Lowerer(CDNA4Target(mfma=16)).lower(kernels.kernel("gemm_256_k32"))
+    assert "wir::RTile<16, 128, 128>" in forced
+
+
+def test_launch_config_from_output_shapes():
+    low = CDNA4Lowerer()
+    k = kernels.kernel("gemm_256_k32")
+    cfg = low.launch_config(k, {"A": (1000, 264), "B": (264, 520), "C_global": (1000, 520)})
+    assert cfg.grid == (3, 4, 1) and cfg.block == (256, 1, 1)
+    m = build_mha_forward_kernel(d=128, block_q=128, block_kv=64, wave_rows=32)
+    cfg = CDNA4Lowerer().launch_config(m, {"O": (2, 3, 512, 128), "L": (2, 3, 512, 1)})
+    assert cfg.grid == (4, 3, 2)
+
+
+def _declared_symbols():
+    with open(os.path.join(ROOT, "include", "warpir_rt.h")) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(wir_\w+)\(", text, re.M)))
+
+
+def test_c_abi_library_exports_every_declared_symbol():
+    if not os.path.exists(LIB_PATH):
+        pytest.skip("libwarpir_rt.so not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(LIB_PATH)
+    syms = _declared_symbols()
+    assert len(syms) == 15
+    for s in syms:
+        assert hasattr(lib, s), s
+    lib.wir_abi_version.restype = ctypes.c_int
+    assert lib.wir_abi_version() == 1
+    lib.wir_error_string.restype = ctypes.c_char_p
+    assert lib.wir_error_string(0)
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
+                    reason="hipcc not available")
+def test_generated_source_compiles_for_gfx950(tmp_path, monkeypatch):
+    import warpir_amd.runtime as rt
+    monkeypatch.setattr(rt, "CACHE_DIR", str(tmp_path))
+    src = CDNA4Lowerer().lower(build_gemm_kernel())
+    path = rt.compile_source(src)
+    with open(path, "rb") as f:
+        assert f.read(24) == b"__CLANG_OFFLOAD_BUNDLE__"
+    usage = rt.resource_usage(src)
+    assert usage.get("scratch", 0) == 0

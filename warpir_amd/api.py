@@ -15,7 +15,7 @@ from typing import Optional, Tuple
 
 from warpir_amd import kernels
 
-GEMM_VARIANT = "gemm_256_k32"
+GEMM_VARIANT = "gemm_256_k64"
 
 
 def gemm(a, b, out=None, variant: str = GEMM_VARIANT):

@@ -88,22 +88,30 @@ __device__ __forceinline__ int ccol(int i, int lh) {
 
 // ---------------------------------------------------------------------------
 // LDS tiles.  ROWS x COLS bf16, row-major, in 16-byte chunks (CPR per row)
-// with an XOR swizzle of the chunk index chosen by how the tile is read:
-//   ROWREAD -- ds_read_b128 of one row per lane (8 consecutive rows per
-//              phase): chunk ^ f(row) spreads 8 rows over 8 bank groups;
-//   TRREAD  -- ds_read_b64_tr_b16 (4 rows x 32 bytes per 16-lane group):
-//              chunk ^ 2*(row%4) spreads the 4 rows over 4 bank ranges.
+// with an XOR swizzle of the chunk index chosen by how the tile is read.
+// gfx950's LDS serves 256 bytes per cycle (64 banks of 4 bytes), so a
+// ds_read_b128 is processed 16 lanes at a time and a ds_read_b64 32 lanes
+// at a time (measured with SQ_LDS_BANK_CONFLICT: swizzles built for 128-byte
+// banks showed 2-way conflicts).  The swizzles are
+// conflict-free for the MFMA operand patterns under both a 256-byte and a
+// 128-byte bank space:
+//   ROWREAD -- ds_read_b128 of one row per lane, 16 consecutive rows per
+//              phase: the 16 rows land in 16 distinct 16-byte bank slots;
+//   TRREAD  -- ds_read_b64_tr_b16, per 32 lanes 4 rows x 64 bytes: the 4
+//              rows' 64-byte runs land in 4 disjoint bank ranges.
 enum Role { ROWREAD = 0, TRREAD = 1 };
 
 template <int CPR, int ROLE>
 __device__ __forceinline__ int swz(int row) {
   if (ROLE == ROWREAD) {
-    if (CPR >= 8) return row & 7;
-    if (CPR == 4) return (row >> 1) & 3;
+    if (CPR >= 16) return row & 15;
+    if (CPR == 8) return (row & 7) ^ ((row >> 3) & 1);
+    if (CPR == 4) return ((row >> 1) ^ (row >> 2)) & 3;
     if (CPR == 2) return (row >> 2) & 1;
     return 0;
   } else {
-    if (CPR >= 8) return (row & 3) << 1;
+    if (CPR >= 16) return ((row & 3) << 2) | (row & 2);
+    if (CPR == 8) return (row & 3) << 1;
     if (CPR == 4) return ((row >> 1) & 1) << 1;
     return 0;
   }
@@ -127,11 +135,36 @@ struct STile {
 
 // ---------------------------------------------------------------------------
 // Asynchronous global -> LDS tile load (the IR's tma_load / tma_load_buf).
+//
+// The DMA instruction is issued from inline assembly on purpose: when LLVM
+// sees global_load_lds it must assume the LDS write may alias any later
+// ds_read and inserts s_waitcnt vmcnt(0) in front of it, which would
+// serialise every ring stage.  Completion is instead tracked by the
+// lowering itself (wait_vm_barrier<N> with N from its schedule analysis).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// Uniform 64-bit base + per-lane 32-bit byte offset (the saddr form).
+__device__ __forceinline__ void dma16_s(const void* gbase, unsigned voff, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(gbase), "s"(lds_addr) : "memory", "m0");
+}
+// Per-lane 64-bit address.
+__device__ __forceinline__ void dma16_v(const void* gaddr, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(gaddr), "s"(lds_addr) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ unsigned lds_addr(char* p) {
+  return (unsigned)(size_t)(lds_char*)p;
+}
+
 // The tile's rows start at global row `row0`, its columns at `col0`
 // (elements).  Chunks outside [0, r) x [0, c) or an out-of-range (b, d)
-// read the zero page.  Every wave issues exactly INSTR_PER_WAVE
-// global_load_lds_dwordx4 instructions, the count the lowering uses for
-// its vmcnt waits.
+// read the zero page.  Every wave issues exactly INSTR_PER_WAVE DMA
+// instructions, the count the lowering uses for its vmcnt waits.  Tiles
+// that lie wholly inside the tensor take the fast path: one uniform base
+// address plus loop-invariant per-lane offsets.
 template <class Tile, int NW>
 struct Loader {
   static constexpr int CHUNKS = Tile::ROWS * Tile::CPR;
@@ -140,40 +173,84 @@ struct Loader {
   static_assert(INSTR % NW == 0, "tile chunks must split evenly over the wavefronts");
   static constexpr int INSTR_PER_WAVE = INSTR / NW;
 
-  static __device__ __forceinline__ void load(char* tile_base, const gl<bf16>& g, int b, int d,
-                                              int row0, int col0) {
-    const int lane = lane_id();
-    const int wave = wave_id();
+  // Row and logical chunk of the 16-byte chunk this lane moves in
+  // instruction j of wave `wave`.
+  static __device__ __forceinline__ void place(int wave, int j, int& row, int& c) {
+    const int p = (wave + j * NW) * 64 + lane_id();
+    row = p / Tile::CPR;
+    c = (p % Tile::CPR) ^ swz<Tile::CPR, Tile::ROLE>(row);
+  }
+
+  // Issue this wave's j-th DMA instruction of the tile.  ALIGNED (the
+  // tensor's extents are multiples of the tile and its row pitch fits the
+  // 32-bit offset form): a tile is either wholly inside or wholly outside
+  // the tensor, so the code is branch-free -- outside tiles read the zero
+  // page at offset 0.  Otherwise tiles straddling an edge are loaded lane
+  // by lane with bounds checks.
+  template <bool ALIGNED>
+  static __device__ __forceinline__ void load_one(int j, char* tile_base, const gl<bf16>& g, int b, int d,
+                                                  int row0, int col0, int wave) {
+    int row, c;
+    place(wave, j, row, c);
+    const unsigned dst = lds_addr(tile_base + (wave + j * NW) * 1024);
     const bool bd_ok = (unsigned)b < (unsigned)g.b && (unsigned)d < (unsigned)g.d;
+    if (ALIGNED) {
+      const bool inb = bd_ok && (unsigned)row0 < (unsigned)g.r && (unsigned)col0 < (unsigned)g.c;
+      const bf16* tbase = g.data + (long long)b * g.sb + (long long)d * g.sd + (long long)row0 * g.sr + col0;
+      const void* base = inb ? (const void*)tbase : (const void*)zero_page;
+      const unsigned voff = inb ? (unsigned)(row * (int)g.sr + c * 8) * 2u : 0u;
+      dma16_s(base, voff, dst);
+      return;
+    }
     const bf16* base = g.data + (long long)b * g.sb + (long long)d * g.sd;
-#pragma unroll
-    for (int j = 0; j < INSTR_PER_WAVE; ++j) {
-      const int ins = wave + j * NW;
-      const int p = ins * 64 + lane;  // physical chunk
-      const int row = p / Tile::CPR;
-      const int c = (p % Tile::CPR) ^ swz<Tile::CPR, Tile::ROLE>(row);
+    const bool fast = bd_ok && row0 >= 0 && col0 >= 0 && row0 + Tile::ROWS <= g.r && col0 + Tile::COLS <= g.c &&
+                      (long long)Tile::ROWS * g.sr < (1ll << 30);
+    if (fast) {
+      const bf16* tbase = base + (long long)row0 * g.sr + col0;
+      dma16_s(tbase, (unsigned)(row * (int)g.sr + c * 8) * 2u, dst);
+    } else {
       const int gr = row0 + row, gc = col0 + c * 8;
       const bool ok = bd_ok && (unsigned)gr < (unsigned)g.r && (unsigned)gc < (unsigned)g.c;
       const void* src = ok ? (const void*)(base + (long long)gr * g.sr + gc) : (const void*)zero_page;
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(tile_base + ins * 1024),
-                                       16, 0, 0);
+      dma16_v(src, dst);
     }
+  }
+
+  template <bool ALIGNED>
+  static __device__ __forceinline__ void load(char* tile_base, const gl<bf16>& g, int b, int d, int row0,
+                                              int col0, int wave) {
+#pragma unroll
+    for (int j = 0; j < INSTR_PER_WAVE; ++j) load_one<ALIGNED>(j, tile_base, g, b, d, row0, col0, wave);
+  }
+
+  // Host-independent check used for the kernel's ALIGNED specialisation.
+  static __device__ __forceinline__ bool aligned(const gl<bf16>& g) {
+    return g.r % Tile::ROWS == 0 && g.c % Tile::COLS == 0 && (long long)Tile::ROWS * g.sr < (1ll << 30);
   }
 };
 
+template <bool B>
+struct bool_tag {
+  static constexpr bool value = B;
+};
+
 // Wait until at most N of this wave's vector-memory instructions are
-// outstanding (s_waitcnt vmcnt(N)), then synchronise the workgroup so every
-// wave's LDS-DMA writes are visible.
+// outstanding and its LDS reads have returned, then synchronise the
+// workgroup: every wave's LDS-DMA writes up to that point are visible and
+// no wave still reads a slot that the next loads overwrite.  The empty asm
+// statements keep the compiler from moving memory accesses across.
 template <int N>
 __device__ __forceinline__ void wait_vm_barrier() {
   static_assert(N >= 0 && N < 64, "vmcnt out of range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" :: "n"(N) : "memory");
   __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 __device__ __forceinline__ void barrier() {
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS reads of this wave are done
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // ---------------------------------------------------------------------------
@@ -278,31 +355,176 @@ __device__ __forceinline__ void load_row_frags(RowFrags<MS, RB, KS>& fr, char* t
 // b^T a^T: its A operand comes from `b`, its B operand from `a`.
 
 // acc += a @ b; a: ROWREAD LDS [.][K]; b: TRREAD LDS [K][.].
+//
+// Software-pipelined over the K/KSTEP MFMA k-steps: the fragments of step
+// ks+1 are read from LDS while the RB*CB MFMAs of step ks run, and a
+// scheduling-group pattern interleaves one LDS read after each MFMA so the
+// reads' latency hides under the matrix core.
 template <int MS, int R, int C, class TA, class TB>
 __device__ __forceinline__ void mma_AB(RTile<MS, R, C>& acc, char* a_base, int a_row0, char* b_base,
                                        int b_col0) {
   static_assert(TA::COLS == TB::ROWS, "inner dimensions differ");
   constexpr int K = TA::COLS;
   constexpr int KS = K / MF<MS>::KSTEP;
+  constexpr int RB = RTile<MS, R, C>::RB, CB = RTile<MS, R, C>::CB;
   static_assert(K % MF<MS>::KSTEP == 0, "k tile must be a multiple of the MFMA k");
   const int lane = lane_id();
   const int lh = lane / MS;
   const int ngrp = (lane % MS) & ~15;
+  bf16x8 bop[2][RB];
+  bf16x8 aop[2][CB];
+  auto read = [&](int ks, int buf) {
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    bf16x8 bop[RTile<MS, R, C>::RB];
+    for (int rb = 0; rb < RB; ++rb) bop[buf][rb] = row_operand<TA, MS>(a_base, a_row0 + rb * MS, ks);
 #pragma unroll
-    for (int rb = 0; rb < acc.RB; ++rb) bop[rb] = row_operand<TA, MS>(a_base, a_row0 + rb * MS, ks);
-#pragma unroll
-    for (int cb = 0; cb < acc.CB; ++cb) {
+    for (int cb = 0; cb < CB; ++cb) {
       const int k0 = ks * MF<MS>::KSTEP + 8 * lh;
       const int n0 = b_col0 + cb * MS + ngrp;
-      const bf16x8 aop = cat(tr_operand4<TB>(b_base, k0, n0), tr_operand4<TB>(b_base, k0 + 4, n0));
+      aop[buf][cb] = cat(tr_operand4<TB>(b_base, k0, n0), tr_operand4<TB>(b_base, k0 + 4, n0));
+    }
+  };
+  read(0, 0);
 #pragma unroll
-      for (int rb = 0; rb < acc.RB; ++rb) acc.f[cb][rb] = MF<MS>::mma(aop, bop[rb], acc.f[cb][rb]);
+  for (int ks = 0; ks < KS; ++ks) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (ks + 1 < KS) read(ks + 1, (ks + 1) & 1);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        acc.f[cb][rb] = MF<MS>::mma(aop[ks & 1][cb], bop[ks & 1][rb], acc.f[cb][rb]);
+    if (ks + 1 < KS) {
+      constexpr int NREAD = RB + 2 * CB;
+      constexpr int NMMA = RB * CB;
+      constexpr int PAIRS = NREAD < NMMA ? NREAD : NMMA;
+#pragma unroll
+      for (int q = 0; q < PAIRS; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      }
+      if (NMMA > PAIRS) __builtin_amdgcn_sched_group_barrier(0x008, NMMA - PAIRS, 0);
+      if (NREAD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NREAD - PAIRS, 0);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
 }
+
+// Rotated form of mma_AB for the steady state of a pipelined ring loop
+// (wait on slot -> loads -> MMA on that slot).  run() first issues the
+// MFMAs of the previous call's last k-step from registers -- so the matrix
+// core has work right after the wait's barrier -- interleaved with the LDS
+// reads of this tile's first k-step, then k-steps 0..KS-2, and leaves the
+// last k-step's fragments pending.  finish() issues the pending MFMAs.
+// The order of MFMAs into every accumulator is exactly mma_AB's.  The
+// pending fragments start as zeros, whose MFMAs add nothing.
+template <int MS, int R, int C, class TA, class TB>
+struct MMAPipeAB {
+  static constexpr int K = TA::COLS;
+  static constexpr int KS = K / MF<MS>::KSTEP;
+  static constexpr int RB = RTile<MS, R, C>::RB, CB = RTile<MS, R, C>::CB;
+  static constexpr int NREAD = RB + 2 * CB;
+  static constexpr int NMMA = RB * CB;
+  static_assert(TA::COLS == TB::ROWS, "inner dimensions differ");
+  static_assert(K % MF<MS>::KSTEP == 0, "k tile must be a multiple of the MFMA k");
+  static_assert(KS % 2 == 0, "the rotated pipeline alternates two fragment buffers");
+  bf16x8 bop[2][RB];
+  bf16x4 aop[2][CB][2];
+
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) bop[(KS - 1) & 1][rb] = bf16x8{};
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) aop[(KS - 1) & 1][cb][0] = aop[(KS - 1) & 1][cb][1] = bf16x4{};
+  }
+
+  __device__ __forceinline__ void read(char* a_base, int a_row0, char* b_base, int b_col0, int ks, int buf) {
+    const int lane = lane_id();
+    const int lh = lane / MS;
+    const int ngrp = (lane % MS) & ~15;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) bop[buf][rb] = row_operand<TA, MS>(a_base, a_row0 + rb * MS, ks);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int k0 = ks * MF<MS>::KSTEP + 8 * lh;
+      const int n0 = b_col0 + cb * MS + ngrp;
+      aop[buf][cb][0] = tr_operand4<TB>(b_base, k0, n0);
+      aop[buf][cb][1] = tr_operand4<TB>(b_base, k0 + 4, n0);
+    }
+  }
+
+  __device__ __forceinline__ void mfmas(RTile<MS, R, C>& acc, int buf) {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        acc.f[cb][rb] = MF<MS>::mma(cat(aop[buf][cb][0], aop[buf][cb][1]), bop[buf][rb], acc.f[cb][rb]);
+  }
+
+  static __device__ __forceinline__ void interleave() {
+    constexpr int PAIRS = NREAD < NMMA ? NREAD : NMMA;
+#pragma unroll
+    for (int q = 0; q < PAIRS; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if (NMMA > PAIRS) __builtin_amdgcn_sched_group_barrier(0x008, NMMA - PAIRS, 0);
+    if (NREAD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NREAD - PAIRS, 0);
+  }
+
+  // Read item q (0 <= q < NREAD) of k-step ks into buffer buf: the RB row
+  // operands first, then the 2*CB transposed half-operands.
+  __device__ __forceinline__ void read_item(char* a_base, int a_row0, char* b_base, int b_col0, int ks, int buf,
+                                            int q) {
+    const int lane = lane_id();
+    const int lh = lane / MS;
+    if (q < RB) {
+      bop[buf][q] = row_operand<TA, MS>(a_base, a_row0 + q * MS, ks);
+      return;
+    }
+    const int cb = (q - RB) / 2, half = (q - RB) % 2;
+    const int k0 = ks * MF<MS>::KSTEP + 8 * lh + 4 * half;
+    const int n0 = b_col0 + cb * MS + ((lane % MS) & ~15);
+    aop[buf][cb][half] = tr_operand4<TB>(b_base, k0, n0);
+  }
+
+  // One steady-state step.  The previous tile's pending k-step MFMAs are
+  // issued first, one per slot, each followed by one of this iteration's
+  // NLOAD DMA instructions (`loads(q)`) and one LDS read of this tile's
+  // first k-step; then k-steps 0..KS-2 with the next k-step's reads
+  // interleaved.  sched_barrier fences pin the order.
+  template <int NLOAD, class LoadFn>
+  __device__ __forceinline__ void run(RTile<MS, R, C>& acc, char* a_base, int a_row0, char* b_base, int b_col0,
+                                      LoadFn loads) {
+    constexpr int PEND = (KS - 1) & 1;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < NMMA; ++q) {
+      const int cb = q / RB, rb = q % RB;
+      acc.f[cb][rb] = MF<MS>::mma(cat(aop[PEND][cb][0], aop[PEND][cb][1]), bop[PEND][rb], acc.f[cb][rb]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (q < NLOAD) loads(q);
+      if (q < NREAD) read_item(a_base, a_row0, b_base, b_col0, 0, 0, q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q = NMMA; q < NLOAD; ++q) loads(q);
+#pragma unroll
+    for (int q = NMMA; q < NREAD; ++q) read_item(a_base, a_row0, b_base, b_col0, 0, 0, q);
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      __builtin_amdgcn_sched_barrier(0);
+      read(a_base, a_row0, b_base, b_col0, ks + 1, (ks + 1) & 1);
+      mfmas(acc, ks & 1);
+      interleave();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  __device__ __forceinline__ void finish(RTile<MS, R, C>& acc) {
+    mfmas(acc, (KS - 1) & 1);
+    init();
+  }
+};
 
 // acc = a @ b^T with `a` from hoisted register fragments or LDS; b: ROWREAD LDS [.][K].
 template <int MS, int R, int C, class TB, int KS>

@@ -10,13 +10,15 @@ from __future__ import annotations
 from typing import Callable, Dict
 
 from warpir_amd.ir import Kernel
-from warpir_amd.passes.modulo_scheduler import GFX950_COST_MODEL, kernel_pass
+from warpir_amd.passes.modulo_scheduler import gfx950_cost_model, kernel_pass
 from warpir_amd.workloads import build_attention_kernel, build_gemm_kernel, build_mha_forward_kernel
 
 
-def _gemm_mi355x(block_k: int = 32, cost=GFX950_COST_MODEL) -> Kernel:
-    return kernel_pass(build_gemm_kernel(block_m=256, block_n=256, block_k=block_k, wave_m=128, wave_n=128,
-                                         name="gemm"), cost_model=cost)
+def _gemm_mi355x(block_k: int = 32, block_m: int = 256, block_n: int = 256, wave_m: int = 128,
+                 wave_n: int = 128) -> Kernel:
+    return kernel_pass(build_gemm_kernel(block_m=block_m, block_n=block_n, block_k=block_k, wave_m=wave_m,
+                                         wave_n=wave_n, name="gemm"),
+                       cost_model=gfx950_cost_model(block_m, block_n, block_k))
 
 
 VARIANTS: Dict[str, Callable[[], Kernel]] = {
@@ -25,6 +27,8 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "gemm_ref_piped": lambda: kernel_pass(build_gemm_kernel()),
     # MI355X GEMM: 256x256 block tile, 4 wavefronts of 128x128, 3-stage LDS ring.
     "gemm_256_k32": lambda: _gemm_mi355x(32),
+    # Same tile with a 64-deep K step: MMA twice as long per stage, 2-slot ring.
+    "gemm_256_k64": lambda: _gemm_mi355x(64),
     # The reference's single-head attention IR (tests/attention_baseline.py:46-186).
     "attn_ref_ssa": lambda: build_attention_kernel(),
     # Multi-head FlashAttention forward, [B, H, S, D] with LSE.

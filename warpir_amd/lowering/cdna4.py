@@ -83,6 +83,7 @@ class CDNA4Target:
     mfma: Optional[int] = None
     xcd_remap: bool = True
     group_m: int = 8
+    rotate_mma: bool = True
 
 
 @dataclass
@@ -174,6 +175,10 @@ class CDNA4Lowerer:
         self._pending_hoist: Dict[str, tuple] = {}
         self._view_cache: Dict[str, SlotViewOp] = {}
         self._view_kernel = None
+        self._rotated: Dict[int, str] = {}
+        self._aligned_checks: set = set()
+        self._fused_loads: Dict[int, List[Op]] = {}
+        self._fused_ids: set = set()
 
     def _build_aliases(self, ops) -> None:
         """iter_arg init / loop results / yielded values -> block arg (``lowering.py:87-100``)."""
@@ -413,6 +418,8 @@ class CDNA4Lowerer:
                 return
             raise LoweringError(f"{type(op).__name__} on {op.result.type}")
         if isinstance(op, (TMALoadOp, TMALoadBufOp)):
+            if id(op) in self._fused_ids:
+                return
             if id(op) in self.war_barrier:
                 w(f"{pad}wir::barrier();")
             if isinstance(op, TMALoadOp):
@@ -422,8 +429,7 @@ class CDNA4Lowerer:
             src = op.source
             sub = src.type.sub_tile_type
             b, d, rt, ct = (self._int(c) for c in op.coords)
-            w(f"{pad}wir::Loader<{self.stile(key)}, {self.geo.nw}>::load({ptr}, globals.{_cname(src.name)[2:]}, "
-              f"{b}, {d}, ({rt}) * {sub.rows}, ({ct}) * {sub.cols});")
+            w(f"{pad}{self._load_call(op, 'load<WIR_AL>(', ptr, key)});")
             return
         if isinstance(op, (WaitOp, WaitBufOp)):
             n = self.wait_n.get(id(op), 0)
@@ -439,8 +445,23 @@ class CDNA4Lowerer:
             b_ptr, b_key = self._buf_ptr(op.b_buf, op.b_slot)
             t = self._rtype(op.accum)
             acc = self._var(op.accum)
-            w(f"{pad}wir::mma_AB<{ms}, {t.rows}, {t.cols}, {self.stile(a_key)}, {self.stile(b_key)}>"
-              f"({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0);")
+            pipe = self._rotated.get(id(op))
+            if pipe is not None:
+                loads = self._fused_loads.get(id(op), [])
+                calls, total = [], 0
+                for ld in loads:
+                    lptr, lkey = self._buf_ptr(ld.buf, ld.slot)
+                    n = self.loads_per_wave(ld.buf.type.tile_type)
+                    calls.append(f"if (q >= {total} && q < {total + n}) "
+                                 + self._load_call(ld, f"load_one<WIR_AL>(q - {total}, ", lptr, lkey) + ");")
+                    total += n
+                w(f"{pad}{pipe}.run<{total}>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int q) {{")
+                for c in calls:
+                    w(f"{pad}  {c}")
+                w(f"{pad}}});")
+            else:
+                w(f"{pad}wir::mma_AB<{ms}, {t.rows}, {t.cols}, {self.stile(a_key)}, {self.stile(b_key)}>"
+                  f"({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0);")
             if self._var(op.result) != acc:
                 w(f"{pad}{self._var(op.result)} = {acc};")
             if isinstance(op.a_slot, BufSlotExpr):
@@ -502,6 +523,14 @@ class CDNA4Lowerer:
             self._emit_for(op, out, depth)
             return
         raise LoweringError(f"no CDNA4 lowering for {type(op).__name__}")
+
+    def _load_call(self, op, fn: str, ptr: str, key: str) -> str:
+        src = op.source
+        sub = src.type.sub_tile_type
+        b, d, rt, ct = (self._int(c) for c in op.coords)
+        self._aligned_checks.add((self.stile(key), _cname(src.name)[2:]))
+        return (f"wir::Loader<{self.stile(key)}, {self.geo.nw}>::{fn}{ptr}, globals.{_cname(src.name)[2:]}, "
+                f"{b}, {d}, ({rt}) * {sub.rows}, ({ct}) * {sub.cols}, wir_wave")
 
     def _emit_yield(self, op: YieldOp, out: List[str], depth: int) -> None:
         pad = "  " * depth
@@ -574,9 +603,47 @@ class CDNA4Lowerer:
         if op.tile_size:
             stop = f"(({stop}) + {op.tile_size - 1}) / {op.tile_size}"
         iv = self._var(op.induction_var)
+        rotated = self._rotatable(op)
+        if rotated is not None:
+            mma, pipe_t = rotated
+            name = f"pipe{len(self._rotated)}"
+            self._rotated[id(mma)] = name
+            loads = [o for o in op.body if isinstance(o, TMALoadBufOp)]
+            if not any(id(o) in self.war_barrier for o in loads):
+                self._fused_loads[id(mma)] = loads
+                self._fused_ids |= {id(o) for o in loads}
+            out.append(f"{pad}{pipe_t} {name};")
+            out.append(f"{pad}{name}.init();")
         out.append(f"{pad}for (int {iv} = {self._int(op.start)}; {iv} < {stop}; {iv} += {self._int(op.step)}) {{")
         self._emit_ops(op.body, out, depth + 1)
         out.append(f"{pad}}}")
+        if rotated is not None:
+            out.append(f"{pad}{self._rotated[id(rotated[0])]}.finish({self._var(rotated[0].accum)});")
+
+    def _rotatable(self, loop: ForOp):
+        """The steady state of a ring pipeline -- ``wait_buf(slot s)``, loads,
+        one ``mma_buf`` on slot ``s`` -- is emitted in rotated form
+        (``wir::MMAPipeAB``): the MMA's last k-step is issued after the next
+        iteration's wait, so the matrix core is busy across the barrier."""
+        if not self.target.rotate_mma:
+            return None
+        body = [o for o in loop.body if not isinstance(o, YieldOp)]
+        if not body or not isinstance(body[0], WaitBufOp):
+            return None
+        mmas = [o for o in body if isinstance(o, MMABufOp)]
+        rest = [o for o in body[1:] if not isinstance(o, (TMALoadBufOp, MMABufOp))]
+        if len(mmas) != 1 or rest or body[-1] is not mmas[0]:
+            return None
+        mma, wait = mmas[0], body[0]
+        if mma.a_slot != wait.slot or mma.b_slot != wait.slot:
+            return None
+        t = self._rtype(mma.accum)
+        k = mma.a_buf.type.tile_type.cols
+        if (k // (16 if self.geo.ms == 32 else 32)) % 2:
+            return None
+        a_key, b_key = self.resolve(mma.a_buf.name), self.resolve(mma.b_buf.name)
+        return mma, (f"wir::MMAPipeAB<{self.geo.ms}, {t.rows}, {t.cols}, {self.stile(a_key)}, "
+                     f"{self.stile(b_key)}>")
 
     # ------------------------------------------------------------------
     # assembly
@@ -653,11 +720,22 @@ class CDNA4Lowerer:
             f"  const int wir_wave = wir::wave_id();",
             f"  const int wave_row0 = (wir_wave / {self.geo.nw_c}) * {self._wave_rows()};",
             f"  const int wave_col0 = (wir_wave % {self.geo.nw_c}) * {self._wave_cols()};",
+        ]
+        checks = " && ".join(f"wir::Loader<{t}, {self.geo.nw}>::aligned(globals.{g})"
+                             for t, g in sorted(self._aligned_checks)) or "true"
+        src += [
+            f"  const bool wir_aligned = {checks};",
+            "  auto wir_body = [&](auto wir_tag) {",
+            "  constexpr bool WIR_AL = decltype(wir_tag)::value;",
             "  int wir_drain = 0;",
             "  (void)wave_row0; (void)wave_col0; (void)wir_drain;",
             *decls,
         ]
-        return "\n".join(src + body + ["}", ""])
+        tail = ["  };",
+                "  if (wir_aligned) wir_body(wir::bool_tag<true>{});",
+                "  else wir_body(wir::bool_tag<false>{});",
+                "}", ""]
+        return "\n".join(src + body + tail)
 
     def _wave_rows(self) -> int:
         for op in _walk(self.kernel.body):

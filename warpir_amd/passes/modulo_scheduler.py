@@ -60,12 +60,24 @@ class CostModel:
 
 REFERENCE_COST_MODEL = CostModel(latency=dict(LATENCY), resources=dict(RESOURCE_COUNTS))
 
-# gfx950, in units of 256 cycles for a 256x256x32 block step: one K-step of
-# MFMAs on a SIMD is 4 units (32 v_mfma_f32_32x32x16_bf16 of 32 cycles),
-# an LDS-DMA tile load under load is ~8 units from issue to landing.  The
-# optimum is ii=4 with the MMA two stages behind its loads: a 3-slot ring.
-GFX950_COST_MODEL = CostModel(latency={TMALoadOp: ("tma", 8), MMAOp: ("tc", 4), TMAStoreOp: ("tma", 8)},
-                              resources={"tma": 4, "tc": 1})
+
+
+def gfx950_cost_model(block_m: int, block_n: int, block_k: int) -> CostModel:
+    """Cost model of one K-step on an MI355X CU, in units of 256 cycles.
+
+    The MMA's latency is the block tile's MFMA time spread over the CU's 4
+    SIMDs at 1024 bf16 flop/clk each; an LDS-DMA tile load takes ~2048
+    cycles from issue to landing under load (8 units).  For 256x256x32 the
+    MMA is 4 units and the optimum is ii=4 with the MMA two stages behind
+    its loads (a 3-slot ring); for 256x256x64 it is 8 units, ii=8 and a
+    2-slot ring.
+    """
+    mma_units = max(1, round(2 * block_m * block_n * block_k / (4 * 1024) / 256))
+    return CostModel(latency={TMALoadOp: ("tma", 8), MMAOp: ("tc", mma_units), TMAStoreOp: ("tma", 8)},
+                     resources={"tma": 4, "tc": 1})
+
+
+GFX950_COST_MODEL = gfx950_cost_model(256, 256, 32)
 
 
 @dataclass
@@ -280,4 +292,4 @@ def kernel_pass(kernel: Kernel, cost_model: Optional[CostModel] = None) -> Kerne
 
 
 __all__ = ["MSInstructionEdge", "MSInstruction", "MSInstructionManager", "PipelineError",
-           "CostModel", "REFERENCE_COST_MODEL", "GFX950_COST_MODEL", "kernel_pass"]
+           "CostModel", "REFERENCE_COST_MODEL", "GFX950_COST_MODEL", "gfx950_cost_model", "kernel_pass"]
