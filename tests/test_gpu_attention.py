@@ -30,22 +30,24 @@ def test_reference_attention_ir(gpu, n):
     assert rel_err(o.cpu(), ref) <= TOL
 
 
-@pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024)])
-def test_mha_d128(gpu, b, h, s):
-    announce(f"mha_d128 B={b} H={h} S={s}")
+@pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_ssa"])
+@pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 1, 64)])
+def test_mha_d128(gpu, variant, b, h, s):
+    announce(f"{variant} B={b} H={h} S={s}")
     q, k, v = (seeded_normal((b, h, s, 128), sd) for sd in (0, 1, 2))
-    o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda())
+    o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda(), variant=variant)
     torch.cuda.synchronize()
     ref, ref_lse = attention_ref(q, k, v)
     assert rel_err(o.cpu(), ref) <= TOL
     assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-3 * ref_lse.abs().max().item() + 1e-3
 
 
-@pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 2, 512), (1, 2, 1024)])
-def test_mha_d64_causal(gpu, b, h, s):
-    announce(f"mha_d64_causal B={b} H={h} S={s}")
+@pytest.mark.parametrize("variant", ["mha_d64_causal", "mha_d64_causal_ssa"])
+@pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 2, 512), (1, 2, 1024), (1, 1, 192)])
+def test_mha_d64_causal(gpu, variant, b, h, s):
+    announce(f"{variant} B={b} H={h} S={s}")
     q, k, v = (seeded_normal((b, h, s, 64), sd) for sd in (3, 4, 5))
-    o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda(), causal=True)
+    o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda(), causal=True, variant=variant)
     torch.cuda.synchronize()
     ref, ref_lse = attention_ref(q, k, v, causal=True)
     assert rel_err(o.cpu(), ref) <= TOL

@@ -34,19 +34,24 @@ def test_reference_ir_square(gpu, variant, n):
     assert err <= TOL, err
 
 
+MI355X_VARIANTS = sorted(v for v in kernels.VARIANTS if v.startswith("gemm_256"))
+
+
+@pytest.mark.parametrize("variant", MI355X_VARIANTS)
 @pytest.mark.parametrize("m,n,k", [(256, 256, 32), (256, 256, 64), (512, 512, 512), (1024, 1024, 1024),
                                    (300, 520, 264), (1000, 776, 1032), (128, 8192, 512)])
-def test_mi355x_gemm(gpu, m, n, k):
-    a, b, c = _run("gemm_256_k32", m, n, k)
+def test_mi355x_gemm(gpu, variant, m, n, k):
+    a, b, c = _run(variant, m, n, k)
     err = rel_err(c, gemm_ref(a, b))
     assert err <= TOL, err
     assert not torch.isnan(c.float()).any()
 
 
+@pytest.mark.parametrize("variant", MI355X_VARIANTS)
 @pytest.mark.parametrize("size", [4096, 8192])
-def test_mi355x_gemm_large_sampled(gpu, size):
+def test_mi355x_gemm_large_sampled(gpu, variant, size):
     """Full-size run; the oracle is evaluated on 256 sampled rows."""
-    a, b, c = _run("gemm_256_k32", size, size, size, seed=3)
+    a, b, c = _run(variant, size, size, size, seed=3)
     rows = torch.randperm(size, generator=torch.Generator().manual_seed(7))[:256]
     ref = gemm_ref(a[rows], b)
     err = rel_err(c[rows], ref)
@@ -61,6 +66,6 @@ def test_identity_returns_a(gpu):
     eye = torch.eye(n, dtype=torch.bfloat16)
     c = torch.empty(n, n, dtype=torch.bfloat16, device="cuda")
     announce("gemm identity 512")
-    kernels.handle("gemm_256_k32")(A=a.cuda(), B=eye.cuda(), N=n, C_global=c)
+    kernels.handle("gemm_256_k64")(A=a.cuda(), B=eye.cuda(), N=n, C_global=c)
     torch.cuda.synchronize()
     assert torch.equal(c.cpu(), a)

@@ -181,37 +181,49 @@ struct Loader {
     c = (p % Tile::CPR) ^ swz<Tile::CPR, Tile::ROLE>(row);
   }
 
-  // Issue this wave's j-th DMA instruction of the tile.  ALIGNED (the
-  // tensor's extents are multiples of the tile and its row pitch fits the
-  // 32-bit offset form): a tile is either wholly inside or wholly outside
-  // the tensor, so the code is branch-free -- outside tiles read the zero
-  // page at offset 0.  Otherwise tiles straddling an edge are loaded lane
-  // by lane with bounds checks.
+  // Source of one tile load, resolved once per tile.
+  struct Src {
+    const bf16* base;  // tile origin (ALIGNED, in bounds) or tensor origin
+    bool inb;          // ALIGNED: tile inside the tensor; else: tile wholly inside (fast path)
+    int row0, col0;
+  };
+
+  // ALIGNED (the tensor's extents are multiples of the tile and its row
+  // pitch fits the 32-bit offset form): a tile is either wholly inside or
+  // wholly outside the tensor, so issue() is branch-free -- outside tiles
+  // read the zero page at offset 0.  Otherwise tiles straddling an edge are
+  // loaded lane by lane with bounds checks.
   template <bool ALIGNED>
-  static __device__ __forceinline__ void load_one(int j, char* tile_base, const gl<bf16>& g, int b, int d,
-                                                  int row0, int col0, int wave) {
+  static __device__ __forceinline__ Src prep(const gl<bf16>& g, int b, int d, int row0, int col0) {
+    const bool bd_ok = (unsigned)b < (unsigned)g.b && (unsigned)d < (unsigned)g.d;
+    const bf16* bd = g.data + (long long)b * g.sb + (long long)d * g.sd;
+    if (ALIGNED) {
+      const bool inb = bd_ok && (unsigned)row0 < (unsigned)g.r && (unsigned)col0 < (unsigned)g.c;
+      const bf16* t = inb ? bd + (long long)row0 * g.sr + col0 : (const bf16*)zero_page;
+      return Src{t, inb, row0, col0};
+    }
+    const bool fast = bd_ok && row0 >= 0 && col0 >= 0 && row0 + Tile::ROWS <= g.r && col0 + Tile::COLS <= g.c &&
+                      (long long)Tile::ROWS * g.sr < (1ll << 30);
+    return Src{bd_ok ? bd : (const bf16*)zero_page, fast, bd_ok ? row0 : -(1 << 30), col0};
+  }
+
+  // Issue this wave's j-th DMA instruction of the tile.
+  template <bool ALIGNED>
+  static __device__ __forceinline__ void issue(int j, char* tile_base, const gl<bf16>& g, const Src& s, int wave) {
     int row, c;
     place(wave, j, row, c);
     const unsigned dst = lds_addr(tile_base + (wave + j * NW) * 1024);
-    const bool bd_ok = (unsigned)b < (unsigned)g.b && (unsigned)d < (unsigned)g.d;
     if (ALIGNED) {
-      const bool inb = bd_ok && (unsigned)row0 < (unsigned)g.r && (unsigned)col0 < (unsigned)g.c;
-      const bf16* tbase = g.data + (long long)b * g.sb + (long long)d * g.sd + (long long)row0 * g.sr + col0;
-      const void* base = inb ? (const void*)tbase : (const void*)zero_page;
-      const unsigned voff = inb ? (unsigned)(row * (int)g.sr + c * 8) * 2u : 0u;
-      dma16_s(base, voff, dst);
+      const unsigned voff = s.inb ? (unsigned)(row * (int)g.sr + c * 8) * 2u : 0u;
+      dma16_s(s.base, voff, dst);
       return;
     }
-    const bf16* base = g.data + (long long)b * g.sb + (long long)d * g.sd;
-    const bool fast = bd_ok && row0 >= 0 && col0 >= 0 && row0 + Tile::ROWS <= g.r && col0 + Tile::COLS <= g.c &&
-                      (long long)Tile::ROWS * g.sr < (1ll << 30);
-    if (fast) {
-      const bf16* tbase = base + (long long)row0 * g.sr + col0;
-      dma16_s(tbase, (unsigned)(row * (int)g.sr + c * 8) * 2u, dst);
+    if (s.inb) {
+      dma16_s(s.base + (long long)s.row0 * g.sr + s.col0, (unsigned)(row * (int)g.sr + c * 8) * 2u, dst);
     } else {
-      const int gr = row0 + row, gc = col0 + c * 8;
-      const bool ok = bd_ok && (unsigned)gr < (unsigned)g.r && (unsigned)gc < (unsigned)g.c;
-      const void* src = ok ? (const void*)(base + (long long)gr * g.sr + gc) : (const void*)zero_page;
+      const int gr = s.row0 + row, gc = s.col0 + c * 8;
+      const bool ok = (unsigned)gr < (unsigned)g.r && (unsigned)gc < (unsigned)g.c;
+      const void* src = ok ? (const void*)(s.base + (long long)gr * g.sr + gc) : (const void*)zero_page;
       dma16_v(src, dst);
     }
   }
@@ -219,11 +231,12 @@ struct Loader {
   template <bool ALIGNED>
   static __device__ __forceinline__ void load(char* tile_base, const gl<bf16>& g, int b, int d, int row0,
                                               int col0, int wave) {
+    const Src src = prep<ALIGNED>(g, b, d, row0, col0);
 #pragma unroll
-    for (int j = 0; j < INSTR_PER_WAVE; ++j) load_one<ALIGNED>(j, tile_base, g, b, d, row0, col0, wave);
+    for (int j = 0; j < INSTR_PER_WAVE; ++j) issue<ALIGNED>(j, tile_base, g, src, wave);
   }
 
-  // Host-independent check used for the kernel's ALIGNED specialisation.
+  // Whether `g` qualifies for the kernel's ALIGNED specialisation.
   static __device__ __forceinline__ bool aligned(const gl<bf16>& g) {
     return g.r % Tile::ROWS == 0 && g.c % Tile::COLS == 0 && (long long)Tile::ROWS * g.sr < (1ll << 30);
   }
@@ -346,6 +359,28 @@ __device__ __forceinline__ void load_row_frags(RowFrags<MS, RB, KS>& fr, char* t
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) fr.f[rb][ks] = row_operand<Tile, MS>(tile_base, row0 + rb * MS, ks);
+}
+
+// Row operands of a tile read straight from global memory into registers,
+// for a tile whose only use is as hoisted MFMA fragments (so it needs no
+// LDS): rows row0 + rb*MS + lane%MS, 8 columns at col0 + 8*(ks*LG +
+// lane/MS).  Out-of-range rows or columns give zeros.
+template <int MS, int RB, int KS>
+__device__ __forceinline__ void load_row_frags_global(RowFrags<MS, RB, KS>& fr, const gl<bf16>& g, int b, int d,
+                                                      int row0, int col0) {
+  const int lane = lane_id();
+  const bool bd_ok = (unsigned)b < (unsigned)g.b && (unsigned)d < (unsigned)g.d;
+  const bf16* base = g.data + (long long)b * g.sb + (long long)d * g.sd;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int row = row0 + rb * MS + lane % MS;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int col = col0 + 8 * (ks * MF<MS>::LG + lane / MS);
+      const bool ok = bd_ok && (unsigned)row < (unsigned)g.r && (unsigned)col < (unsigned)g.c;
+      fr.f[rb][ks] = ok ? *(const bf16x8*)(base + (long long)row * g.sr + col) : bf16x8{};
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -531,6 +566,7 @@ template <int MS, int R, int C, class TB, int KS>
 __device__ __forceinline__ void mma_ABt_frags(RTile<MS, R, C>& acc, const RowFrags<MS, R / MS, KS>& a,
                                               char* b_base, int b_row0) {
   static_assert(TB::COLS == KS * MF<MS>::KSTEP, "inner dimensions differ");
+  __builtin_amdgcn_s_setprio(1);  // MFMA run first; a co-resident wave's VALU fills the gaps
   fill(acc, 0.f);
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -541,6 +577,7 @@ __device__ __forceinline__ void mma_ABt_frags(RTile<MS, R, C>& acc, const RowFra
       for (int rb = 0; rb < acc.RB; ++rb) acc.f[cb][rb] = MF<MS>::mma(aop, a.f[rb][ks], acc.f[cb][rb]);
     }
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 template <int MS, int R, int C, class TA, class TB>
@@ -577,6 +614,7 @@ __device__ __forceinline__ void mma_rAB(RTile<MS, R, C>& acc, const BTile<MS, R,
   const int lane = lane_id();
   const int lh = lane / MS;
   const int ngrp = (lane % MS) & ~15;
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int q = 0; q < NG; q += 2) {
     const int kb0 = q / G, g0 = q % G, kb1 = (q + 1) / G, g1 = (q + 1) % G;
@@ -591,6 +629,7 @@ __device__ __forceinline__ void mma_rAB(RTile<MS, R, C>& acc, const BTile<MS, R,
         acc.f[cb][rb] = MF<MS>::mma(aop, cat(a.f[kb0][rb][g0], a.f[kb1][rb][g1]), acc.f[cb][rb]);
     }
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // ---------------------------------------------------------------------------
@@ -670,6 +709,21 @@ __device__ __forceinline__ void row_apply(RTile<MS, R, C>& out, const RTile<MS, 
 #pragma unroll
       for (int i = 0; i < MF<MS>::CREGS; ++i) out.f[cb][rb][i] = fn(t.f[cb][rb][i], s);
     }
+}
+
+// out = t * v[row], skipping the multiplies when every v is exactly 1.0
+// (the online-softmax correction once the running maximum has settled):
+// x * 1.0f == x bit for bit, so the result is the same either way.
+template <int MS, int R, int C>
+__device__ __forceinline__ void row_scale(RTile<MS, R, C>& out, const RTile<MS, R, C>& t, const RVec<MS, R>& v) {
+  bool ones = true;
+#pragma unroll
+  for (int rb = 0; rb < out.RB; ++rb) ones = ones && (v.v[rb] == 1.0f);
+  if (__builtin_amdgcn_ballot_w64(!ones) == 0) {
+    out = t;
+    return;
+  }
+  row_apply(out, t, v, [](float x, float s) { return x * s; });
 }
 
 template <int MS, int R, int C>

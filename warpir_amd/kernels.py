@@ -10,7 +10,7 @@ from __future__ import annotations
 from typing import Callable, Dict
 
 from warpir_amd.ir import Kernel
-from warpir_amd.passes.modulo_scheduler import gfx950_cost_model, kernel_pass
+from warpir_amd.passes.modulo_scheduler import gfx950_attention_cost_model, gfx950_cost_model, kernel_pass
 from warpir_amd.workloads import build_attention_kernel, build_gemm_kernel, build_mha_forward_kernel
 
 
@@ -29,13 +29,25 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "gemm_256_k32": lambda: _gemm_mi355x(32),
     # Same tile with a 64-deep K step: MMA twice as long per stage, 2-slot ring.
     "gemm_256_k64": lambda: _gemm_mi355x(64),
+    # 8 wavefronts (2 per SIMD) of 128x64 / 64x128 on the 256x256x64 tile.
+    "gemm_256_k64_w8": lambda: _gemm_mi355x(64, wave_m=128, wave_n=64),
+    "gemm_256_k64_w8t": lambda: _gemm_mi355x(64, wave_m=64, wave_n=128),
     # The reference's single-head attention IR (tests/attention_baseline.py:46-186).
     "attn_ref_ssa": lambda: build_attention_kernel(),
-    # Multi-head FlashAttention forward, [B, H, S, D] with LSE.
-    "mha_d128": lambda: build_mha_forward_kernel(d=128, block_q=128, block_kv=64, wave_rows=32),
-    "mha_d64_causal": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
-                                                       causal=True, name="mha_fwd_causal"),
+    # Multi-head FlashAttention forward, [B, H, S, D] with LSE: SSA form (loads
+    # waited every KV step) and the pipelined prefetch form of kernel_pass.
+    "mha_d128_ssa": lambda: build_mha_forward_kernel(d=128, block_q=128, block_kv=64, wave_rows=32),
+    "mha_d128": lambda: _mha(128, 128, 64, 32, causal=False),
+    "mha_d64_causal_ssa": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
+                                                           causal=True, name="mha_fwd_causal"),
+    "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True),
 }
+
+
+def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool) -> Kernel:
+    k = build_mha_forward_kernel(d=d, block_q=block_q, block_kv=block_kv, wave_rows=wave_rows, causal=causal,
+                                 name="mha_fwd_causal" if causal else "mha_fwd")
+    return kernel_pass(k, cost_model=gfx950_attention_cost_model(block_q, block_kv, d))
 
 _handles: Dict[str, object] = {}
 

@@ -127,9 +127,10 @@ class CDNA4Lowerer:
         self._classify(kernel)
         self.geo = self._geometry(kernel)
         self._assign_roles(kernel.body)
+        self._pending_hoist = self._hoistable()
+        self._register_tiles = self._register_only_tiles()
         self._allocate_lds()
         self.wait_n, self.war_barrier = _schedule(kernel, self)
-        self._pending_hoist = self._hoistable()
         body: List[str] = []
         self._emit_ops(kernel.body, body, 1)
         return self._assemble(kernel, body)
@@ -176,6 +177,7 @@ class CDNA4Lowerer:
         self._view_cache: Dict[str, SlotViewOp] = {}
         self._view_kernel = None
         self._rotated: Dict[int, str] = {}
+        self._register_tiles: Dict[str, tuple] = {}
         self._aligned_checks: set = set()
         self._fused_loads: Dict[int, List[Op]] = {}
         self._fused_ids: set = set()
@@ -310,6 +312,8 @@ class CDNA4Lowerer:
         for op in _walk(self.kernel.body):
             if isinstance(op, TMALoadOp):
                 key, t, count = self.resolve(op.result.name), op.result.type, 1
+                if key in self._register_tiles:
+                    continue
             elif isinstance(op, AllocSharedOp):
                 key, t = self.resolve(op.result.name), op.result.type.tile_type
                 count = op.result.type.count
@@ -417,6 +421,16 @@ class CDNA4Lowerer:
                 w(f"{pad}wir::fill({self._var(op.result)}, {val});")
                 return
             raise LoweringError(f"{type(op).__name__} on {op.result.type}")
+        if isinstance(op, TMALoadOp) and self.resolve(op.result.name) in self._register_tiles:
+            name = self.resolve(op.result.name)
+            var, ks, rows, _loop = self._register_tiles[name]
+            sub = op.source.type.sub_tile_type
+            b, d, rt, ct = (self._int(c) for c in op.coords)
+            w(f"{pad}wir::RowFrags<{ms}, {rows // ms}, {ks}> {var};")
+            w(f"{pad}wir::load_row_frags_global({var}, globals.{_cname(op.source.name)[2:]}, {b}, {d}, "
+              f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols});")
+            self._hoisted[name] = (var, ks)
+            return
         if isinstance(op, (TMALoadOp, TMALoadBufOp)):
             if id(op) in self._fused_ids:
                 return
@@ -432,6 +446,8 @@ class CDNA4Lowerer:
             w(f"{pad}{self._load_call(op, 'load<WIR_AL>(', ptr, key)});")
             return
         if isinstance(op, (WaitOp, WaitBufOp)):
+            if isinstance(op, WaitOp) and all(self.resolve(v.name) in self._register_tiles for v in op.values):
+                return
             n = self.wait_n.get(id(op), 0)
             w(f"{pad}wir::wait_vm_barrier<{n}>();")
             return
@@ -449,11 +465,18 @@ class CDNA4Lowerer:
             if pipe is not None:
                 loads = self._fused_loads.get(id(op), [])
                 calls, total = [], 0
-                for ld in loads:
+                for n_ld, ld in enumerate(loads):
                     lptr, lkey = self._buf_ptr(ld.buf, ld.slot)
                     n = self.loads_per_wave(ld.buf.type.tile_type)
-                    calls.append(f"if (q >= {total} && q < {total + n}) "
-                                 + self._load_call(ld, f"load_one<WIR_AL>(q - {total}, ", lptr, lkey) + ");")
+                    loader = f"wir::Loader<{self.stile(lkey)}, {self.geo.nw}>"
+                    g = f"globals.{_cname(ld.source.name)[2:]}"
+                    sub = ld.source.type.sub_tile_type
+                    bb, dd, rt, ct = (self._int(c) for c in ld.coords)
+                    self._aligned_checks.add((self.stile(lkey), _cname(ld.source.name)[2:]))
+                    w(f"{pad}const auto src{n_ld}_ = {loader}::prep<WIR_AL>({g}, {bb}, {dd}, ({rt}) * {sub.rows}, "
+                      f"({ct}) * {sub.cols});")
+                    calls.append(f"if (q >= {total} && q < {total + n}) {loader}::issue<WIR_AL>(q - {total}, "
+                                 f"{lptr}, {g}, src{n_ld}_, wir_wave);")
                     total += n
                 w(f"{pad}{pipe}.run<{total}>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int q) {{")
                 for c in calls:
@@ -503,9 +526,11 @@ class CDNA4Lowerer:
                 w(f"{pad}  wir::row_apply({self._var(op.result)}, {self._var(op.tile)}, rcp_, "
                   f"[](float x, float s) {{ return x * s; }}); }}")
                 return
-            sym = "-" if isinstance(op, SubRowOp) else "*"
+            if isinstance(op, MulRowOp):
+                w(f"{pad}wir::row_scale({self._var(op.result)}, {self._var(op.tile)}, {self._var(op.vec)});")
+                return
             w(f"{pad}wir::row_apply({self._var(op.result)}, {self._var(op.tile)}, {self._var(op.vec)}, "
-              f"[](float x, float s) {{ return x {sym} s; }});")
+              f"[](float x, float s) {{ return x - s; }});")
             return
         if isinstance(op, CausalMaskOp):
             t = op.tile.type
@@ -591,7 +616,7 @@ class CDNA4Lowerer:
     def _emit_for(self, op: ForOp, out: List[str], depth: int) -> None:
         pad = "  " * depth
         for name, (var, ks, rows, loop) in self._pending_hoist.items():
-            if loop is op:
+            if loop is op and name not in self._register_tiles:
                 ptr, key = self._tile_ptr(self.values[name])
                 out.append(f"{pad}wir::RowFrags<{self.geo.ms}, {rows // self.geo.ms}, {ks}> {var};")
                 out.append(f"{pad}wir::load_row_frags<{self.stile(key)}>({var}, {ptr}, wave_row0);")
@@ -648,6 +673,32 @@ class CDNA4Lowerer:
     # ------------------------------------------------------------------
     # assembly
     # ------------------------------------------------------------------
+    def _register_only_tiles(self) -> Dict[str, tuple]:
+        """Shared tiles loaded once whose only reads are hoisted MMA fragments.
+
+        Such a tile never needs LDS: its fragments are loaded from global
+        memory straight into registers where the IR loads it, and waits on
+        it need no barrier (the compiler tracks the register loads)."""
+        out: Dict[str, tuple] = {}
+        for name, info in self._pending_hoist.items():
+            loads = [o for o in _walk(self.kernel.body)
+                     if isinstance(o, TMALoadOp) and self.resolve(o.result.name) == name]
+            if len(loads) != 1 or any(ld in _walk(info[3].body) for ld in loads):
+                continue
+            uses_ok = True
+            for o in _walk(self.kernel.body):
+                if isinstance(o, (TMALoadOp, WaitOp, TMALoadBufOp, WaitBufOp)):
+                    continue
+                for f, v in vars(o).items():
+                    for x in _values_in(v):
+                        if self.resolve(x.name) != name:
+                            continue
+                        if not (isinstance(o, MMAOp) and o.transpose_b and f == "a"):
+                            uses_ok = False
+            if uses_ok:
+                out[name] = info
+        return out
+
     def _hoistable(self) -> Dict[str, tuple]:
         """Shared tiles read as the row operand of a transpose_b MMA inside a
         loop that never reloads them (e.g. the resident Q tile): their MFMA
@@ -834,18 +885,22 @@ class _Sim:
         low = self.low
         for op in ops:
             if isinstance(op, TMALoadOp):
+                if low.resolve(op.result.name) in low._register_tiles:
+                    continue
                 self.load(op, (low.resolve(op.result.name), 0), op.result.type)
             elif isinstance(op, TMALoadBufOp):
                 key = (low.resolve(op.buf.name), self.slot(op.slot))
                 self.load(op, key, op.buf.type.tile_type)
             elif isinstance(op, WaitOp):
-                self.wait(op, {self.key_of_tile(v) for v in op.values})
+                keys = {self.key_of_tile(v) for v in op.values if low.resolve(v.name) not in low._register_tiles}
+                if keys:
+                    self.wait(op, keys)
             elif isinstance(op, WaitBufOp):
                 s = self.slot(op.slot)
                 self.wait(op, {(low.resolve(b.name), s) for b in op.bufs})
             elif isinstance(op, MMAOp):
                 for v in (op.a, op.b):
-                    if low._lds_key(v) is not None:
+                    if low._lds_key(v) is not None and low.resolve(v.name) not in low._register_tiles:
                         self.read(self.key_of_tile(v))
             elif isinstance(op, MMABufOp):
                 self.read((low.resolve(op.a_buf.name), self.slot(op.a_slot)))

@@ -24,15 +24,18 @@ from warpir_amd.ir.ops import (
     AllocSharedOp,
     BufSlotExpr,
     ForOp,
+    IntAffineOp,
     Kernel,
     MMABufOp,
     MMAOp,
     Op,
+    SlotViewOp,
     TMALoadBufOp,
     TMALoadOp,
     TMAStoreOp,
     Value,
     WaitBufOp,
+    WaitOp,
     YieldOp,
 )
 from warpir_amd.ir.types import SharedBufferType
@@ -56,6 +59,8 @@ class CostModel:
     resources: Dict[str, int]
     max_cycles: int = MAX_CYCLES
     depth: int = DEPTH
+    # Upper bound on ring slots (the LDS budget); None = no bound.
+    max_stages: Optional[int] = None
 
 
 REFERENCE_COST_MODEL = CostModel(latency=dict(LATENCY), resources=dict(RESOURCE_COUNTS))
@@ -78,6 +83,20 @@ def gfx950_cost_model(block_m: int, block_n: int, block_k: int) -> CostModel:
 
 
 GFX950_COST_MODEL = gfx950_cost_model(256, 256, 32)
+
+
+def gfx950_attention_cost_model(block_q: int, block_kv: int, d: int, lds_budget: int = 64 * 1024) -> CostModel:
+    """Cost model of one FlashAttention KV step on an MI355X CU.
+
+    Each of the two MMAs (S = Q K^T and O += P V) is ``2*block_q*block_kv*d``
+    flops; loads take ~8 units as for GEMM.  The ring depth is capped by an
+    LDS budget per workgroup (64 KiB by default, so two workgroups share a
+    CU and one's softmax overlaps the other's MFMAs).
+    """
+    mma_units = max(1, round(2 * block_q * block_kv * d / (4 * 1024) / 256))
+    stage_bytes = 2 * block_kv * d * 2
+    return CostModel(latency={TMALoadOp: ("tma", 8), MMAOp: ("tc", mma_units), TMAStoreOp: ("tma", 8)},
+                     resources={"tma": 4, "tc": 1}, max_stages=max(2, lds_budget // stage_bytes))
 
 
 @dataclass
@@ -176,7 +195,7 @@ def _shape_schedule(instructions: List[MSInstruction], offsets: List[int], ii: i
     return prologue, steady_state, epilogue, ii, num_stages, stage_of
 
 
-def _loop_instructions(loop: ForOp, cost: CostModel) -> Dict[str, MSInstruction]:
+def _loop_instructions(loop: ForOp, cost: CostModel, transitive: bool = False) -> Dict[str, MSInstruction]:
     """One ``MSInstruction`` per load / MMA / store, keyed by the op's text (``:183-217``)."""
     instrs: Dict[str, MSInstruction] = {}
     for op in loop.body:
@@ -187,6 +206,22 @@ def _loop_instructions(loop: ForOp, cost: CostModel) -> Dict[str, MSInstruction]
     producer: Dict[Value, MSInstruction] = {
         op.result: instrs[str(op)] for op in loop.body if type(op) in (TMALoadOp, MMAOp)
     }
+    if transitive:
+        # Values computed by unscheduled ops (the softmax chain) inherit the
+        # scheduled producers of their operands, so an MMA fed by them still
+        # depends on the MMA that started the chain.
+        chains: Dict[Value, List[MSInstruction]] = {}
+        for op in loop.body:
+            if str(op) in instrs or not hasattr(op, "result"):
+                continue
+            srcs: List[MSInstruction] = []
+            for name, operand in vars(op).items():
+                if name == "result" or not isinstance(operand, Value):
+                    continue
+                if operand in producer:
+                    srcs.append(producer[operand])
+                srcs.extend(chains.get(operand, []))
+            chains[op.result] = srcs
     carried = {ia.block_arg for ia in loop.iter_args}
     yld = next(op for op in loop.body if isinstance(op, YieldOp))
     next_value = {ia.block_arg: yld.values[k] for k, ia in enumerate(loop.iter_args)}
@@ -202,10 +237,29 @@ def _loop_instructions(loop: ForOp, cost: CostModel) -> Dict[str, MSInstruction]
             src = producer.get(next_value.get(operand, operand))
             if src is not None:
                 ins.parent_edges.append(MSInstructionEdge(source=src, dest=ins, distance=distance))
+            if transitive and distance == 0:
+                for s in chains.get(operand, []):
+                    if s is not ins and all(e.source is not s for e in ins.parent_edges):
+                        ins.parent_edges.append(MSInstructionEdge(source=s, dest=ins, distance=0))
     return instrs
 
 
+def _reference_form_applies(loop: ForOp) -> bool:
+    """The reference rewrite (``:239-358``) handles bodies of loads, waits and
+    MMAs whose operands are all loaded inside the loop."""
+    loaded = {op.result for op in loop.body if isinstance(op, TMALoadOp)}
+    for op in loop.body:
+        if isinstance(op, MMAOp):
+            if op.transpose_b or op.a not in loaded or op.b not in loaded:
+                return False
+        elif not isinstance(op, (TMALoadOp, WaitOp, YieldOp)):
+            return False
+    return True
+
+
 def _pipeline_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
+    if not _reference_form_applies(loop) and any(isinstance(op, TMALoadOp) for op in loop.body):
+        return _prefetch_loop(loop, cost)
     instrs = _loop_instructions(loop, cost)
     manager = MSInstructionManager()
     for ins in instrs.values():
@@ -272,13 +326,82 @@ def _pipeline_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
     return out
 
 
+def _prefetch_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
+    """Buffer form for loops the reference rewrite cannot take: an MMA reads
+    a loop-invariant tile (the resident Q of FlashAttention), a register
+    value, or the body carries non-MMA work (the online-softmax chain).
+
+    The loop keeps every compute op in place; only its loads move.  With
+    ``S`` ring slots chosen by the modulo schedule (the MMAs' stage behind
+    their loads, at least 2, at most ``cost.max_stages``), the prologue
+    loads tiles ``start .. start+S-2``; iteration ``i`` waits on slot
+    ``i % S``, issues the loads of tile ``i + S - 1`` into the slot freed
+    by iteration ``i - 1``, and names the tiles it reads through
+    ``slot_view``.  Loads past the end of the data read zeros (TMA
+    out-of-bounds semantics), so no drain steps are needed: the last
+    ``S - 1`` iterations simply prefetch tiles that are never read.
+    """
+    instrs = _loop_instructions(loop, cost, transitive=True)
+    manager = MSInstructionManager()
+    for ins in instrs.values():
+        manager.add_instruction(ins)
+    prologue, _steady, _epi, _ii, stages, stage_of = manager.solve(
+        max_cycles=cost.max_cycles, depth=cost.depth, resource_counts=cost.resources)
+    if prologue is None:
+        return None
+    loads = [op for op in loop.body if isinstance(op, TMALoadOp)]
+    mmas = [op for op in loop.body if isinstance(op, MMAOp)]
+    if not mmas:
+        raise PipelineError("loop has no MMA to pipeline")
+    stages = max(2, stages)
+    if cost.max_stages is not None:
+        stages = max(2, min(stages, cost.max_stages))
+    if not isinstance(loop.start, int):
+        raise PipelineError("the prefetch form needs a constant loop start")
+    iv = loop.induction_var
+    ring = {ld.result: Value(f"{ld.source.name.lower()}_bufs",
+                             SharedBufferType(tile_type=ld.result.type, count=stages)) for ld in loads}
+    all_rings = tuple(ring[ld.result] for ld in loads)
+    out: List[Op] = [AllocSharedOp(result=ring[ld.result]) for ld in loads]
+    for p in range(stages - 1):
+        tile = loop.start + p * (loop.step if isinstance(loop.step, int) else 1)
+        for ld in loads:
+            out.append(TMALoadBufOp(buf=ring[ld.result], slot=tile % stages, source=ld.source,
+                                    coords=ld.substitute({iv: tile}).coords))
+    nxt = Value(f"{iv.name}_pf", iv.type)
+    body: List[Op] = [WaitBufOp(bufs=all_rings, slot=BufSlotExpr(value=iv, offset=0, modulus=stages)),
+                      IntAffineOp(result=nxt, input=iv, mul=1, add=stages - 1)]
+    for ld in loads:
+        body.append(TMALoadBufOp(buf=ring[ld.result], slot=BufSlotExpr(value=iv, offset=stages - 1, modulus=stages),
+                                 source=ld.source, coords=ld.substitute({iv: nxt}).coords))
+    for ld in loads:
+        body.append(SlotViewOp(result=ld.result, buf=ring[ld.result],
+                               slot=BufSlotExpr(value=iv, offset=0, modulus=stages)))
+    ring_tiles = set(ring)
+    for op in loop.body:
+        if isinstance(op, TMALoadOp):
+            continue
+        if isinstance(op, WaitOp):
+            rest = tuple(v for v in op.values if v not in ring_tiles)
+            if rest:
+                body.append(WaitOp(values=rest))
+            continue
+        body.append(op)
+    out.append(ForOp(induction_var=iv, start=loop.start, stop=loop.stop, step=loop.step,
+                     iter_args=loop.iter_args, body=tuple(body), results=loop.results,
+                     tile_size=loop.tile_size))
+    return out
+
+
 def kernel_pass(kernel: Kernel, cost_model: Optional[CostModel] = None) -> Kernel:
     """Pipeline every top-level unit-step loop of *kernel* (``:168-358``).
 
     Loops whose schedule has no solution are kept unchanged, as in the
-    reference.  Raises ``PipelineError`` (a ``KeyError``) on a loop whose
-    MMA reads a tile that is not loaded inside the loop.  ``cost_model``
-    defaults to the reference's constants.
+    reference.  Loops of loads and MMAs get the reference's buffer form;
+    loops with a softmax chain, loop-invariant or register MMA operands
+    (FlashAttention) get the prefetch form of ``_prefetch_loop`` where the
+    reference raises ``KeyError`` (``:309``).  ``cost_model`` defaults to
+    the reference's constants.
     """
     cost = cost_model or REFERENCE_COST_MODEL
     body: List[Op] = []
@@ -292,4 +415,5 @@ def kernel_pass(kernel: Kernel, cost_model: Optional[CostModel] = None) -> Kerne
 
 
 __all__ = ["MSInstructionEdge", "MSInstruction", "MSInstructionManager", "PipelineError",
-           "CostModel", "REFERENCE_COST_MODEL", "GFX950_COST_MODEL", "gfx950_cost_model", "kernel_pass"]
+           "CostModel", "REFERENCE_COST_MODEL", "GFX950_COST_MODEL", "gfx950_cost_model",
+           "gfx950_attention_cost_model", "kernel_pass"]
