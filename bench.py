@@ -172,6 +172,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["gemm", "fa"], default=None)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of MIB MiB (read MIB, write MIB) three times, "
+                         "the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -193,6 +196,15 @@ def main() -> int:
     if args.only in (None, "fa"):
         print("[bench] fa-fwd B16 H16 S4096 D128", file=sys.stderr, flush=True)
         fa = bench_fa(args.steps, args.warmup, not args.no_cpu)
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] calibration copy: {args.calibrate_copy} MiB read + written, 3 launches",
+              file=sys.stderr, flush=True)
     head = gemm or fa
     line = {
         "metric": METRIC, "value": head["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,

@@ -13,7 +13,7 @@ import sys
 _ALIASED = (
     "ir", "ir.ops", "ir.types",
     "printing", "printing.printer",
-    "passes", "passes.modulo_scheduler",
+    "passes", "passes.modulo_scheduler", "passes.warp_assigner",
     "lowering", "runtime",
 )
 
