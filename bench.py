@@ -165,6 +165,47 @@ def bench_fa(steps, warmup, cpu: bool):
     return res
 
 
+def bench_extra(steps: int, warmup: int):
+    """The other BASELINE configurations, one timed line each (no CPU leg).
+
+    GEMM 4096^3 (config 2), skinny GEMM M=128 N=K=8192 (config 3', judged
+    on the HBM roofline: 2(MK+KN+MN) bytes), causal FA B8 H32 S8192 D64
+    (config 5, matmul flops halved for the mask).
+    """
+    import torch
+
+    from oracle.torch_ref import seeded_normal
+    from warpir_amd import api, kernels
+
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    for name, (m, n, k) in {"gemm_4096": (4096, 4096, 4096), "gemm_skinny_m128": (128, 8192, 8192)}.items():
+        a = seeded_normal((m, k), 5, 0.1).cuda()
+        b = seeded_normal((k, n), 6, 0.1).cuda()
+        c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        variant = api.SKINNY_GEMM_VARIANT if m <= 128 else api.GEMM_VARIANT
+        h = kernels.handle(variant)
+        ms, _ = _time_launches(lambda: h(A=a, B=b, N=k, C_global=c), steps, warmup, stream)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        rec = {"M": m, "N": n, "K": k, "ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
+               "kernel": variant}
+        if name == "gemm_skinny_m128":
+            gbs = 2.0 * (m * k + k * n + m * n) / (ms * 1e-3) / 1e9
+            rec.update({"hbm_gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "bound": "hbm"})
+        out[name] = rec
+        del a, b, c
+    bsz, heads, seq, d = 8, 32, 8192, 64
+    q, k, v = (seeded_normal((bsz, heads, seq, d), s).cuda() for s in (3, 4, 5))
+    o = torch.empty_like(q)
+    lse = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
+    h = kernels.handle("mha_d64_causal")
+    ms, _ = _time_launches(lambda: h(Q=q, K=k, V=v, N=seq, O=o, L=lse), steps, warmup, stream)
+    tf = api.attention_flops(bsz, heads, seq, d, causal=True) / (ms * 1e-3) / 1e12
+    out["fa_fwd_causal_b8_h32_s8192_d64"] = {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
+                                             "kernel": "mha_d64_causal"}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +213,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["gemm", "fa"], default=None)
+    ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (read MIB, write MIB) three times, "
                          "the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -196,6 +238,10 @@ def main() -> int:
     if args.only in (None, "fa"):
         print("[bench] fa-fwd B16 H16 S4096 D128", file=sys.stderr, flush=True)
         fa = bench_fa(args.steps, args.warmup, not args.no_cpu)
+    extra = None
+    if args.only is None and not args.no_extra:
+        print("[bench] other configurations", file=sys.stderr, flush=True)
+        extra = bench_extra(max(5, args.steps // 2), max(2, args.warmup // 2))
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
@@ -216,6 +262,8 @@ def main() -> int:
         line["cpu_baseline"] = head["cpu_baseline"]
     if gemm is not None and fa is not None:
         line["fa_fwd"] = fa
+    if extra is not None:
+        line["other_configs"] = extra
     line["device"] = info
     print(json.dumps(line))
     return 0

@@ -16,10 +16,14 @@ from typing import Optional, Tuple
 from warpir_amd import kernels
 
 GEMM_VARIANT = "gemm_256_k64"
+SKINNY_GEMM_VARIANT = "gemm_128_k64"   # M <= 128: four times the workgroups of the 256x256 tile
 
 
-def gemm(a, b, out=None, variant: str = GEMM_VARIANT):
-    """``out[M, N] = a[M, K] @ b[K, N]`` in bf16 with fp32 accumulation."""
+def gemm(a, b, out=None, variant: Optional[str] = None):
+    """``out[M, N] = a[M, K] @ b[K, N]`` in bf16 with fp32 accumulation.
+
+    The default variant is the 256x256 tile; M <= 128 takes the 128x128 one.
+    """
     import torch
 
     if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
@@ -30,6 +34,8 @@ def gemm(a, b, out=None, variant: str = GEMM_VARIANT):
         raise ValueError("gemm: K and N must be multiples of 8 (16-byte rows)")
     if out is None:
         out = torch.empty(m, n, dtype=torch.bfloat16, device=a.device)
+    if variant is None:
+        variant = SKINNY_GEMM_VARIANT if m <= 128 else GEMM_VARIANT
     kernels.handle(variant)(A=a, B=b, N=k, C_global=out)
     return out
 

@@ -561,6 +561,88 @@ struct MMAPipeAB {
   }
 };
 
+// 8-wave ping-pong form of the ring-pipelined MMA (a 256x256 block tile as
+// 8 wavefronts, two per SIMD).  Every wavefront runs the same step per
+// tile -- a memory phase (the LDS reads of the tile's MFMA fragments and,
+// in group 0 = wavefronts 0-3, the LDS-DMA of the tile the IR loads this
+// iteration), a barrier, then a compute phase of MFMAs from registers, and
+// the barrier that opens the next memory phase -- but group 1 (wavefronts
+// 4-7) starts one barrier later and group 0 ends one barrier later.  The
+// groups are therefore one phase apart: on every SIMD one wavefront feeds
+// the matrix core while its partner moves data.  Both groups execute the
+// same number of barriers.  A slot is refilled (by group 0's DMA in the
+// memory phase of tile t) only after both groups have read its previous
+// tile t-1 in the two phases before; group 0 waits for its own DMAs of
+// tile t before the barrier that opens the first phase reading it.
+// MFMAs into each accumulator run in k order, exactly as mma_AB.
+template <int MS, int R, int C, class TA, class TB>
+struct PingPongAB {
+  static constexpr int K = TA::COLS;
+  static constexpr int KS = K / MF<MS>::KSTEP;
+  static constexpr int RB = RTile<MS, R, C>::RB, CB = RTile<MS, R, C>::CB;
+  static_assert(TA::COLS == TB::ROWS, "inner dimensions differ");
+  static_assert(K % MF<MS>::KSTEP == 0, "k tile must be a multiple of the MFMA k");
+  int group;
+
+  // Drain the prologue's DMAs (issued by all eight wavefronts), then put
+  // group 1 one barrier behind group 0.
+  __device__ __forceinline__ void init(int wave) {
+    group = wave >> 2;
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (group != 0) barrier();
+  }
+
+  // One step on tile t (slot pointers a_t, b_t).  Group 0 also issues NLOAD
+  // DMAs via loads(q) and, first, waits until at most VM of its DMAs (those
+  // of tiles newer than t) are in flight.
+  template <int VM, int NLOAD, class LoadFn>
+  __device__ __forceinline__ void step(RTile<MS, R, C>& acc, char* a_t, int a_row0, char* b_t, int b_col0,
+                                       LoadFn loads) {
+    if (group == 0) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" :: "n"(VM) : "memory");
+    else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int lane = lane_id();
+    const int lh = lane / MS;
+    const int ngrp = (lane % MS) & ~15;
+    bf16x8 bop[KS][RB];
+    bf16x4 aop[KS][CB][2];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) bop[ks][rb] = row_operand<TA, MS>(a_t, a_row0 + rb * MS, ks);
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const int k0 = ks * MF<MS>::KSTEP + 8 * lh;
+        const int n0 = b_col0 + cb * MS + ngrp;
+        aop[ks][cb][0] = tr_operand4<TB>(b_t, k0, n0);
+        aop[ks][cb][1] = tr_operand4<TB>(b_t, k0 + 4, n0);
+      }
+    }
+    if (group == 0) {
+#pragma unroll
+      for (int q = 0; q < NLOAD; ++q) loads(q);
+    }
+    barrier();
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc.f[cb][rb] = MF<MS>::mma(cat(aop[ks][cb][0], aop[ks][cb][1]), bop[ks][rb], acc.f[cb][rb]);
+    __builtin_amdgcn_s_setprio(0);
+  }
+
+  // Group 0 matches group 1's extra barrier.
+  __device__ __forceinline__ void finish(RTile<MS, R, C>&) {
+    if (group == 0) barrier();
+  }
+};
+
 // acc = a @ b^T with `a` from hoisted register fragments or LDS; b: ROWREAD LDS [.][K].
 template <int MS, int R, int C, class TB, int KS>
 __device__ __forceinline__ void mma_ABt_frags(RTile<MS, R, C>& acc, const RowFrags<MS, R / MS, KS>& a,

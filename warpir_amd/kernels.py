@@ -15,10 +15,10 @@ from warpir_amd.workloads import build_attention_kernel, build_gemm_kernel, buil
 
 
 def _gemm_mi355x(block_k: int = 32, block_m: int = 256, block_n: int = 256, wave_m: int = 128,
-                 wave_n: int = 128) -> Kernel:
+                 wave_n: int = 128, load_units: int = 8) -> Kernel:
     return kernel_pass(build_gemm_kernel(block_m=block_m, block_n=block_n, block_k=block_k, wave_m=wave_m,
                                          wave_n=wave_n, name="gemm"),
-                       cost_model=gfx950_cost_model(block_m, block_n, block_k))
+                       cost_model=gfx950_cost_model(block_m, block_n, block_k, load_units=load_units))
 
 
 VARIANTS: Dict[str, Callable[[], Kernel]] = {
@@ -29,9 +29,10 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "gemm_256_k32": lambda: _gemm_mi355x(32),
     # Same tile with a 64-deep K step: MMA twice as long per stage, 2-slot ring.
     "gemm_256_k64": lambda: _gemm_mi355x(64),
-    # 8 wavefronts (2 per SIMD) of 128x64 / 64x128 on the 256x256x64 tile.
-    "gemm_256_k64_w8": lambda: _gemm_mi355x(64, wave_m=128, wave_n=64),
-    "gemm_256_k64_w8t": lambda: _gemm_mi355x(64, wave_m=64, wave_n=128),
+    # 128x128 block tile (4 wavefronts of 64x64): more workgroups for short M (skinny GEMM).
+    "gemm_128_k64": lambda: _gemm_mi355x(64, block_m=128, block_n=128, wave_m=64, wave_n=64),
+    # 8 wavefronts (2 per SIMD) of 128x64 in the ping-pong form, K=32 with a 4-slot ring.
+    "gemm_256_pp": lambda: _gemm_mi355x(32, wave_m=128, wave_n=64, load_units=12),
     # The reference's single-head attention IR (tests/attention_baseline.py:46-186).
     "attn_ref_ssa": lambda: build_attention_kernel(),
     # Multi-head FlashAttention forward, [B, H, S, D] with LSE: SSA form (loads

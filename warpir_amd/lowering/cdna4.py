@@ -84,6 +84,7 @@ class CDNA4Target:
     xcd_remap: bool = True
     group_m: int = 8
     rotate_mma: bool = True
+    pingpong: bool = True
 
 
 @dataclass
@@ -179,6 +180,7 @@ class CDNA4Lowerer:
         self._rotated: Dict[int, str] = {}
         self._register_tiles: Dict[str, tuple] = {}
         self._aligned_checks: set = set()
+        self._pp_ops: Dict[int, tuple] = {}     # id(op) -> (role, pipe name, extra)
         self._fused_loads: Dict[int, List[Op]] = {}
         self._fused_ids: set = set()
 
@@ -445,6 +447,12 @@ class CDNA4Lowerer:
             b, d, rt, ct = (self._int(c) for c in op.coords)
             w(f"{pad}{self._load_call(op, 'load<WIR_AL>(', ptr, key)});")
             return
+        pp = self._pp_ops.get(id(op))
+        if pp is not None and pp[0] == "skip":
+            return
+        if pp is not None and pp[0] in ("step", "drain"):
+            self._emit_pingpong_mma(op, pp, out, depth)
+            return
         if isinstance(op, (WaitOp, WaitBufOp)):
             if isinstance(op, WaitOp) and all(self.resolve(v.name) in self._register_tiles for v in op.values):
                 return
@@ -557,6 +565,42 @@ class CDNA4Lowerer:
         return (f"wir::Loader<{self.stile(key)}, {self.geo.nw}>::{fn}{ptr}, globals.{_cname(src.name)[2:]}, "
                 f"{b}, {d}, ({rt}) * {sub.rows}, ({ct}) * {sub.cols}, wir_wave")
 
+    def _emit_pingpong_mma(self, op: MMABufOp, pp, out: List[str], depth: int) -> None:
+        pad = "  " * depth
+        role, name, extra = pp
+        a_ptr, _ = self._buf_ptr(op.a_buf, op.a_slot)
+        b_ptr, _ = self._buf_ptr(op.b_buf, op.b_slot)
+        acc = self._var(op.accum)
+        if role == "step":
+            vm, per4, loads = extra
+            calls, total = [], 0
+            for n_ld, ld in enumerate(loads):
+                lptr, lkey = self._buf_ptr(ld.buf, ld.slot)
+                n = self.loads_per_wave(ld.buf.type.tile_type) * self.geo.nw // 4
+                loader = f"wir::Loader<{self.stile(lkey)}, 4>"
+                g = f"globals.{_cname(ld.source.name)[2:]}"
+                sub = ld.source.type.sub_tile_type
+                bb, dd, rt, ct = (self._int(c) for c in ld.coords)
+                self._aligned_checks.add((self.stile(lkey), _cname(ld.source.name)[2:]))
+                out.append(f"{pad}const auto src{n_ld}_ = {loader}::prep<WIR_AL>({g}, {bb}, {dd}, ({rt}) * {sub.rows}, "
+                           f"({ct}) * {sub.cols});")
+                calls.append(f"if (q >= {total} && q < {total + n}) {loader}::issue<WIR_AL>(q - {total}, "
+                             f"{lptr}, {g}, src{n_ld}_, wir_wave & 3);")
+                total += n
+            out.append(f"{pad}{name}.step<{vm}, {total}>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int q) {{")
+            for c in calls:
+                out.append(f"{pad}  {c}")
+            out.append(f"{pad}}});")
+        else:
+            vm, last = extra
+            out.append(f"{pad}{name}.step<{vm}, 0>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int) {{}});")
+            if last:
+                out.append(f"{pad}{name}.finish({acc});")
+        if self._var(op.result) != acc:
+            out.append(f"{pad}{self._var(op.result)} = {acc};")
+        if isinstance(op.a_slot, BufSlotExpr):
+            out.append(f"{pad}wir_drain = (wir_drain + 1) % {op.a_slot.modulus};")
+
     def _emit_yield(self, op: YieldOp, out: List[str], depth: int) -> None:
         pad = "  " * depth
         loop = self._loop_of_yield[id(op)]
@@ -628,6 +672,11 @@ class CDNA4Lowerer:
         if op.tile_size:
             stop = f"(({stop}) + {op.tile_size - 1}) / {op.tile_size}"
         iv = self._var(op.induction_var)
+        if self._setup_pingpong(op, out, depth):
+            out.append(f"{pad}for (int {iv} = {self._int(op.start)}; {iv} < {stop}; {iv} += {self._int(op.step)}) {{")
+            self._emit_ops(op.body, out, depth + 1)
+            out.append(f"{pad}}}")
+            return
         rotated = self._rotatable(op)
         if rotated is not None:
             mma, pipe_t = rotated
@@ -645,12 +694,66 @@ class CDNA4Lowerer:
         if rotated is not None:
             out.append(f"{pad}{self._rotated[id(rotated[0])]}.finish({self._var(rotated[0].accum)});")
 
-    def _rotatable(self, loop: ForOp):
+    def _setup_pingpong(self, loop: ForOp, out: List[str], depth: int) -> bool:
+        """Eight-wavefront ring loops (steady state + drain steps) use the
+        ping-pong form ``wir::PingPongAB``: two wave groups alternate between
+        MFMA-only phases and LDS-read/DMA phases, one phase apart."""
+        if not self.target.pingpong or self.geo.nw != 8:
+            return False
+        rot = self._rotatable(loop, for_pingpong=True)
+        if rot is None:
+            return False
+        mma, _ = rot
+        top = list(self.kernel.body)
+        if loop not in top:
+            return False
+        after = top[top.index(loop) + 1:]
+        drains = []
+        for o in after:
+            if isinstance(o, WaitBufOp) and isinstance(o.slot, BufSlotExpr) and o.slot.value is None:
+                continue
+            if (isinstance(o, MMABufOp) and isinstance(o.a_slot, BufSlotExpr) and o.a_slot.value is None
+                    and o.a_buf == mma.a_buf and o.b_buf == mma.b_buf):
+                drains.append(o)
+                continue
+            break
+        stages = mma.a_buf.type.count
+        if len(drains) != stages - 1:
+            return False
+        loads = [o for o in loop.body if isinstance(o, TMALoadBufOp)]
+        if any(id(o) in self.war_barrier for o in loads):
+            return False
+        per4 = 0
+        for ld in loads:
+            t = ld.buf.type.tile_type
+            instr = t.rows * t.cols * 2 // 16 // 64
+            if instr % 4:
+                return False
+            per4 += instr // 4
+        t = self._rtype(mma.accum)
+        a_key, b_key = self.resolve(mma.a_buf.name), self.resolve(mma.b_buf.name)
+        name = f"pp{len(self._pp_ops)}"
+        pad = "  " * depth
+        out.append(f"{pad}wir::PingPongAB<{self.geo.ms}, {t.rows}, {t.cols}, {self.stile(a_key)}, {self.stile(b_key)}> {name};")
+        out.append(f"{pad}{name}.init(wir_wave);")
+        self._pp_ops[id(loop.body[0])] = ("skip", name, None)
+        for o in loop.body:
+            if isinstance(o, TMALoadBufOp):
+                self._fused_ids.add(id(o))
+        self._pp_ops[id(mma)] = ("step", name, ((stages - 2) * per4, per4, loads))
+        for e, d in enumerate(drains):
+            self._pp_ops[id(d)] = ("drain", name, ((stages - 2 - e) * per4, e == len(drains) - 1))
+        for o in after[:2 * len(drains)]:
+            if isinstance(o, WaitBufOp):
+                self._pp_ops[id(o)] = ("skip", name, None)
+        return True
+
+    def _rotatable(self, loop: ForOp, for_pingpong: bool = False):
         """The steady state of a ring pipeline -- ``wait_buf(slot s)``, loads,
         one ``mma_buf`` on slot ``s`` -- is emitted in rotated form
         (``wir::MMAPipeAB``): the MMA's last k-step is issued after the next
         iteration's wait, so the matrix core is busy across the barrier."""
-        if not self.target.rotate_mma:
+        if not self.target.rotate_mma and not for_pingpong:
             return None
         body = [o for o in loop.body if not isinstance(o, YieldOp)]
         if not body or not isinstance(body[0], WaitBufOp):
@@ -664,7 +767,7 @@ class CDNA4Lowerer:
             return None
         t = self._rtype(mma.accum)
         k = mma.a_buf.type.tile_type.cols
-        if (k // (16 if self.geo.ms == 32 else 32)) % 2:
+        if (k // (16 if self.geo.ms == 32 else 32)) % 2 and not for_pingpong:
             return None
         a_key, b_key = self.resolve(mma.a_buf.name), self.resolve(mma.b_buf.name)
         return mma, (f"wir::MMAPipeAB<{self.geo.ms}, {t.rows}, {t.cols}, {self.stile(a_key)}, "

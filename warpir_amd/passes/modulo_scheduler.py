@@ -67,7 +67,7 @@ REFERENCE_COST_MODEL = CostModel(latency=dict(LATENCY), resources=dict(RESOURCE_
 
 
 
-def gfx950_cost_model(block_m: int, block_n: int, block_k: int) -> CostModel:
+def gfx950_cost_model(block_m: int, block_n: int, block_k: int, load_units: int = 8) -> CostModel:
     """Cost model of one K-step on an MI355X CU, in units of 256 cycles.
 
     The MMA's latency is the block tile's MFMA time spread over the CU's 4
@@ -75,11 +75,13 @@ def gfx950_cost_model(block_m: int, block_n: int, block_k: int) -> CostModel:
     cycles from issue to landing under load (8 units).  For 256x256x32 the
     MMA is 4 units and the optimum is ii=4 with the MMA two stages behind
     its loads (a 3-slot ring); for 256x256x64 it is 8 units, ii=8 and a
-    2-slot ring.
+    2-slot ring.  ``load_units`` raises the load latency for schedules that
+    keep more tiles in flight (12 units: a 4-slot ring at K=32).
     """
     mma_units = max(1, round(2 * block_m * block_n * block_k / (4 * 1024) / 256))
-    return CostModel(latency={TMALoadOp: ("tma", 8), MMAOp: ("tc", mma_units), TMAStoreOp: ("tma", 8)},
-                     resources={"tma": 4, "tc": 1})
+    return CostModel(latency={TMALoadOp: ("tma", load_units), MMAOp: ("tc", mma_units),
+                              TMAStoreOp: ("tma", load_units)},
+                     resources={"tma": 8, "tc": 1})
 
 
 GFX950_COST_MODEL = gfx950_cost_model(256, 256, 32)
