@@ -39,9 +39,17 @@ def _waits(src):
 
 
 def test_pipelined_gemm_waits_keep_one_stage_in_flight():
-    src = CDNA4Lowerer().lower(kernels.kernel("gemm_256_k32"))
+    src = CDNA4Lowerer(CDNA4Target(mve=False)).lower(kernels.kernel("gemm_256_k32"))
     # 256x32 A tile and 32x256 B tile: 16 KiB each = 16 DMA instructions / 4 waves = 4 + 4 per stage
     assert _waits(src) == [8, 8, 0]
+
+
+def test_modulo_variable_expansion_unrolls_by_ring_size():
+    src = CDNA4Lowerer().lower(kernels.kernel("gemm_256_k32"))
+    # 3-slot ring: 3 unrolled copies with constant slots + the run-time remainder loop, then 2 drains
+    assert _waits(src) == [8, 8, 8, 8, 8, 0]
+    loop = src[src.index("int wir_base_i"):]
+    assert "(smem + 0 + 2 * 16384)" in loop and "% 3) * 16384" in loop
     assert "wir::barrier()" not in src  # the ring's waits already order every slot reuse
 
 

@@ -15,10 +15,11 @@ from warpir_amd.workloads import build_attention_kernel, build_gemm_kernel, buil
 
 
 def _gemm_mi355x(block_k: int = 32, block_m: int = 256, block_n: int = 256, wave_m: int = 128,
-                 wave_n: int = 128, load_units: int = 8) -> Kernel:
+                 wave_n: int = 128, load_units: int = 8, lds_budget: int = 160 * 1024) -> Kernel:
     return kernel_pass(build_gemm_kernel(block_m=block_m, block_n=block_n, block_k=block_k, wave_m=wave_m,
                                          wave_n=wave_n, name="gemm"),
-                       cost_model=gfx950_cost_model(block_m, block_n, block_k, load_units=load_units))
+                       cost_model=gfx950_cost_model(block_m, block_n, block_k, load_units=load_units,
+                                                    lds_budget=lds_budget))
 
 
 VARIANTS: Dict[str, Callable[[], Kernel]] = {
@@ -30,7 +31,8 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # Same tile with a 64-deep K step: MMA twice as long per stage, 2-slot ring.
     "gemm_256_k64": lambda: _gemm_mi355x(64),
     # 128x128 block tile (4 wavefronts of 64x64): more workgroups for short M (skinny GEMM).
-    "gemm_128_k64": lambda: _gemm_mi355x(64, block_m=128, block_n=128, wave_m=64, wave_n=64),
+    "gemm_128_k64": lambda: _gemm_mi355x(64, block_m=128, block_n=128, wave_m=64, wave_n=64,
+                                         lds_budget=80 * 1024),
     # 8 wavefronts (2 per SIMD) of 128x64 in the ping-pong form, K=32 with a 4-slot ring.
     "gemm_256_pp": lambda: _gemm_mi355x(32, wave_m=128, wave_n=64, load_units=12),
     # The reference's single-head attention IR (tests/attention_baseline.py:46-186).
@@ -66,15 +68,27 @@ def handle(name: str):
     return _handles[name]
 
 
-def build_all(verbose: bool = False) -> Dict[str, str]:
-    """Lower and compile every variant; returns name -> code-object path."""
+def build_all(verbose: bool = False, prune: bool = True) -> Dict[str, str]:
+    """Lower and compile every variant; returns name -> code-object path.
+
+    With ``prune`` the cache keeps only the files of the current variants.
+    """
+    import os
+
     from warpir_amd.lowering import CDNA4Lowerer
-    from warpir_amd.runtime import compile_source
+    from warpir_amd.runtime import CACHE_DIR, compile_source, resource_usage
 
     out = {}
     for name, make in VARIANTS.items():
         src = CDNA4Lowerer().lower(make())
         out[name] = compile_source(src, force=True)
         if verbose:
-            print(f"built {name}: {out[name]}", flush=True)
+            u = resource_usage(src)
+            print(f"built {name}: {os.path.basename(out[name])} vgpr={u.get('vgpr')} agpr={u.get('agpr')} "
+                  f"spill={u.get('vgpr_spill')} lds={u.get('lds')}", flush=True)
+    if prune and os.path.isdir(CACHE_DIR):
+        keep = {os.path.basename(p)[: -len(".hsaco")] for p in out.values()}
+        for f in os.listdir(CACHE_DIR):
+            if f.split(".")[0] not in keep:
+                os.remove(os.path.join(CACHE_DIR, f))
     return out

@@ -85,6 +85,9 @@ class CDNA4Target:
     group_m: int = 8
     rotate_mma: bool = True
     pingpong: bool = True
+    # Modulo variable expansion: unroll ring loops by their slot count so
+    # every slot index is a compile-time constant.
+    mve: bool = True
 
 
 @dataclass
@@ -181,6 +184,7 @@ class CDNA4Lowerer:
         self._register_tiles: Dict[str, tuple] = {}
         self._aligned_checks: set = set()
         self._pp_ops: Dict[int, tuple] = {}     # id(op) -> (role, pipe name, extra)
+        self._slot_const: Dict[str, int] = {}   # induction var -> its value mod the ring size
         self._fused_loads: Dict[int, List[Op]] = {}
         self._fused_ids: set = set()
 
@@ -368,6 +372,9 @@ class CDNA4Lowerer:
         if slot.value is None:
             return "wir_drain"
         m = slot.modulus
+        name = self.resolve(slot.value.name)
+        if name in self._slot_const:
+            return str((self._slot_const[name] + slot.offset) % m)
         return f"((({self._int(slot.value)}) + {slot.offset % m}) % {m})"
 
     def _tile_ptr(self, v: Value) -> Tuple[str, str]:
@@ -673,9 +680,7 @@ class CDNA4Lowerer:
             stop = f"(({stop}) + {op.tile_size - 1}) / {op.tile_size}"
         iv = self._var(op.induction_var)
         if self._setup_pingpong(op, out, depth):
-            out.append(f"{pad}for (int {iv} = {self._int(op.start)}; {iv} < {stop}; {iv} += {self._int(op.step)}) {{")
-            self._emit_ops(op.body, out, depth + 1)
-            out.append(f"{pad}}}")
+            self._emit_loop(op, stop, out, depth)
             return
         rotated = self._rotatable(op)
         if rotated is not None:
@@ -688,11 +693,51 @@ class CDNA4Lowerer:
                 self._fused_ids |= {id(o) for o in loads}
             out.append(f"{pad}{pipe_t} {name};")
             out.append(f"{pad}{name}.init();")
-        out.append(f"{pad}for (int {iv} = {self._int(op.start)}; {iv} < {stop}; {iv} += {self._int(op.step)}) {{")
-        self._emit_ops(op.body, out, depth + 1)
-        out.append(f"{pad}}}")
+        self._emit_loop(op, stop, out, depth)
         if rotated is not None:
             out.append(f"{pad}{self._rotated[id(rotated[0])]}.finish({self._var(rotated[0].accum)});")
+
+    def _ring_modulus(self, loop: ForOp) -> Optional[int]:
+        """Slot count of the ring slots this loop indexes by its induction variable."""
+        iv = self.resolve(loop.induction_var.name)
+        mods = set()
+        for o in loop.body:
+            for f in vars(o).values():
+                if isinstance(f, BufSlotExpr) and f.value is not None and self.resolve(f.value.name) == iv:
+                    mods.add(f.modulus)
+        if len(mods) != 1:
+            return None
+        return mods.pop()
+
+    def _emit_loop(self, op: ForOp, stop: str, out: List[str], depth: int) -> None:
+        """Emit the loop; ring loops are unrolled by their slot count S
+        (modulo variable expansion) when the start is a constant and the step
+        is 1: copy u of the body sees the constant slot (start + u + offset)
+        % S, so LDS addresses fold into instruction offsets.  A remainder loop
+        with run-time slots finishes the last (trips mod S) iterations."""
+        pad = "  " * depth
+        iv = self._var(op.induction_var)
+        ivn = self.resolve(op.induction_var.name)
+        m = self._ring_modulus(op) if self.target.mve else None
+        if m is None or m < 2 or m > 4 or not isinstance(op.start, int) or op.step != 1:
+            out.append(f"{pad}for (int {iv} = {self._int(op.start)}; {iv} < {stop}; {iv} += {self._int(op.step)}) {{")
+            self._emit_ops(op.body, out, depth + 1)
+            out.append(f"{pad}}}")
+            return
+        base = f"wir_base_{iv[2:]}"
+        out.append(f"{pad}int {base} = {op.start};")
+        out.append(f"{pad}for (; {base} + {m} <= ({stop}); {base} += {m}) {{")
+        for u in range(m):
+            self._slot_const[ivn] = (op.start + u) % m
+            out.append(f"{pad}  {{")
+            out.append(f"{pad}    const int {iv} = {base} + {u};")
+            self._emit_ops(op.body, out, depth + 2)
+            out.append(f"{pad}  }}")
+        del self._slot_const[ivn]
+        out.append(f"{pad}}}")
+        out.append(f"{pad}for (int {iv} = {base}; {iv} < {stop}; {iv} += 1) {{")
+        self._emit_ops(op.body, out, depth + 1)
+        out.append(f"{pad}}}")
 
     def _setup_pingpong(self, loop: ForOp, out: List[str], depth: int) -> bool:
         """Eight-wavefront ring loops (steady state + drain steps) use the

@@ -67,7 +67,8 @@ REFERENCE_COST_MODEL = CostModel(latency=dict(LATENCY), resources=dict(RESOURCE_
 
 
 
-def gfx950_cost_model(block_m: int, block_n: int, block_k: int, load_units: int = 8) -> CostModel:
+def gfx950_cost_model(block_m: int, block_n: int, block_k: int, load_units: int = 8,
+                      lds_budget: int = 160 * 1024) -> CostModel:
     """Cost model of one K-step on an MI355X CU, in units of 256 cycles.
 
     The MMA's latency is the block tile's MFMA time spread over the CU's 4
@@ -76,12 +77,14 @@ def gfx950_cost_model(block_m: int, block_n: int, block_k: int, load_units: int 
     MMA is 4 units and the optimum is ii=4 with the MMA two stages behind
     its loads (a 3-slot ring); for 256x256x64 it is 8 units, ii=8 and a
     2-slot ring.  ``load_units`` raises the load latency for schedules that
-    keep more tiles in flight (12 units: a 4-slot ring at K=32).
+    keep more tiles in flight (12 units: a 4-slot ring at K=32).  The ring
+    depth is capped by ``lds_budget`` bytes per workgroup.
     """
     mma_units = max(1, round(2 * block_m * block_n * block_k / (4 * 1024) / 256))
+    stage_bytes = (block_m + block_n) * block_k * 2
     return CostModel(latency={TMALoadOp: ("tma", load_units), MMAOp: ("tc", mma_units),
                               TMAStoreOp: ("tma", load_units)},
-                     resources={"tma": 8, "tc": 1})
+                     resources={"tma": 8, "tc": 1}, max_stages=max(2, lds_budget // stage_bytes))
 
 
 GFX950_COST_MODEL = gfx950_cost_model(256, 256, 32)
@@ -197,6 +200,15 @@ def _shape_schedule(instructions: List[MSInstruction], offsets: List[int], ii: i
     return prologue, steady_state, epilogue, ii, num_stages, stage_of
 
 
+def _shape_from_stages(names: List[str], stage_of: Dict[str, int], depth: int):
+    """Prologue / steady-state / epilogue lists for given stages (as ``_shape_schedule``)."""
+    num_stages = max(stage_of.values()) + 1
+    prologue = [[(i - stage_of[n], n) for n in names if stage_of[n] <= i] for i in range(num_stages - 1)]
+    steady_state = [[(n, k - stage_of[n]) for n in names] for k in range(num_stages - 1, depth)]
+    epilogue = [[(n, stage_of[n] - i) for n in names if stage_of[n] >= i] for i in range(1, num_stages)]
+    return prologue, steady_state, epilogue, num_stages
+
+
 def _loop_instructions(loop: ForOp, cost: CostModel, transitive: bool = False) -> Dict[str, MSInstruction]:
     """One ``MSInstruction`` per load / MMA / store, keyed by the op's text (``:183-217``)."""
     instrs: Dict[str, MSInstruction] = {}
@@ -270,6 +282,11 @@ def _pipeline_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
         max_cycles=cost.max_cycles, depth=cost.depth, resource_counts=cost.resources)
     if prologue is None:
         return None
+    if cost.max_stages is not None and stages > cost.max_stages:
+        # The LDS budget holds fewer slots than the schedule wants: pull the
+        # late instructions forward to the last stage that fits.
+        stage_of = {n: min(st, cost.max_stages - 1) for n, st in stage_of.items()}
+        prologue, steady, epilogue, stages = _shape_from_stages(list(stage_of), stage_of, cost.depth)
 
     by_name: Dict[str, Op] = {str(op): op for op in loop.body}
     loads = [op for op in loop.body if isinstance(op, TMALoadOp)]
