@@ -50,7 +50,21 @@ def test_modulo_variable_expansion_unrolls_by_ring_size():
     assert _waits(src) == [8, 8, 8, 8, 8, 0]
     loop = src[src.index("int wir_base_i"):]
     assert "(smem + 0 + 2 * 16384)" in loop and "% 3) * 16384" in loop
-    assert "wir::barrier()" not in src  # the ring's waits already order every slot reuse
+    # the ring's waits already order every slot reuse: the only barrier is the one before the staged store
+    assert src.count("wir::barrier()") == 1 and src.index("wir::barrier()") > src.index("pipe0.finish")
+
+
+def test_final_store_is_staged_through_lds():
+    src = CDNA4Lowerer().lower(kernels.kernel("gemm_256_k64"))
+    tail = src[src.index("pipe0.finish"):]
+    assert tail.index("wir::barrier()") < tail.index("store_tile_staged") and "wir::store_tile(" not in tail
+    assert "smem + wir_wave * 32768" in tail        # 128x128 bf16 per wavefront
+    plain = CDNA4Lowerer(CDNA4Target(staged_stores=False)).lower(kernels.kernel("gemm_256_k64"))
+    plain = plain[plain.rindex('extern "C" __global__'):]
+    assert "store_tile_staged" not in plain and "wir::store_tile(" in plain
+    # the attention output is staged; its fp32 LSE column vector is stored directly
+    fa = CDNA4Lowerer().lower(kernels.kernel("mha_d128"))
+    assert "store_tile_staged(globals.O" in fa and "store_vec(globals.L" in fa
 
 
 def test_ssa_gemm_waits_for_everything_and_guards_reuse():

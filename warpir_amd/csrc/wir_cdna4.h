@@ -888,6 +888,58 @@ __device__ __forceinline__ void store_tile(const gl<T>& g, const RTile<MS, R, C>
   }
 }
 
+// Register tile -> bf16 global through this wave's private LDS area `stage`
+// (R * C * 2 bytes, free for the rest of the kernel).  In the lane = row
+// layout one store instruction would touch MS rows with 8 bytes each; the
+// staged form writes the bf16 tile to LDS row-major (16-byte chunks XOR-
+// swizzled by row) and reads it back as whole rows, so each store
+// instruction writes C*2 contiguous bytes per row and 16 bytes per lane.
+template <int MS, int R, int C>
+__device__ __forceinline__ void store_tile_staged(const gl<bf16>& g, const RTile<MS, R, C>& t, int b, int d,
+                                                  int row0, int col0, char* stage) {
+  constexpr int CPR = C / 8;   // 16-byte chunks per row
+  static_assert(C % 8 == 0 && (CPR & (CPR - 1)) == 0, "staged store needs a power-of-two count of 16-byte chunks");
+  constexpr int SW = CPR < 16 ? CPR - 1 : 15;
+  if ((unsigned)b >= (unsigned)g.b || (unsigned)d >= (unsigned)g.d) return;
+  const int lane = lane_id();
+  const int lr = lane % MS, lh = lane / MS;
+  lds_char* s = lds(stage);
+#pragma unroll
+  for (int rb = 0; rb < t.RB; ++rb) {
+    const int row = rb * MS + lr;
+#pragma unroll
+    for (int cb = 0; cb < t.CB; ++cb)
+#pragma unroll
+      for (int q = 0; q < MF<MS>::CREGS / 4; ++q) {
+        const int col = cb * MS + ccol<MS>(4 * q, lh);
+        bf16x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (bf16)t.f[cb][rb][4 * q + j];
+        *(__attribute__((address_space(3))) bf16x4*)(s + row * (C * 2) + (((col >> 3) ^ (row & SW)) << 4) +
+                                                      (col & 7) * 2) = v;
+      }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  bf16* base = g.data + (long long)b * g.sb + (long long)d * g.sd;
+  const bool vec_ok = ((g.sr & 7) == 0) && ((col0 & 7) == 0) && ((((size_t)base) & 15) == 0);
+#pragma unroll
+  for (int it = 0; it < R * CPR / 64; ++it) {
+    const int idx = it * 64 + lane;
+    const int row = idx / CPR, ch = idx % CPR;
+    const bf16x8 v = *(__attribute__((address_space(3))) bf16x8*)(s + row * (C * 2) + ((ch ^ (row & SW)) << 4));
+    const int grow = row0 + row, gcol = col0 + ch * 8;
+    if (grow >= g.r) continue;
+    bf16* p = base + (long long)grow * g.sr + gcol;
+    if (vec_ok && gcol + 8 <= g.c) {
+      *(bf16x8*)p = v;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (gcol + j < g.c) p[j] = v[j];
+    }
+  }
+}
+
 // Column vector -> global column `col0` of rows row0.. (one writer lane per row).
 template <typename T, int MS, int R>
 __device__ __forceinline__ void store_vec(const gl<T>& g, const RVec<MS, R>& v, int b, int d, int row0, int col0) {

@@ -88,6 +88,8 @@ class CDNA4Target:
     # Modulo variable expansion: unroll ring loops by their slot count so
     # every slot index is a compile-time constant.
     mve: bool = True
+    # Final bf16 stores of register tiles go through LDS as whole rows.
+    staged_stores: bool = True
 
 
 @dataclass
@@ -134,6 +136,7 @@ class CDNA4Lowerer:
         self._pending_hoist = self._hoistable()
         self._register_tiles = self._register_only_tiles()
         self._allocate_lds()
+        self._staged = self._staged_stores()
         self.wait_n, self.war_barrier = _schedule(kernel, self)
         body: List[str] = []
         self._emit_ops(kernel.body, body, 1)
@@ -173,6 +176,8 @@ class CDNA4Lowerer:
         self.roles: Dict[str, int] = {}
         self.lds_off: Dict[str, int] = {}
         self.lds_total = 0
+        self._staged: Dict[int, int] = {}
+        self._stage_barrier_done = False
         self.globals: List[Value] = []
         self.drain_modulus: Optional[int] = None
         self._loop_of_yield: Dict[int, ForOp] = {}
@@ -335,6 +340,37 @@ class CDNA4Lowerer:
         self.lds_total = off
         if off > self.target.lds_bytes:
             raise LoweringError(f"LDS use {off} B exceeds the {self.target.lds_bytes} B per workgroup")
+
+    def _staged_stores(self) -> Dict[int, int]:
+        """Stores of fp32 register tiles to bf16 globals that go through LDS.
+
+        Eligible are top-level stores after which no op touches shared
+        memory: the ring buffers are dead, so each wavefront can stage its
+        tile in a private LDS area (id(op) -> bytes per wavefront).  The
+        first staged store is preceded by one workgroup barrier.
+        """
+        if not self.target.staged_stores:
+            return {}
+        lds_ops = (TMALoadOp, TMALoadBufOp, WaitOp, WaitBufOp, MMAOp, MMABufOp, AllocSharedOp, ForOp, SlotViewOp)
+        out: Dict[int, int] = {}
+        body = list(self.kernel.body)
+        for i, op in enumerate(body):
+            if not isinstance(op, TMAStoreOp):
+                continue
+            if any(isinstance(o, lds_ops) for o in body[i:]):
+                continue
+            st = self._rtype(op.source)
+            if not (isinstance(st, RegTileType) and st.data_type == GPUType.fp32
+                    and op.dest.type.data_type == GPUType.bf16):
+                continue
+            cpr = st.cols // 8
+            per_wave = st.rows * st.cols * 2
+            if st.cols % 8 or cpr & (cpr - 1) or (st.rows * cpr) % 64 or per_wave * self.geo.nw > self.target.lds_bytes:
+                continue
+            out[id(op)] = per_wave
+        if out:
+            self.lds_total = max(self.lds_total, max(out.values()) * self.geo.nw)
+        return out
 
     # ------------------------------------------------------------------
     # emission helpers
@@ -655,7 +691,14 @@ class CDNA4Lowerer:
         b, d, rt, ct = (self._int(c) for c in op.coords)
         g = f"globals.{_cname(dest.name)[2:]}"
         st = self._rtype(op.source)
-        if isinstance(st, RegTileType):
+        if isinstance(st, RegTileType) and id(op) in self._staged:
+            if not self._stage_barrier_done:
+                out.append(f"{pad}wir::barrier();  // ring buffers dead: LDS becomes per-wave staging")
+                self._stage_barrier_done = True
+            out.append(f"{pad}wir::store_tile_staged({g}, {self._var(op.source)}, {b}, {d}, "
+                       f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols} + wave_col0, "
+                       f"smem + wir_wave * {self._staged[id(op)]});")
+        elif isinstance(st, RegTileType):
             out.append(f"{pad}wir::store_tile({g}, {self._var(op.source)}, {b}, {d}, "
                        f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols} + wave_col0);")
         elif isinstance(st, ColVecType):
