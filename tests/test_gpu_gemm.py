@@ -34,7 +34,7 @@ def test_reference_ir_square(gpu, variant, n):
     assert err <= TOL, err
 
 
-MI355X_VARIANTS = sorted(v for v in kernels.VARIANTS if v.startswith("gemm_256"))
+MI355X_VARIANTS = sorted(v for v in kernels.VARIANTS if v.startswith(("gemm_256", "gemm_128")))
 
 
 @pytest.mark.parametrize("variant", MI355X_VARIANTS)

@@ -148,3 +148,13 @@ def test_generated_source_compiles_for_gfx950(tmp_path, monkeypatch):
         assert f.read(24) == b"__CLANG_OFFLOAD_BUNDLE__"
     usage = rt.resource_usage(src)
     assert usage.get("scratch", 0) == 0
+
+
+def test_gemm_variant_selection():
+    from warpir_amd import api
+    assert api.gemm_variant(8192, 8192) == "gemm_256_k64"
+    assert api.gemm_variant(4096, 4096) == "gemm_256_k64"      # 256 tiles: one per CU
+    assert api.gemm_variant(2048, 2048) == "gemm_128_k64"      # 64 tiles of 256x256
+    assert api.gemm_variant(128, 8192) == "gemm_128x32_k64"
+    for v in ("gemm_256_k64", "gemm_128_k64", "gemm_128x32_k64"):
+        assert v in kernels.VARIANTS

@@ -16,13 +16,24 @@ from typing import Optional, Tuple
 from warpir_amd import kernels
 
 GEMM_VARIANT = "gemm_256_k64"
-SKINNY_GEMM_VARIANT = "gemm_128_k64"   # M <= 128: four times the workgroups of the 256x256 tile
+SKINNY_GEMM_VARIANT = "gemm_128x32_k64"   # M <= 128: 128x32 tiles, 256 workgroups at N = 8192
+MID_GEMM_VARIANT = "gemm_128_k64"         # fewer 256x256 tiles than CUs: 128x128 tiles
+
+
+def gemm_variant(m: int, n: int) -> str:
+    """Kernel variant for an M x N output on the 256 CUs of one MI355X."""
+    if m <= 128:
+        return SKINNY_GEMM_VARIANT
+    if math.ceil(m / 256) * math.ceil(n / 256) < 256:
+        return MID_GEMM_VARIANT
+    return GEMM_VARIANT
 
 
 def gemm(a, b, out=None, variant: Optional[str] = None):
     """``out[M, N] = a[M, K] @ b[K, N]`` in bf16 with fp32 accumulation.
 
-    The default variant is the 256x256 tile; M <= 128 takes the 128x128 one.
+    The default variant is the 256x256 tile; outputs with fewer 256x256
+    tiles than CUs take 128x128 tiles and M <= 128 takes 128x32 tiles.
     """
     import torch
 
@@ -35,7 +46,7 @@ def gemm(a, b, out=None, variant: Optional[str] = None):
     if out is None:
         out = torch.empty(m, n, dtype=torch.bfloat16, device=a.device)
     if variant is None:
-        variant = SKINNY_GEMM_VARIANT if m <= 128 else GEMM_VARIANT
+        variant = gemm_variant(m, n)
     kernels.handle(variant)(A=a, B=b, N=k, C_global=out)
     return out
 
@@ -78,4 +89,4 @@ def _loops(kernel):
     return (op for op in kernel.body if isinstance(op, ForOp))
 
 
-__all__ = ["gemm", "attention_forward", "attention_flops"]
+__all__ = ["gemm", "gemm_variant", "attention_forward", "attention_flops"]

@@ -33,6 +33,12 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # 128x128 block tile (4 wavefronts of 64x64): more workgroups for short M (skinny GEMM).
     "gemm_128_k64": lambda: _gemm_mi355x(64, block_m=128, block_n=128, wave_m=64, wave_n=64,
                                          lds_budget=80 * 1024),
+    # Narrow-N tiles for short M (skinny GEMM): 128 and 256 workgroups at M=128, N=8192,
+    # two workgroups per CU (LDS <= 80 KiB).
+    "gemm_128x64_k64": lambda: _gemm_mi355x(64, block_m=128, block_n=64, wave_m=64, wave_n=32,
+                                            lds_budget=80 * 1024),
+    "gemm_128x32_k64": lambda: _gemm_mi355x(64, block_m=128, block_n=32, wave_m=32, wave_n=32,
+                                            lds_budget=80 * 1024),
     # 8 wavefronts (2 per SIMD) of 128x64 in the ping-pong form, K=32 with a 4-slot ring.
     "gemm_256_pp": lambda: _gemm_mi355x(32, wave_m=128, wave_n=64, load_units=12),
     # The reference's single-head attention IR (tests/attention_baseline.py:46-186).
@@ -41,6 +47,8 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # waited every KV step) and the pipelined prefetch form of kernel_pass.
     "mha_d128_ssa": lambda: build_mha_forward_kernel(d=128, block_q=128, block_kv=64, wave_rows=32),
     "mha_d128": lambda: _mha(128, 128, 64, 32, causal=False),
+    # 256 query rows per workgroup (8 wavefronts): each K/V tile in LDS serves twice the rows.
+    "mha_d128_q256": lambda: _mha(128, 256, 64, 32, causal=False),
     "mha_d64_causal_ssa": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
                                                            causal=True, name="mha_fwd_causal"),
     "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True),
