@@ -61,6 +61,11 @@ class CostModel:
     depth: int = DEPTH
     # Upper bound on ring slots (the LDS budget); None = no bound.
     max_stages: Optional[int] = None
+    # Prefetch form only: issue the next tiles' loads after the first MMA of
+    # the body instead of before it.  Issuing a wave's LDS-DMA instructions
+    # can stall that wave for tens of cycles each; after the MMA they fall in
+    # the shadow of its MFMAs, whose results the next op waits for anyway.
+    loads_after_first_mma: bool = False
 
 
 REFERENCE_COST_MODEL = CostModel(latency=dict(LATENCY), resources=dict(RESOURCE_COUNTS))
@@ -101,7 +106,8 @@ def gfx950_attention_cost_model(block_q: int, block_kv: int, d: int, lds_budget:
     mma_units = max(1, round(2 * block_q * block_kv * d / (4 * 1024) / 256))
     stage_bytes = 2 * block_kv * d * 2
     return CostModel(latency={TMALoadOp: ("tma", 8), MMAOp: ("tc", mma_units), TMAStoreOp: ("tma", 8)},
-                     resources={"tma": 4, "tc": 1}, max_stages=max(2, lds_budget // stage_bytes))
+                     resources={"tma": 4, "tc": 1}, max_stages=max(2, lds_budget // stage_bytes),
+                     loads_after_first_mma=True)
 
 
 @dataclass
@@ -390,9 +396,13 @@ def _prefetch_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
     nxt = Value(f"{iv.name}_pf", iv.type)
     body: List[Op] = [WaitBufOp(bufs=all_rings, slot=BufSlotExpr(value=iv, offset=0, modulus=stages)),
                       IntAffineOp(result=nxt, input=iv, mul=1, add=stages - 1)]
-    for ld in loads:
-        body.append(TMALoadBufOp(buf=ring[ld.result], slot=BufSlotExpr(value=iv, offset=stages - 1, modulus=stages),
-                                 source=ld.source, coords=ld.substitute({iv: nxt}).coords))
+    # The prefetches write slot (i + S - 1) % S, which no op of iteration i
+    # reads, so they may go anywhere in the body.
+    prefetch = [TMALoadBufOp(buf=ring[ld.result], slot=BufSlotExpr(value=iv, offset=stages - 1, modulus=stages),
+                             source=ld.source, coords=ld.substitute({iv: nxt}).coords) for ld in loads]
+    if not cost.loads_after_first_mma:
+        body.extend(prefetch)
+        prefetch = []
     for ld in loads:
         body.append(SlotViewOp(result=ld.result, buf=ring[ld.result],
                                slot=BufSlotExpr(value=iv, offset=0, modulus=stages)))
@@ -406,6 +416,10 @@ def _prefetch_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
                 body.append(WaitOp(values=rest))
             continue
         body.append(op)
+        if isinstance(op, MMAOp) and prefetch:
+            body.extend(prefetch)
+            prefetch = []
+    body.extend(prefetch)
     out.append(ForOp(induction_var=iv, start=loop.start, stop=loop.stop, step=loop.step,
                      iter_args=loop.iter_args, body=tuple(body), results=loop.results,
                      tile_size=loop.tile_size))
