@@ -49,16 +49,20 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_d128": lambda: _mha(128, 128, 64, 32, causal=False),
     # 256 query rows per workgroup (8 wavefronts): each K/V tile in LDS serves twice the rows.
     "mha_d128_q256": lambda: _mha(128, 256, 64, 32, causal=False),
+    # The same with a 3-slot K/V ring, lowered in 8-wavefront ping-pong form.
+    "mha_d128_pp": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=96 * 1024, min_stages=3),
     "mha_d64_causal_ssa": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
                                                            causal=True, name="mha_fwd_causal"),
     "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True),
 }
 
 
-def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool) -> Kernel:
+def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_budget: int = 64 * 1024,
+         min_stages: int = 2) -> Kernel:
     k = build_mha_forward_kernel(d=d, block_q=block_q, block_kv=block_kv, wave_rows=wave_rows, causal=causal,
                                  name="mha_fwd_causal" if causal else "mha_fwd")
-    return kernel_pass(k, cost_model=gfx950_attention_cost_model(block_q, block_kv, d))
+    return kernel_pass(k, cost_model=gfx950_attention_cost_model(block_q, block_kv, d, lds_budget=lds_budget,
+                                                                 min_stages=min_stages))
 
 _handles: Dict[str, object] = {}
 

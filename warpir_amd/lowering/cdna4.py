@@ -190,6 +190,7 @@ class CDNA4Lowerer:
         self._aligned_checks: set = set()
         self._pp_ops: Dict[int, tuple] = {}     # id(op) -> (role, pipe name, extra)
         self._slot_const: Dict[str, int] = {}   # induction var -> its value mod the ring size
+        self._slot_shift: Dict[str, int] = {}   # induction var -> offset added to its ring slots
         self._fused_loads: Dict[int, List[Op]] = {}
         self._fused_ids: set = set()
 
@@ -409,9 +410,10 @@ class CDNA4Lowerer:
             return "wir_drain"
         m = slot.modulus
         name = self.resolve(slot.value.name)
+        off = slot.offset + self._slot_shift.get(name, 0)
         if name in self._slot_const:
-            return str((self._slot_const[name] + slot.offset) % m)
-        return f"((({self._int(slot.value)}) + {slot.offset % m}) % {m})"
+            return str((self._slot_const[name] + off) % m)
+        return f"((({self._int(slot.value)}) + {off % m}) % {m})"
 
     def _tile_ptr(self, v: Value) -> Tuple[str, str]:
         """(LDS pointer expression, LDS key) of a shared tile or slot view."""
@@ -722,6 +724,8 @@ class CDNA4Lowerer:
         if op.tile_size:
             stop = f"(({stop}) + {op.tile_size - 1}) / {op.tile_size}"
         iv = self._var(op.induction_var)
+        if self._emit_attention_pingpong(op, stop, out, depth):
+            return
         if self._setup_pingpong(op, out, depth):
             self._emit_loop(op, stop, out, depth)
             return
@@ -781,6 +785,146 @@ class CDNA4Lowerer:
         out.append(f"{pad}for (int {iv} = {base}; {iv} < {stop}; {iv} += 1) {{")
         self._emit_ops(op.body, out, depth + 1)
         out.append(f"{pad}}}")
+
+    def _attention_pingpong_plan(self, loop: ForOp):
+        """Match the prefetch-form attention loop that the ping-pong emitter
+        takes: wait on slot i, the slot views, a first MMA with B^T from
+        ring K, VALU ops, a last MMA (bf16 register A, B from ring V) whose
+        result is carried in place, and one prefetch load per ring into slot
+        i + S - 1 with S >= 3."""
+        if not self.target.pingpong or self.geo.nw != 8 or loop not in list(self.kernel.body):
+            return None
+        body = list(loop.body)
+        if not body or not isinstance(body[0], WaitBufOp) or not isinstance(body[-1], YieldOp):
+            return None
+        mmas = [o for o in body if isinstance(o, MMAOp)]
+        if len(mmas) != 2 or not mmas[0].transpose_b or mmas[1].transpose_b or body[-2] is not mmas[1]:
+            return None
+        qk, pv = mmas
+        views = self._views()
+        vk, vv = views.get(self.resolve(qk.b.name)), views.get(self.resolve(pv.b.name))
+        if vk is None or vv is None or vk.buf == vv.buf:
+            return None
+        loads = [o for o in body if isinstance(o, TMALoadBufOp)]
+        if sorted(self.resolve(o.buf.name) for o in loads) != sorted(
+                [self.resolve(vk.buf.name), self.resolve(vv.buf.name)]):
+            return None
+        ivn = self.resolve(loop.induction_var.name)
+        mods = {o.slot.modulus for o in loads} | {vk.slot.modulus, vv.slot.modulus, body[0].slot.modulus}
+        if len(mods) != 1:
+            return None
+        S = mods.pop()
+        if S < 3 or not isinstance(loop.start, int) or loop.step != 1:
+            return None
+        for o in loads:
+            if not (isinstance(o.slot, BufSlotExpr) and o.slot.value is not None
+                    and self.resolve(o.slot.value.name) == ivn and o.slot.offset % S == S - 1):
+                return None
+            t = o.buf.type.tile_type
+            if (t.rows * t.cols * 2 // 1024) % 4:
+                return None
+        for v in (vk, vv):
+            if self.resolve(v.slot.value.name) != ivn or v.slot.offset % S:
+                return None
+        affine = [o for o in body if isinstance(o, IntAffineOp)]
+        if len(affine) != 1 or affine[0].mul != 1 or affine[0].add != S - 1:
+            return None
+        mid = body[body.index(qk) + 1: body.index(pv)]
+        lds_ops = (TMALoadOp, WaitOp, WaitBufOp, MMAOp, MMABufOp, SlotViewOp, ForOp)
+        if any(isinstance(o, lds_ops) for o in mid):
+            return None
+        yld = body[-1]
+        k = list(yld.values).index(pv.result) if pv.result in yld.values else -1
+        if k < 0 or self._var(loop.iter_args[k].block_arg) != self._var(pv.result):
+            return None
+        softmax = [o for o in mid if not isinstance(o, (TMALoadBufOp, IntAffineOp))]
+        k_load = next(o for o in loads if o.buf == vk.buf)
+        v_load = next(o for o in loads if o.buf == vv.buf)
+        return dict(S=S, qk=qk, pv=pv, softmax=softmax, k_load=k_load, v_load=v_load, affine=affine[0],
+                    yld=yld)
+
+    def _emit_attention_pingpong(self, loop: ForOp, stop: str, out: List[str], depth: int) -> bool:
+        """Eight-wavefront attention in ping-pong form.
+
+        Wave groups 0 (waves 0-3) and 1 (waves 4-7) share the SIMDs pairwise
+        and run one phase apart, so one group's MFMA phase overlaps the other
+        group's softmax (VALU) phase.  Iteration i of a group is
+          M(i): O += P_{i-1} V_{i-1} (the PV MMA of the previous iteration,
+                rotated), the DMAs of tile i + S - 2, then S_i = Q K_i^T;
+          V(i): the online-softmax ops of iteration i (P_i, rescaled O).
+        Every phase starts at a workgroup barrier.  Group 0 loads the K
+        tiles and group 1 the V tiles (4 waves each); a ring of S >= 3
+        slots keeps V_{i-1} resident while tile i + S - 2 is written.
+        """
+        plan = self._attention_pingpong_plan(loop)
+        if plan is None:
+            return False
+        pad = "  " * depth
+        p1 = pad + "  "
+        S, qk, pv = plan["S"], plan["qk"], plan["pv"]
+        iv = self._var(loop.induction_var)
+        ivn = self.resolve(loop.induction_var.name)
+        start = loop.start
+
+        def dma(ld, grp: int) -> List[str]:
+            t = ld.buf.type.tile_type
+            per = t.rows * t.cols * 2 // 1024 // 4
+            ptr, key = self._buf_ptr(ld.buf, ld.slot)
+            src = ld.source
+            sub = src.type.sub_tile_type
+            b, d, rt, ct = (self._int(c) for c in ld.coords)
+            self._aligned_checks.add((self.stile(key), _cname(src.name)[2:]))
+            return [f"{p1}  if (wir_grp == {grp}) wir::Loader<{self.stile(key)}, 4>::load<WIR_AL>({ptr}, "
+                    f"globals.{_cname(src.name)[2:]}, {b}, {d}, ({rt}) * {sub.rows}, ({ct}) * {sub.cols}, wir_gw);"], per
+
+        def emit_pv(dst: List[str], d: int) -> None:
+            self._slot_shift[ivn] = -1
+            self._emit_op(pv, dst, d)
+            del self._slot_shift[ivn]
+
+        # Tensors that are not tile-aligned take the plain loop (per-lane
+        # bounds-checked loads need more registers than the ping-pong leaves).
+        out.append(f"{pad}if constexpr (!WIR_AL) {{")
+        self._emit_loop(loop, stop, out, depth + 1)
+        out.append(f"{pad}}} else {{")
+        pad, p1, depth = pad + "  ", p1 + "  ", depth + 1
+        out.append(f"{pad}const int wir_grp = wir_wave >> 2, wir_gw = wir_wave & 3;")
+        out.append(f"{pad}asm volatile(\"s_waitcnt vmcnt(0) lgkmcnt(0)\" ::: \"memory\");")
+        out.append(f"{pad}wir::barrier();")
+        out.append(f"{pad}if (wir_grp == 1) wir::barrier();  // group 1 runs one phase behind")
+        out.append(f"{pad}for (int {iv} = {start}; {iv} < {stop}; ++{iv}) {{")
+        # M phase
+        out.append(f"{p1}if (wir_grp == 0) asm volatile(\"s_waitcnt vmcnt(0)\" ::: \"memory\");")
+        out.append(f"{p1}wir::barrier();")
+        # PV of the previous iteration first: its P and V operands die before
+        # S = Q K^T is allocated, which keeps the phase within 256 VGPRs.
+        out.append(f"{p1}if ({iv} > {start}) {{")
+        emit_pv(out, depth + 2)
+        aff = plan["affine"]
+        out.append(f"{p1}  const int {self._var(aff.result)} = ({iv}) + {S - 2};")
+        self._slot_shift[ivn] = -1
+        k_lines, k_per = dma(plan["k_load"], 0)
+        v_lines, v_per = dma(plan["v_load"], 1)
+        del self._slot_shift[ivn]
+        out.extend(k_lines + v_lines)
+        out.append(f"{p1}}}")
+        out.append(f"{p1}__builtin_amdgcn_sched_barrier(0);")
+        self._emit_op(qk, out, depth + 1)
+        # V phase
+        out.append(f"{p1}if (wir_grp == 1) asm volatile(\"s_waitcnt vmcnt({v_per})\" ::: \"memory\");")
+        out.append(f"{p1}wir::barrier();")
+        self._emit_ops(plan["softmax"], out, depth + 1)
+        self._emit_op(plan["yld"], out, depth + 1)
+        out.append(f"{pad}}}")
+        # final M phase: the last PV, then group 0 matches group 1's extra barrier
+        out.append(f"{pad}wir::barrier();")
+        out.append(f"{pad}if (({stop}) > {start}) {{")
+        out.append(f"{p1}const int {iv} = ({stop});")
+        emit_pv(out, depth + 1)
+        out.append(f"{pad}}}")
+        out.append(f"{pad}if (wir_grp == 0) wir::barrier();")
+        out.append(f"{pad[:-2]}}}")
+        return True
 
     def _setup_pingpong(self, loop: ForOp, out: List[str], depth: int) -> bool:
         """Eight-wavefront ring loops (steady state + drain steps) use the

@@ -61,6 +61,9 @@ class CostModel:
     depth: int = DEPTH
     # Upper bound on ring slots (the LDS budget); None = no bound.
     max_stages: Optional[int] = None
+    # Lower bound on ring slots of the prefetch form (a lowering that keeps
+    # a tile resident one iteration longer asks for 3).
+    min_stages: int = 2
     # Prefetch form only: issue the next tiles' loads after the first MMA of
     # the body instead of before it.  Issuing a wave's LDS-DMA instructions
     # can stall that wave for tens of cycles each; after the MMA they fall in
@@ -95,19 +98,22 @@ def gfx950_cost_model(block_m: int, block_n: int, block_k: int, load_units: int 
 GFX950_COST_MODEL = gfx950_cost_model(256, 256, 32)
 
 
-def gfx950_attention_cost_model(block_q: int, block_kv: int, d: int, lds_budget: int = 64 * 1024) -> CostModel:
+def gfx950_attention_cost_model(block_q: int, block_kv: int, d: int, lds_budget: int = 64 * 1024,
+                                min_stages: int = 2) -> CostModel:
     """Cost model of one FlashAttention KV step on an MI355X CU.
 
     Each of the two MMAs (S = Q K^T and O += P V) is ``2*block_q*block_kv*d``
     flops; loads take ~8 units as for GEMM.  The ring depth is capped by an
     LDS budget per workgroup (64 KiB by default, so two workgroups share a
-    CU and one's softmax overlaps the other's MFMAs).
+    CU and one's softmax overlaps the other's MFMAs).  ``min_stages`` = 3
+    suits the 8-wavefront ping-pong lowering, which reads each V tile one
+    iteration after its K tile.
     """
     mma_units = max(1, round(2 * block_q * block_kv * d / (4 * 1024) / 256))
     stage_bytes = 2 * block_kv * d * 2
     return CostModel(latency={TMALoadOp: ("tma", 8), MMAOp: ("tc", mma_units), TMAStoreOp: ("tma", 8)},
                      resources={"tma": 4, "tc": 1}, max_stages=max(2, lds_budget // stage_bytes),
-                     loads_after_first_mma=True)
+                     min_stages=min_stages, loads_after_first_mma=True)
 
 
 @dataclass
@@ -378,7 +384,7 @@ def _prefetch_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
     mmas = [op for op in loop.body if isinstance(op, MMAOp)]
     if not mmas:
         raise PipelineError("loop has no MMA to pipeline")
-    stages = max(2, stages)
+    stages = max(cost.min_stages, stages)
     if cost.max_stages is not None:
         stages = max(2, min(stages, cost.max_stages))
     if not isinstance(loop.start, int):
