@@ -495,17 +495,6 @@ struct MMAPipeAB {
         acc.f[cb][rb] = MF<MS>::mma(cat(aop[buf][cb][0], aop[buf][cb][1]), bop[buf][rb], acc.f[cb][rb]);
   }
 
-  static __device__ __forceinline__ void interleave() {
-    constexpr int PAIRS = NREAD < NMMA ? NREAD : NMMA;
-#pragma unroll
-    for (int q = 0; q < PAIRS; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    if (NMMA > PAIRS) __builtin_amdgcn_sched_group_barrier(0x008, NMMA - PAIRS, 0);
-    if (NREAD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NREAD - PAIRS, 0);
-  }
-
   // Read item q (0 <= q < NREAD) of k-step ks into buffer buf: the RB row
   // operands first, then the 2*CB transposed half-operands.
   __device__ __forceinline__ void read_item(char* a_base, int a_row0, char* b_base, int b_col0, int ks, int buf,
@@ -523,35 +512,48 @@ struct MMAPipeAB {
   }
 
   // One steady-state step.  The previous tile's pending k-step MFMAs are
-  // issued first, one per slot, each followed by one of this iteration's
-  // NLOAD DMA instructions (`loads(q)`) and one LDS read of this tile's
-  // first k-step; then k-steps 0..KS-2 with the next k-step's reads
-  // interleaved.  sched_barrier fences pin the order.
+  // issued first, each followed by one LDS read of this tile's first
+  // k-step; then k-steps 0..KS-2, each MFMA followed by one read of the
+  // next k-step.  The NLOAD DMA instructions of this iteration (`loads(q)`)
+  // go after every EVERY-th MFMA from the start, i.e. spread over the first
+  // half of the tile's MFMAs: bunched DMA issue stalls the issuing wave
+  // (measured: 2764 -> 2416 cycles per 256x256x64 step with one DMA every
+  // second MFMA), and issuing them later leaves too little time for them to
+  // land before the next barrier.  sched_barrier fences pin the order.
   template <int NLOAD, class LoadFn>
   __device__ __forceinline__ void run(RTile<MS, R, C>& acc, char* a_base, int a_row0, char* b_base, int b_col0,
                                       LoadFn loads) {
     constexpr int PEND = (KS - 1) & 1;
+    constexpr int HALF = (NMMA * KS) / 2;
+    constexpr int EVERY = NLOAD > 0 && HALF / NLOAD > 1 ? HALF / NLOAD : 1;
+    int nl = 0;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < NMMA; ++q) {
       const int cb = q / RB, rb = q % RB;
       acc.f[cb][rb] = MF<MS>::mma(cat(aop[PEND][cb][0], aop[PEND][cb][1]), bop[PEND][rb], acc.f[cb][rb]);
       __builtin_amdgcn_sched_barrier(0);
-      if (q < NLOAD) loads(q);
+      if (q % EVERY == 0 && nl < NLOAD) loads(nl++);
       if (q < NREAD) read_item(a_base, a_row0, b_base, b_col0, 0, 0, q);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int q = NMMA; q < NLOAD; ++q) loads(q);
-#pragma unroll
     for (int q = NMMA; q < NREAD; ++q) read_item(a_base, a_row0, b_base, b_col0, 0, 0, q);
 #pragma unroll
     for (int ks = 0; ks + 1 < KS; ++ks) {
-      __builtin_amdgcn_sched_barrier(0);
-      read(a_base, a_row0, b_base, b_col0, ks + 1, (ks + 1) & 1);
-      mfmas(acc, ks & 1);
-      interleave();
+#pragma unroll
+      for (int q = 0; q < NMMA; ++q) {
+        const int cb = q / RB, rb = q % RB;
+        acc.f[cb][rb] = MF<MS>::mma(cat(aop[ks & 1][cb][0], aop[ks & 1][cb][1]), bop[ks & 1][rb], acc.f[cb][rb]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (q % EVERY == 0 && nl < NLOAD) loads(nl++);
+        if (q < NREAD) read_item(a_base, a_row0, b_base, b_col0, ks + 1, (ks + 1) & 1, q);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int q = NMMA; q < NREAD; ++q) read_item(a_base, a_row0, b_base, b_col0, ks + 1, (ks + 1) & 1, q);
     }
+    while (nl < NLOAD) loads(nl++);
     __builtin_amdgcn_sched_barrier(0);
   }
 
