@@ -206,6 +206,63 @@ def bench_extra(steps: int, warmup: int):
     return out
 
 
+def mfma_ceiling(iters: int = 20000):
+    """Sustained whole-chip bf16 MFMA rate with no memory traffic, and its clock.
+
+    Runs ``warpir_amd/mfma_ceiling.hsaco`` (one workgroup of 4 wavefronts
+    per CU, 16 independent 32x32x16 MFMAs per loop trip) with random and
+    with constant operands; the shader clock comes from the kernel's own
+    s_memtime / s_memrealtime deltas.  MI355X's clock is power-limited, so
+    this is the MFMA roof that a kernel on random bf16 data can approach.
+    """
+    import ctypes
+
+    import torch
+
+    from warpir_amd.runtime import Event, check, library
+
+    path = os.path.join(ROOT, "warpir_amd", "mfma_ceiling.hsaco")
+    if not os.path.exists(path):
+        return None
+    lib = library()
+    image = open(path, "rb").read()
+    mod, fn = ctypes.c_void_p(), ctypes.c_void_p()
+    check(lib.wir_module_load(image, len(image), ctypes.byref(mod)), "wir_module_load(mfma_ceiling)")
+    check(lib.wir_module_get_function(mod, b"wir_mfma_ceiling", ctypes.byref(fn)), "wir_mfma_ceiling")
+
+    class Args(ctypes.Structure):
+        _fields_ = [("sink", ctypes.c_void_p), ("clocks", ctypes.c_void_p), ("iters", ctypes.c_int),
+                    ("mode", ctypes.c_int)]
+
+    blocks = info_cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(256, dtype=torch.float32, device="cuda")
+    clocks = torch.zeros(2 * 4 * blocks, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    for mode, name in ((0, "random_operands"), (1, "constant_operands")):
+        def launch(n):
+            args = Args(sink.data_ptr(), clocks.data_ptr(), n, mode)
+            check(lib.wir_launch(fn, blocks, 1, 1, 256, 1, 1, 0, ctypes.c_void_p(stream), ctypes.byref(args),
+                                 ctypes.sizeof(args)), "wir_launch(mfma_ceiling)")
+        launch(200)
+        torch.cuda.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        launch(iters)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_ms(e1)
+        c = clocks.view(-1, 2).double().cpu()
+        ghz = float((c[:, 0] / (c[:, 1] / 100e6)).median()) / 1e9
+        flops = 2.0 * 32 * 32 * 16 * 16 * iters * 4 * info_cus
+        out[name] = {"tflops": flops / (ms * 1e-3) / 1e12, "clock_ghz": ghz,
+                     "cycles_per_mfma": float((c[:, 0] / (16.0 * iters)).median())}
+    lib.wir_module_unload(mod)
+    out["note"] = ("MFMA-only kernel, no memory traffic, one workgroup of 4 wavefronts per CU; "
+                   "the clock is the kernel's own s_memtime rate")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -238,6 +295,10 @@ def main() -> int:
     if args.only in (None, "fa"):
         print("[bench] fa-fwd B16 H16 S4096 D128", file=sys.stderr, flush=True)
         fa = bench_fa(args.steps, args.warmup, not args.no_cpu)
+    ceiling = None
+    if args.only is None:
+        print("[bench] mfma ceiling probe", file=sys.stderr, flush=True)
+        ceiling = mfma_ceiling()
     extra = None
     if args.only is None and not args.no_extra:
         print("[bench] other configurations", file=sys.stderr, flush=True)
@@ -264,6 +325,8 @@ def main() -> int:
         line["fa_fwd"] = fa
     if extra is not None:
         line["other_configs"] = extra
+    if ceiling is not None:
+        line["mfma_ceiling"] = ceiling
     line["device"] = info
     print(json.dumps(line))
     return 0
