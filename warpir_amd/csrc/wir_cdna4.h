@@ -646,20 +646,38 @@ struct PingPongAB {
 };
 
 // acc = a @ b^T with `a` from hoisted register fragments or LDS; b: ROWREAD LDS [.][K].
+// The LDS reads of b run LOOK k-steps ahead of the MFMAs that use them
+// (explicit ring of fragment registers, order pinned by sched_barrier):
+// left to itself the compiler issues each read right before its MFMA at
+// two wavefronts per SIMD, exposing the LDS latency once per k-step.
 template <int MS, int R, int C, class TB, int KS>
 __device__ __forceinline__ void mma_ABt_frags(RTile<MS, R, C>& acc, const RowFrags<MS, R / MS, KS>& a,
                                               char* b_base, int b_row0) {
   static_assert(TB::COLS == KS * MF<MS>::KSTEP, "inner dimensions differ");
+  constexpr int CB = RTile<MS, R, C>::CB, RB = RTile<MS, R, C>::RB;
+  constexpr int LOOK = KS < 2 ? KS : 2;
+  bf16x8 ring[LOOK + 1][CB];
   __builtin_amdgcn_s_setprio(1);  // MFMA run first; a co-resident wave's VALU fills the gaps
-  fill(acc, 0.f);
+#pragma unroll
+  for (int p = 0; p < LOOK; ++p)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) ring[p][cb] = row_operand<TB, MS>(b_base, b_row0 + cb * MS, p);
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
+    if (ks + LOOK < KS) {
 #pragma unroll
-    for (int cb = 0; cb < acc.CB; ++cb) {
-      const bf16x8 aop = row_operand<TB, MS>(b_base, b_row0 + cb * MS, ks);
-#pragma unroll
-      for (int rb = 0; rb < acc.RB; ++rb) acc.f[cb][rb] = MF<MS>::mma(aop, a.f[rb][ks], acc.f[cb][rb]);
+      for (int cb = 0; cb < CB; ++cb)
+        ring[(ks + LOOK) % (LOOK + 1)][cb] = row_operand<TB, MS>(b_base, b_row0 + cb * MS, ks + LOOK);
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const typename MF<MS>::cvec c0 = ks == 0 ? typename MF<MS>::cvec{} : acc.f[cb][rb];
+        acc.f[cb][rb] = MF<MS>::mma(ring[ks % (LOOK + 1)][cb], a.f[rb][ks], c0);
+      }
+    __builtin_amdgcn_sched_barrier(0);
   }
   __builtin_amdgcn_s_setprio(0);
 }
@@ -687,7 +705,8 @@ __device__ __forceinline__ void mma_ABt(RTile<MS, R, C>& acc, char* a_base, int 
 // acc += a @ b with `a` a bf16 register tile (lane = row, k along its
 // columns) and b: TRREAD LDS [K][.].  The k order inside each MFMA follows
 // the register layout of `a`: its 4-register group g of column block kb
-// covers k = kb*MS + g*4*LG + 4*lh + (0..3).
+// covers k = kb*MS + g*4*LG + 4*lh + (0..3).  The transposed LDS reads of b
+// run LOOK MFMAs ahead of their use (see mma_ABt_frags).
 template <int MS, int R, int K, int C, class TB>
 __device__ __forceinline__ void mma_rAB(RTile<MS, R, C>& acc, const BTile<MS, R, K>& a, char* b_base,
                                         int b_col0) {
@@ -695,23 +714,34 @@ __device__ __forceinline__ void mma_rAB(RTile<MS, R, C>& acc, const BTile<MS, R,
   constexpr int G = BTile<MS, R, K>::G;      // 4-register groups per C fragment
   constexpr int NG = (K / MS) * G;            // groups along k
   static_assert(NG % 2 == 0, "k extent must fill whole MFMAs");
+  constexpr int CB = RTile<MS, R, C>::CB, RB = RTile<MS, R, C>::RB;
+  constexpr int ITEMS = (NG / 2) * CB;        // one B operand (two half reads) per item
+  constexpr int LOOK = ITEMS < 4 ? ITEMS : 4;
   const int lane = lane_id();
   const int lh = lane / MS;
   const int ngrp = (lane % MS) & ~15;
-  __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-  for (int q = 0; q < NG; q += 2) {
+  auto read = [&](int t) {
+    const int q = 2 * (t / CB), cb = t % CB;
     const int kb0 = q / G, g0 = q % G, kb1 = (q + 1) / G, g1 = (q + 1) % G;
     const int k0 = kb0 * MS + g0 * 4 * MF<MS>::LG + 4 * lh;
     const int k1 = kb1 * MS + g1 * 4 * MF<MS>::LG + 4 * lh;
+    const int n0 = b_col0 + cb * MS + ngrp;
+    return cat(tr_operand4<TB>(b_base, k0, n0), tr_operand4<TB>(b_base, k1, n0));
+  };
+  bf16x8 ring[LOOK + 1];
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int cb = 0; cb < acc.CB; ++cb) {
-      const int n0 = b_col0 + cb * MS + ngrp;
-      const bf16x8 aop = cat(tr_operand4<TB>(b_base, k0, n0), tr_operand4<TB>(b_base, k1, n0));
+  for (int p = 0; p < LOOK; ++p) ring[p] = read(p);
 #pragma unroll
-      for (int rb = 0; rb < acc.RB; ++rb)
-        acc.f[cb][rb] = MF<MS>::mma(aop, cat(a.f[kb0][rb][g0], a.f[kb1][rb][g1]), acc.f[cb][rb]);
-    }
+  for (int t = 0; t < ITEMS; ++t) {
+    if (t + LOOK < ITEMS) ring[(t + LOOK) % (LOOK + 1)] = read(t + LOOK);
+    __builtin_amdgcn_sched_barrier(0);
+    const int q = 2 * (t / CB), cb = t % CB;
+    const int kb0 = q / G, g0 = q % G, kb1 = (q + 1) / G, g1 = (q + 1) % G;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      acc.f[cb][rb] = MF<MS>::mma(ring[t % (LOOK + 1)], cat(a.f[kb0][rb][g0], a.f[kb1][rb][g1]), acc.f[cb][rb]);
+    __builtin_amdgcn_sched_barrier(0);
   }
   __builtin_amdgcn_s_setprio(0);
 }
