@@ -183,7 +183,7 @@ def bench_extra(steps: int, warmup: int):
         a = seeded_normal((m, k), 5, 0.1).cuda()
         b = seeded_normal((k, n), 6, 0.1).cuda()
         c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-        variant = api.gemm_variant(m, n)
+        variant = api.gemm_variant(m, n, k)
         h = kernels.handle(variant)
         ms, _ = _time_launches(lambda: h(A=a, B=b, N=k, C_global=c), steps, warmup, stream)
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12

@@ -156,5 +156,18 @@ def test_gemm_variant_selection():
     assert api.gemm_variant(4096, 4096) == "gemm_256_k64"      # 256 tiles: one per CU
     assert api.gemm_variant(2048, 2048) == "gemm_128_k64"      # 64 tiles of 256x256
     assert api.gemm_variant(128, 8192) == "gemm_128x32_k64"
+    assert api.gemm_variant(256, 8192) == "gemm_128x64_k64"
+    assert api.gemm_variant(64, 8192, 8192) == "gemm_128_splitk"
+    assert api.gemm_variant(64, 8192, 100) == "gemm_128x32_k64"   # K too short to split
     for v in ("gemm_256_k64", "gemm_128_k64", "gemm_128x32_k64"):
         assert v in kernels.VARIANTS
+
+
+def test_split_k_count_and_ir():
+    from warpir_amd import api
+    assert api.splitk_count(128, 8192, 8192) == 4        # 64 tiles x 4 slices = 256 workgroups
+    assert api.splitk_count(8192, 8192, 8192) == 1
+    assert api.splitk_count(128, 256, 4096) == 16        # 2 tiles: as many 64-deep slices as fit
+    assert api.splitk_count(128, 8192, 8256) == 3        # 8256 = 3 * 2752 = 3 * 43 * 64
+    src = CDNA4Lowerer().lower(kernels.kernel("gemm_128_splitk"))
+    assert "wir::gl<float> C_global" in src and "pid_z, (pid_y) * 128" in src

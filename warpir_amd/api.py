@@ -20,20 +20,94 @@ SKINNY_GEMM_VARIANT = "gemm_128x32_k64"   # M <= 128: 128x32 tiles, 256 workgrou
 MID_GEMM_VARIANT = "gemm_128_k64"         # fewer 256x256 tiles than CUs: 128x128 tiles
 
 
-def gemm_variant(m: int, n: int) -> str:
-    """Kernel variant for an M x N output on the 256 CUs of one MI355X."""
+def gemm_variant(m: int, n: int, k: Optional[int] = None) -> str:
+    """Kernel variant for an M x N (x K) GEMM on the 256 CUs of one MI355X.
+
+    Measured at N = K = 8192 (TFLOP/s): M=64 split-K x4 214 vs 128x32 125;
+    M=128 128x32 443 vs split-K x4 438; M=256 128x64 718 vs 128x32 469."""
+    if m <= 64 and k is not None and splitk_count(m, n, k) >= 4:
+        return SPLITK_GEMM_VARIANT
     if m <= 128:
         return SKINNY_GEMM_VARIANT
+    if m <= 256:
+        return "gemm_128x64_k64"
     if math.ceil(m / 256) * math.ceil(n / 256) < 256:
         return MID_GEMM_VARIANT
     return GEMM_VARIANT
 
 
+SPLITK_GEMM_VARIANT = "gemm_128_splitk"
+_reduce_kernel = None
+
+
+def splitk_count(m: int, n: int, k: int, num_cus: int = 256) -> int:
+    """Number of K slices for the split-K kernel: enough 128x128 tiles x
+    slices to cover the CUs, with every slice a whole number of 64-deep
+    K steps.  1 means no split."""
+    tiles = math.ceil(m / 128) * math.ceil(n / 128)
+    best = 1
+    for s in range(2, 17):
+        if tiles * s > num_cus:
+            break
+        if k % (64 * s) == 0:
+            best = s
+    return best
+
+
+def _splitk_reduce(partials, out, splits: int) -> None:
+    import ctypes
+
+    from warpir_amd.runtime import RawKernel
+
+    global _reduce_kernel
+    if _reduce_kernel is None:
+        _reduce_kernel = RawKernel("splitk_reduce.hsaco", "wir_splitk_reduce")
+
+    class Args(ctypes.Structure):
+        _fields_ = [("partials", ctypes.c_void_p), ("out", ctypes.c_void_p), ("n", ctypes.c_longlong),
+                    ("split_stride", ctypes.c_longlong), ("splits", ctypes.c_int)]
+
+    n = out.numel()
+    args = Args(partials.data_ptr(), out.data_ptr(), n, partials.stride(1), splits)
+    _reduce_kernel.launch(((n // 8 + 255) // 256, 1, 1), (256, 1, 1), args)
+
+
+def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None):
+    """``out = a @ b`` as ``splits`` K slices run side by side (``blockIdx.z``)
+    plus an fp32 reduction: the form for short M and long K, where the
+    output alone has too few tiles to fill the chip.  ``workspace`` is an
+    fp32 tensor of at least ``splits * M * N`` elements (allocated if
+    omitted)."""
+    import torch
+
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
+        raise ValueError(f"gemm: shapes {tuple(a.shape)} @ {tuple(b.shape)} do not chain")
+    m, k = a.shape
+    n = b.shape[1]
+    splits = splits or splitk_count(m, n, k)
+    if k % (64 * splits) or n % 8 or not a.is_contiguous() or not b.is_contiguous():
+        raise ValueError(f"gemm_split_k: K={k} must split into {splits} multiples of 64, N % 8 == 0, "
+                         "contiguous operands")
+    kc = k // splits
+    if out is None:
+        out = torch.empty(m, n, dtype=torch.bfloat16, device=a.device)
+    if workspace is None:
+        workspace = torch.empty(splits * m * n, dtype=torch.float32, device=a.device)
+    if workspace.numel() < splits * m * n or workspace.dtype != torch.float32:
+        raise ValueError("gemm_split_k: workspace must be fp32 with splits * M * N elements")
+    av = a.as_strided((1, splits, m, kc), (0, kc, k, 1))
+    bv = b.view(1, splits, kc, n)
+    part = workspace[: splits * m * n].view(1, splits, m, n)
+    kernels.handle(SPLITK_GEMM_VARIANT)(A=av, B=bv, N=kc, C_global=part)
+    _splitk_reduce(part, out, splits)
+    return out
+
+
 def gemm(a, b, out=None, variant: Optional[str] = None):
     """``out[M, N] = a[M, K] @ b[K, N]`` in bf16 with fp32 accumulation.
 
-    The default variant is the 256x256 tile; outputs with fewer 256x256
-    tiles than CUs take 128x128 tiles and M <= 128 takes 128x32 tiles.
+    The variant follows ``gemm_variant``: 256x256 tiles by default, smaller
+    tiles for outputs with fewer tiles than CUs, split-K for M <= 64.
     """
     import torch
 
@@ -46,7 +120,9 @@ def gemm(a, b, out=None, variant: Optional[str] = None):
     if out is None:
         out = torch.empty(m, n, dtype=torch.bfloat16, device=a.device)
     if variant is None:
-        variant = gemm_variant(m, n)
+        variant = gemm_variant(m, n, k)
+    if variant == SPLITK_GEMM_VARIANT:
+        return gemm_split_k(a, b, out=out)
     kernels.handle(variant)(A=a, B=b, N=k, C_global=out)
     return out
 
@@ -89,4 +165,4 @@ def _loops(kernel):
     return (op for op in kernel.body if isinstance(op, ForOp))
 
 
-__all__ = ["gemm", "gemm_variant", "attention_forward", "attention_flops"]
+__all__ = ["gemm", "gemm_split_k", "splitk_count", "gemm_variant", "attention_forward", "attention_flops"]

@@ -15,9 +15,11 @@ from warpir_amd.workloads import build_attention_kernel, build_gemm_kernel, buil
 
 
 def _gemm_mi355x(block_k: int = 32, block_m: int = 256, block_n: int = 256, wave_m: int = 128,
-                 wave_n: int = 128, load_units: int = 8, lds_budget: int = 160 * 1024) -> Kernel:
+                 wave_n: int = 128, load_units: int = 8, lds_budget: int = 160 * 1024,
+                 split_k: bool = False) -> Kernel:
     return kernel_pass(build_gemm_kernel(block_m=block_m, block_n=block_n, block_k=block_k, wave_m=wave_m,
-                                         wave_n=wave_n, name="gemm"),
+                                         wave_n=wave_n, name="gemm_splitk" if split_k else "gemm",
+                                         split_k=split_k),
                        cost_model=gfx950_cost_model(block_m, block_n, block_k, load_units=load_units,
                                                     lds_budget=lds_budget))
 
@@ -39,6 +41,10 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
                                             lds_budget=80 * 1024),
     "gemm_128x32_k64": lambda: _gemm_mi355x(64, block_m=128, block_n=32, wave_m=32, wave_n=32,
                                             lds_budget=80 * 1024),
+    # Split-K form of the 128x128 tile: K slices along blockIdx.z, fp32 partials
+    # summed by the split-K reduction (short M, long K).
+    "gemm_128_splitk": lambda: _gemm_mi355x(64, block_m=128, block_n=128, wave_m=64, wave_n=64,
+                                            lds_budget=80 * 1024, split_k=True),
     # 8 wavefronts (2 per SIMD) of 128x64 in the ping-pong form, K=32 with a 4-slot ring.
     "gemm_256_pp": lambda: _gemm_mi355x(32, wave_m=128, wave_n=64, load_units=12),
     # The reference's single-head attention IR (tests/attention_baseline.py:46-186).

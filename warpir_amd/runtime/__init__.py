@@ -326,6 +326,49 @@ def compile_kernel(kernel: Kernel, lowerer=None) -> KernelHandle:
     return KernelHandle(kernel, lowerer)
 
 
+class RawKernel:
+    """A hand-written kernel from a prebuilt code object in the package
+    (``__graft_entry__.build()`` compiles them), launched through the C ABI
+    with a ctypes argument structure on the current stream."""
+
+    def __init__(self, filename: str, symbol: str):
+        self.path = os.path.join(PKG_DIR, filename)
+        self.symbol = symbol
+        self._module = None
+        self._function = None
+
+    def _load(self) -> None:
+        if self._function is not None:
+            return
+        if not os.path.exists(self.path):
+            raise CompileError(f"{self.path} is not built (run __graft_entry__.build())")
+        lib = library()
+        with open(self.path, "rb") as f:
+            self._image = f.read()
+        mod, fn = ctypes.c_void_p(), ctypes.c_void_p()
+        check(lib.wir_module_load(self._image, len(self._image), ctypes.byref(mod)), f"wir_module_load({self.path})")
+        check(lib.wir_module_get_function(mod, self.symbol.encode(), ctypes.byref(fn)),
+              f"wir_module_get_function({self.symbol})")
+        self._module, self._function = mod, fn
+
+    def launch(self, grid: Tuple[int, int, int], block: Tuple[int, int, int], args: ctypes.Structure,
+               stream=None) -> None:
+        import torch
+
+        self._load()
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
+        check(library().wir_launch(self._function, *grid, *block, 0, ctypes.c_void_p(stream), ctypes.byref(args),
+                                   ctypes.sizeof(args)), f"wir_launch({self.symbol})")
+
+    def __del__(self):
+        if _lib is not None and self._module:
+            try:
+                _lib.wir_module_unload(self._module)
+            except Exception:
+                pass
+
+
 class Event:
     """A HIP timing event recorded on a stream through the C ABI."""
 
@@ -349,5 +392,5 @@ class Event:
                 pass
 
 
-__all__ = ["HipError", "CompileError", "KernelHandle", "compile_kernel", "compile_source", "library",
-           "device_info", "Event", "kernarg_struct", "GL", "hsaco_path", "resource_usage"]
+__all__ = ["HipError", "CompileError", "KernelHandle", "RawKernel", "compile_kernel", "compile_source",
+           "library", "device_info", "Event", "kernarg_struct", "GL", "hsaco_path", "resource_usage"]

@@ -61,7 +61,8 @@ def _bf16_global(tile: SharedTileType, batch: int = 1, depth: int = 1) -> Global
 
 
 def build_gemm_kernel(block_m: int = 64, block_n: int = 64, block_k: int = 64,
-                      wave_m: int = 16, wave_n: int = 64, name: str = "gemm") -> Kernel:
+                      wave_m: int = 16, wave_n: int = 64, name: str = "gemm",
+                      split_k: bool = False) -> Kernel:
     """``C[M, N] = A[M, K] @ B[K, N]``, bf16 in, fp32 accumulate, bf16 out.
 
     One program per ``block_m x block_n`` tile of C at
@@ -72,11 +73,24 @@ def build_gemm_kernel(block_m: int = 64, block_n: int = 64, block_k: int = 64,
     ``(block_m / wave_m) * (block_n / wave_n)`` wavefronts.
 
     Defaults reproduce ``tests/gemm_baseline_v2.py:31-88``.
+
+    ``split_k`` (additive): the globals get a depth dimension indexed by
+    ``blockIdx.z``, one K slice per depth -- A as ``[1, S, M, K/S]``, B as
+    ``[1, S, K/S, N]`` -- and C_global becomes an fp32 ``[1, S, M, N]`` of
+    partial products, which the host sums (``warpir_amd.api.gemm``).  ``N``
+    is then the slice's reduction extent.
     """
     a_tile = SharedTileType(GPUType.bf16, block_m, block_k)
     b_tile = SharedTileType(GPUType.bf16, block_k, block_n)
-    c_tile = SharedTileType(GPUType.bf16, block_m, block_n)
-    a_glob, b_glob, c_glob = _bf16_global(a_tile), _bf16_global(b_tile), _bf16_global(c_tile)
+    if split_k:
+        c_tile = SharedTileType(GPUType.fp32, block_m, block_n)
+        a_glob, b_glob = _bf16_global(a_tile, depth=-1), _bf16_global(b_tile, depth=-1)
+        c_glob = GlobalType(data_type=GPUType.fp32, sub_tile_type=c_tile, batch=1, depth=-1, rows=-1, cols=-1)
+        depth = Value("blockIdx.z", IntType())
+    else:
+        c_tile = SharedTileType(GPUType.bf16, block_m, block_n)
+        a_glob, b_glob, c_glob = _bf16_global(a_tile), _bf16_global(b_tile), _bf16_global(c_tile)
+        depth = 0
     acc = RegTileType(GPUType.fp32, wave_m, wave_n)
 
     A, B, C = Value("A", a_glob), Value("B", b_glob), Value("C_global", c_glob)
@@ -90,8 +104,8 @@ def build_gemm_kernel(block_m: int = 64, block_n: int = 64, block_k: int = 64,
         induction_var=i, start=0, stop=n_red, step=1, tile_size=block_k,
         iter_args=(IterArg(block_arg=c_accum, init=c_init),),
         body=(
-            TMALoadOp(result=a_sh, source=A, coords=(0, 0, row, i)),
-            TMALoadOp(result=b_sh, source=B, coords=(0, 0, i, col)),
+            TMALoadOp(result=a_sh, source=A, coords=(0, depth, row, i)),
+            TMALoadOp(result=b_sh, source=B, coords=(0, depth, i, col)),
             WaitOp(values=(a_sh, b_sh)),
             MMAOp(result=c_new, a=a_sh, b=b_sh, accum=c_accum),
             YieldOp(values=(c_new,)),
@@ -101,7 +115,7 @@ def build_gemm_kernel(block_m: int = 64, block_n: int = 64, block_k: int = 64,
     return Kernel(
         name=name, inputs=(A, B, n_red), outputs=(C,),
         body=(ZeroOp(result=c_init), loop,
-              TMAStoreOp(source=c_final, dest=C, coords=(0, 0, row, col))),
+              TMAStoreOp(source=c_final, dest=C, coords=(0, depth, row, col))),
     )
 
 
