@@ -19,7 +19,12 @@ pipelined IR relies on it (``warpir/lowering/lowering.py``):
 * tile loads read zeros outside the tensor and stores drop elements
   outside it (TMA's out-of-bounds behaviour);
 * a ``CopyOp`` into a bf16 type, and every store to a bf16 global, round
-  to bf16.
+  to bf16; a ``CopyOp`` of a shared tile into a register tile is a plain
+  read (the tile is already fp32 here);
+* ``LoadVecOp`` reads ``L`` consecutive rows of an ``L x 1``-tiled global
+  (zeros outside), as a block-level vector: a col_vec's length is its
+  block's rows, a row_vec's its tile's columns; ``SubColOp`` subtracts a
+  row_vec from every row.
 
 Tile coordinates are ``(batch, depth, row_tile, col_tile)`` in units of
 the global's ``sub_tile_type``.  The grid covers every store: a coordinate
@@ -34,9 +39,9 @@ import torch
 
 from warpir_amd.ir import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, ColVecType, CopyOp, DivRowOp, Exp2Op,
-    ForOp, GPUType, IntAffineOp, Kernel, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp,
-    NegInftyOp, RegTileType, RowMaxOp, RowSumOp, SlotViewOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp,
-    TMAStoreOp, Value, WaitBufOp, WaitOp, YieldOp, ZeroOp,
+    ForOp, GPUType, IntAffineOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp,
+    NegInftyOp, RegTileType, RowMaxOp, RowSumOp, RowVecType, SlotViewOp, SubColOp, SubOp, SubRowOp,
+    TMALoadBufOp, TMALoadOp, TMAStoreOp, Value, WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
 
 BUILTINS = ("blockIdx.x", "blockIdx.y", "blockIdx.z")
@@ -219,6 +224,17 @@ class Interpreter:
             s(op.result, t.masked_fill(c > r, float("-inf")))
         elif isinstance(op, IntAffineOp):
             s(op.result, self._int(op.input) * op.mul + op.add)
+        elif isinstance(op, SubColOp):
+            s(op.result, g(op.tile) - g(op.vec).reshape(1, -1))
+        elif isinstance(op, LoadVecOp):
+            gl = _as4d(self.tensors[op.source.name], op.source.type)
+            n = op.source.type.sub_tile_type.rows
+            b, d, rt, _ct = (self._int(c) for c in op.coords)
+            vec = torch.zeros(n, dtype=torch.float32)
+            if 0 <= b < gl.shape[0] and 0 <= d < gl.shape[1]:
+                blk = gl[b, d, rt * n:rt * n + n, 0].float()
+                vec[:blk.shape[0]] = blk
+            s(op.result, vec)
         elif isinstance(op, TMAStoreOp):
             self._store(g(op.source), op.dest, op.coords)
         elif isinstance(op, ForOp):

@@ -7,6 +7,10 @@ Follows the reference's checks:
   to bound the score matrix, with an optional causal mask
   (``kernel_examples/attention/mha_h100.cu:160-176``) and the natural-log
   log-sum-exp of the scaled scores.
+* attention backward: the gradients of that fp32 forward by torch
+  autograd (the reference has no backward oracle; its TK backward,
+  ``mha_h100.cu:253-303,482-642``, is checked against torch autograd in
+  the same way upstream).  Closed forms pinning it are in the tests.
 """
 from __future__ import annotations
 
@@ -57,6 +61,27 @@ def attention_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Opti
         o = o.reshape(*lead, q.shape[-2], v.shape[-1])
         lse = lse.reshape(*lead, q.shape[-2])
     return o, lse
+
+
+def attention_bwd_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, do: torch.Tensor,
+                      scale: Optional[float] = None, causal: bool = False):
+    """``(dQ, dK, dV)`` of ``sum(softmax(q k^T * scale) v * do)`` in fp32 on CPU,
+    by autograd over ``[..., S, D]`` inputs (per leading index, to bound memory)."""
+    scale = scale if scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    lead = q.shape[:-2]
+    qf, kf, vf, dof = (t.float().reshape(-1, *t.shape[-2:]) for t in (q, k, v, do))
+    outs = ([], [], [])
+    for n in range(qf.shape[0]):
+        qn, kn, vn = (t[n].clone().requires_grad_(True) for t in (qf, kf, vf))
+        s = (qn @ kn.t()) * scale
+        if causal:
+            rows, cols = s.shape
+            s = s.masked_fill(torch.ones(rows, cols, dtype=torch.bool).triu(1), float("-inf"))
+        o = torch.softmax(s, dim=-1) @ vn
+        o.backward(dof[n])
+        for acc, t in zip(outs, (qn, kn, vn)):
+            acc.append(t.grad.detach())
+    return tuple(torch.stack(a).reshape(*lead, *a[0].shape) for a in outs)
 
 
 def rel_err(out: torch.Tensor, ref: torch.Tensor) -> float:

@@ -260,6 +260,31 @@ class CausalMaskOp(Op):
 
 
 @dataclass(frozen=True)
+class SubColOp(Op):
+    """*Additive.* ``result[r, c] = tile[r, c] - vec[c]`` (``vec`` a row_vec)."""
+
+    result: Value
+    tile: Value
+    vec: Value
+
+
+@dataclass(frozen=True)
+class LoadVecOp(Op):
+    """*Additive.* Synchronous load of a register vector from an fp32 global.
+
+    The global's sub tile is ``L x 1``; ``coords = (batch, depth, tile, 0)``
+    select elements ``tile*L .. tile*L + L - 1`` along its rows.  A col_vec
+    result takes them as per-row values of its tile, a row_vec result as
+    per-column values.  Elements outside the tensor read 0.  (Statistics
+    saved by the forward pass, e.g. the log-sum-exp, for the backward.)
+    """
+
+    result: Value
+    source: Value
+    coords: tuple
+
+
+@dataclass(frozen=True)
 class IntAffineOp(Op):
     """*Additive.* Integer ``result = input * mul + add``.
 

@@ -109,6 +109,20 @@ class ColVecType:
 
 
 @dataclass(frozen=True)
+class RowVecType:
+    """*Additive.* A per-column register vector of a ``rows x cols`` register
+    tile: one value per column, shared by all rows (e.g. the per-query
+    log-sum-exp across a key-major score tile in attention backward)."""
+
+    data_type: GPUType
+    rows: int
+    cols: int
+
+    def __str__(self) -> str:
+        return f"row_vec<{self.data_type.value}, {self.rows}x{self.cols}>"
+
+
+@dataclass(frozen=True)
 class ScalarType:
     """A named scalar type (``types.py:74-79``)."""
 

@@ -19,6 +19,7 @@ from warpir_amd.ir.ops import (
     Exp2Op,
     ForOp,
     IntAffineOp,
+    LoadVecOp,
     Kernel,
     Log2Op,
     MMABufOp,
@@ -32,6 +33,7 @@ from warpir_amd.ir.ops import (
     RowSumOp,
     SlotViewOp,
     SubOp,
+    SubColOp,
     SubRowOp,
     TMALoadBufOp,
     TMALoadOp,
@@ -124,6 +126,8 @@ _LINE: Dict[type, Callable[[Op], str]] = {
     IntAffineOp: lambda op: (
         f"{op.result!r} = int_affine({_coord(op.input)}, {op.mul}, {op.add})"
     ),
+    SubColOp: lambda op: _call(op, "sub_col", op.tile, op.vec),
+    LoadVecOp: lambda op: f"{op.result!r} = load_vec({op.source!r}, {_coords(op.coords)})",
 }
 
 

@@ -28,6 +28,7 @@ from warpir_amd.ir import (
     IntType,
     IterArg,
     Kernel,
+    LoadVecOp,
     Log2Op,
     MMAOp,
     MulOp,
@@ -37,7 +38,9 @@ from warpir_amd.ir import (
     RegTileType,
     RowMaxOp,
     RowSumOp,
+    RowVecType,
     SharedTileType,
+    SubColOp,
     SubOp,
     SubRowOp,
     TMALoadOp,
@@ -260,3 +263,183 @@ def _attention(*, name, d, block_q, block_kv, wave_rows, scale, multi_head, caus
         ]
         outputs.append(L)
     return Kernel(name=name, inputs=(Q, K, V, n_kv), outputs=tuple(outputs), body=tuple(kernel_body))
+
+
+# ---------------------------------------------------------------------------
+# FlashAttention backward (additive): three kernels over the forward's O and
+# LSE, following the structure of the reference's TK backward
+# (kernel_examples/attention/mha_h100.cu:253-303 prep, :482-642 main) with
+# dQ computed by its own query-major kernel instead of atomic adds:
+#   prep:  Dv[q]   = sum_d dO[q, d] * O[q, d]
+#   dq:    per query tile, over key tiles: P = exp(Q K^T s - LSE),
+#          dS = P * (dO V^T - Dv),  dQ = s * sum dS K
+#   dkdv:  per key tile, over query tiles (key-major, so P^T and dS^T come
+#          straight out of the MMAs): dV = sum P^T dO,  dK = s * sum dS^T Q
+# with s = 1/sqrt(D).  Exponentials run in the exp2 domain.
+# ---------------------------------------------------------------------------
+
+def _bwd_globals(d: int, rows: int):
+    tile = SharedTileType(GPUType.bf16, rows, d)
+    vec_tile = SharedTileType(GPUType.fp32, rows, 1)
+    return GlobalType(GPUType.bf16, tile), GlobalType(GPUType.fp32, vec_tile, cols=1), tile
+
+
+def build_mha_bwd_prep_kernel(d: int = 128, block_q: int = 128, wave_rows: int = 32,
+                              name: str = "mha_bwd_prep") -> Kernel:
+    """``Dv[b, h, q] = sum_d dO * O`` over ``[B, H, S, D]`` (bwd prep, ``mha_h100.cu:253-303``)."""
+    g_bf, g_vec, tile = _bwd_globals(d, block_q)
+    O, dO, Dv = Value("O", g_bf), Value("dO", g_bf), Value("Dv", g_vec)
+    q_idx, head, batch = (Value(n, IntType()) for n in ("blockIdx.x", "blockIdx.y", "blockIdx.z"))
+    reg = RegTileType(GPUType.fp32, wave_rows, d)
+    cvec = ColVecType(GPUType.fp32, wave_rows, d)
+    o_sh, do_sh = Value("o_shared", tile), Value("do_shared", tile)
+    o_r, do_r, prod = Value("o_reg", reg), Value("do_reg", reg), Value("prod", reg)
+    zero, dvec = Value("d_zero", cvec), Value("d_vec", cvec)
+    body = (
+        TMALoadOp(result=o_sh, source=O, coords=(batch, head, q_idx, 0)),
+        TMALoadOp(result=do_sh, source=dO, coords=(batch, head, q_idx, 0)),
+        WaitOp(values=(o_sh, do_sh)),
+        CopyOp(result=o_r, input=o_sh),
+        CopyOp(result=do_r, input=do_sh),
+        MulOp(result=prod, a=o_r, b=do_r),
+        ZeroOp(result=zero),
+        RowSumOp(result=dvec, tile=prod, prev=zero),
+        TMAStoreOp(source=dvec, dest=Dv, coords=(batch, head, q_idx, 0)),
+    )
+    return Kernel(name=name, inputs=(O, dO), outputs=(Dv,), body=body)
+
+
+def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64, wave_rows: int = 32,
+                            name: str = "mha_bwd_dq") -> Kernel:
+    """``dQ`` of attention forward, query-major: one program per query tile
+    ``(blockIdx.x, head, batch)``; the loop walks key tiles."""
+    scale = 1.0 / math.sqrt(d)
+    q_glob, vec_glob, q_tile = _bwd_globals(d, block_q)
+    kv_glob, _, kv_tile = _bwd_globals(d, block_kv)
+    Q, K, V, dO = Value("Q", q_glob), Value("K", kv_glob), Value("V", kv_glob), Value("dO", q_glob)
+    L, Dv, dQ = Value("L", vec_glob), Value("Dv", vec_glob), Value("dQ", q_glob)
+    n_kv = Value("N", IntType())
+    q_idx, head, batch = (Value(n, IntType()) for n in ("blockIdx.x", "blockIdx.y", "blockIdx.z"))
+    bh = (batch, head)
+    att_f = RegTileType(GPUType.fp32, wave_rows, block_kv)
+    att_b = RegTileType(GPUType.bf16, wave_rows, block_kv)
+    acc = RegTileType(GPUType.fp32, wave_rows, d)
+    cvec = ColVecType(GPUType.fp32, wave_rows, block_kv)
+
+    def v(n, t):
+        return Value(n, t)
+
+    q_sh, do_sh, k_sh, v_sh = v("q_shared", q_tile), v("do_shared", q_tile), v("k_shared", kv_tile), v("v_shared", kv_tile)
+    lse, dvec, lse2 = v("lse", cvec), v("d_vec", cvec), v("lse_log2", cvec)
+    i = v("i", IntType())
+    dq_init, dq_acc, dq_new, dq_final, dq_out = (v(n, acc) for n in ("dq_init", "dq_accum", "dq_new", "dq_final", "dq_out"))
+    zero, s_t, s_sc, s_sh, p = (v(n, att_f) for n in ("s_zero", "s", "s_scaled", "s_shifted", "p"))
+    dp_zero, dp, dp_sub, ds = (v(n, att_f) for n in ("dp_zero", "dp", "dp_minus_d", "ds"))
+    ds_b = v("ds_bf16", att_b)
+    loop = ForOp(
+        induction_var=i, start=0, stop=n_kv, step=1, tile_size=block_kv,
+        iter_args=(IterArg(block_arg=dq_acc, init=dq_init),),
+        body=(
+            TMALoadOp(result=k_sh, source=K, coords=(*bh, i, 0)),
+            TMALoadOp(result=v_sh, source=V, coords=(*bh, i, 0)),
+            WaitOp(values=(k_sh, v_sh)),
+            ZeroOp(result=zero),
+            MMAOp(result=s_t, a=q_sh, b=k_sh, accum=zero, transpose_b=True),
+            MulScalarOp(result=s_sc, input=s_t, scalar=scale * LOG2E),
+            SubRowOp(result=s_sh, tile=s_sc, vec=lse2),
+            Exp2Op(result=p, input=s_sh),
+            ZeroOp(result=dp_zero),
+            MMAOp(result=dp, a=do_sh, b=v_sh, accum=dp_zero, transpose_b=True),
+            SubRowOp(result=dp_sub, tile=dp, vec=dvec),
+            MulOp(result=ds, a=p, b=dp_sub),
+            CopyOp(result=ds_b, input=ds),
+            MMAOp(result=dq_new, a=ds_b, b=k_sh, accum=dq_acc),
+            YieldOp(values=(dq_new,)),
+        ),
+        results=(dq_final,),
+    )
+    body = (
+        TMALoadOp(result=q_sh, source=Q, coords=(*bh, q_idx, 0)),
+        TMALoadOp(result=do_sh, source=dO, coords=(*bh, q_idx, 0)),
+        WaitOp(values=(q_sh, do_sh)),
+        LoadVecOp(result=lse, source=L, coords=(*bh, q_idx, 0)),
+        LoadVecOp(result=dvec, source=Dv, coords=(*bh, q_idx, 0)),
+        MulScalarOp(result=lse2, input=lse, scalar=LOG2E),
+        ZeroOp(result=dq_init),
+        loop,
+        MulScalarOp(result=dq_out, input=dq_final, scalar=scale),
+        TMAStoreOp(source=dq_out, dest=dQ, coords=(*bh, q_idx, 0)),
+    )
+    return Kernel(name=name, inputs=(Q, K, V, dO, L, Dv, n_kv), outputs=(dQ,), body=body)
+
+
+def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 64, wave_rows: int = 32,
+                              name: str = "mha_bwd_dkdv") -> Kernel:
+    """``dK`` and ``dV`` of attention forward, key-major: one program per key
+    tile ``(blockIdx.x, head, batch)``; the loop walks query tiles.  Scores
+    are computed transposed (``S^T = K Q^T``), so the per-query LSE and Dv
+    are row_vecs loaded per query tile."""
+    scale = 1.0 / math.sqrt(d)
+    kv_glob, vec_glob, kv_tile = _bwd_globals(d, block_kv)
+    q_glob, qvec_glob, q_tile = _bwd_globals(d, block_q)
+    Q, K, V, dO = Value("Q", q_glob), Value("K", kv_glob), Value("V", kv_glob), Value("dO", q_glob)
+    L, Dv = Value("L", qvec_glob), Value("Dv", qvec_glob)
+    dK, dV = Value("dK", kv_glob), Value("dV", kv_glob)
+    n_q = Value("N", IntType())
+    kv_idx, head, batch = (Value(n, IntType()) for n in ("blockIdx.x", "blockIdx.y", "blockIdx.z"))
+    bh = (batch, head)
+    st_f = RegTileType(GPUType.fp32, wave_rows, block_q)
+    st_b = RegTileType(GPUType.bf16, wave_rows, block_q)
+    acc = RegTileType(GPUType.fp32, wave_rows, d)
+    rvec = RowVecType(GPUType.fp32, wave_rows, block_q)
+
+    def v(n, t):
+        return Value(n, t)
+
+    k_sh, v_sh, q_sh, do_sh = v("k_shared", kv_tile), v("v_shared", kv_tile), v("q_shared", q_tile), v("do_shared", q_tile)
+    i = v("i", IntType())
+    lse, lse2, dvec = v("lse", rvec), v("lse_log2", rvec), v("d_vec", rvec)
+    dk_init, dk_acc, dk_new, dk_final, dk_out = (v(n, acc) for n in ("dk_init", "dk_accum", "dk_new", "dk_final", "dk_out"))
+    dv_init, dv_acc, dv_new, dv_final = (v(n, acc) for n in ("dv_init", "dv_accum", "dv_new", "dv_final"))
+    zero, st, st_sc, st_sh, pt = (v(n, st_f) for n in ("st_zero", "st", "st_scaled", "st_shifted", "pt"))
+    dpt_zero, dpt, dpt_sub, dst = (v(n, st_f) for n in ("dpt_zero", "dpt", "dpt_minus_d", "dst"))
+    pt_b, dst_b = v("pt_bf16", st_b), v("dst_bf16", st_b)
+    loop = ForOp(
+        induction_var=i, start=0, stop=n_q, step=1, tile_size=block_q,
+        iter_args=(IterArg(block_arg=dk_acc, init=dk_init), IterArg(block_arg=dv_acc, init=dv_init)),
+        body=(
+            TMALoadOp(result=q_sh, source=Q, coords=(*bh, i, 0)),
+            TMALoadOp(result=do_sh, source=dO, coords=(*bh, i, 0)),
+            WaitOp(values=(q_sh, do_sh)),
+            LoadVecOp(result=lse, source=L, coords=(*bh, i, 0)),
+            LoadVecOp(result=dvec, source=Dv, coords=(*bh, i, 0)),
+            ZeroOp(result=zero),
+            MMAOp(result=st, a=k_sh, b=q_sh, accum=zero, transpose_b=True),
+            MulScalarOp(result=st_sc, input=st, scalar=scale * LOG2E),
+            MulScalarOp(result=lse2, input=lse, scalar=LOG2E),
+            SubColOp(result=st_sh, tile=st_sc, vec=lse2),
+            Exp2Op(result=pt, input=st_sh),
+            ZeroOp(result=dpt_zero),
+            MMAOp(result=dpt, a=v_sh, b=do_sh, accum=dpt_zero, transpose_b=True),
+            SubColOp(result=dpt_sub, tile=dpt, vec=dvec),
+            MulOp(result=dst, a=pt, b=dpt_sub),
+            CopyOp(result=pt_b, input=pt),
+            CopyOp(result=dst_b, input=dst),
+            MMAOp(result=dv_new, a=pt_b, b=do_sh, accum=dv_acc),
+            MMAOp(result=dk_new, a=dst_b, b=q_sh, accum=dk_acc),
+            YieldOp(values=(dk_new, dv_new)),
+        ),
+        results=(dk_final, dv_final),
+    )
+    body = (
+        TMALoadOp(result=k_sh, source=K, coords=(*bh, kv_idx, 0)),
+        TMALoadOp(result=v_sh, source=V, coords=(*bh, kv_idx, 0)),
+        WaitOp(values=(k_sh, v_sh)),
+        ZeroOp(result=dk_init),
+        ZeroOp(result=dv_init),
+        loop,
+        MulScalarOp(result=dk_out, input=dk_final, scalar=scale),
+        TMAStoreOp(source=dk_out, dest=dK, coords=(*bh, kv_idx, 0)),
+        TMAStoreOp(source=dv_final, dest=dV, coords=(*bh, kv_idx, 0)),
+    )
+    return Kernel(name=name, inputs=(Q, K, V, dO, L, Dv, n_q), outputs=(dK, dV), body=body)
