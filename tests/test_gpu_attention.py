@@ -1,9 +1,10 @@
-"""GPU parity of WarpIR-generated FlashAttention-forward kernels.
+"""GPU parity of WarpIR-generated FlashAttention kernels.
 
 Oracle: naive fp32 ``softmax(q k^T / sqrt(d)) v`` (reference
 ``tests/test_modal_attention.py:92-98``) and the natural-log
 log-sum-exp, on the CPU from the same seeded bf16 inputs, at
-``max|out - ref| / max|ref| <= 1e-2``.
+``max|out - ref| / max|ref| <= 1e-2``; for the backward kernels, torch
+autograd of that fp32 forward at the same tolerance.
 """
 import math
 
@@ -66,3 +67,43 @@ def test_mha_full_size_sampled(gpu):
         ref, ref_lse = attention_ref(q[bi, hi], k[bi, hi], v[bi, hi])
         assert rel_err(o[bi, hi], ref) <= TOL
         assert (lse[bi, hi] - ref_lse).abs().max().item() <= 1e-2
+
+
+@pytest.mark.parametrize("b,h,s,d", [(1, 1, 128, 128), (2, 3, 256, 128), (1, 2, 192, 128), (1, 1, 1024, 128),
+                                     (1, 2, 256, 64), (1, 1, 64, 64)])
+def test_mha_backward(gpu, b, h, s, d):
+    from oracle.torch_ref import attention_bwd_ref
+    announce(f"mha backward B={b} H={h} S={s} D={d}")
+    q, k, v, do = (seeded_normal((b, h, s, d), sd) for sd in (10, 11, 12, 13))
+    if d == 128:
+        o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda())
+    else:
+        o, lse = _fwd_d64(q, k, v)
+    dq, dk, dv = api.attention_backward(q.cuda(), k.cuda(), v.cuda(), o, lse, do.cuda())
+    torch.cuda.synchronize()
+    rq, rk, rv = attention_bwd_ref(q, k, v, do)
+    for name, got, ref in (("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
+        err = rel_err(got.cpu().float(), ref)
+        assert err <= TOL, (name, err)
+
+
+def _fwd_d64(q, k, v):
+    """Forward outputs for D=64 (no non-causal D=64 forward variant): the oracle's, as bf16 / fp32 on the GPU."""
+    o, lse = attention_ref(q, k, v)
+    return o.to(torch.bfloat16).cuda(), lse.float().cuda()
+
+
+def test_mha_backward_full_size_sampled(gpu):
+    """Config-4 shape; the autograd oracle runs on 2 of the 256 (b, h) heads."""
+    from oracle.torch_ref import attention_bwd_ref
+    shape = (16, 16, 4096, 128)
+    announce(f"mha backward full {shape}")
+    q, k, v, do = (seeded_normal(shape, sd) for sd in (10, 11, 12, 13))
+    o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda())
+    dq, dk, dv = api.attention_backward(q.cuda(), k.cuda(), v.cuda(), o, lse, do.cuda())
+    torch.cuda.synchronize()
+    for (bi, hi) in [(0, 0), (15, 9)]:
+        rq, rk, rv = attention_bwd_ref(q[bi, hi], k[bi, hi], v[bi, hi], do[bi, hi])
+        for name, got, ref in (("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
+            err = rel_err(got[bi, hi].cpu().float(), ref)
+            assert err <= TOL, (name, bi, hi, err)

@@ -154,6 +154,41 @@ def attention_forward(q, k, v, causal: bool = False, out=None, lse=None,
     return out, lse
 
 
+def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None):
+    """Gradients ``(dQ, dK, dV)`` of ``attention_forward`` over ``[B, H, S, D]``
+    bf16 (non-causal), from its outputs ``o`` and ``lse`` and the output
+    gradient ``do``; S must be a multiple of 64.  Three WarpIR kernels run
+    on the current stream: ``Dv = rowsum(dO * O)`` (into ``dvec``, fp32
+    ``[B, H, S]``, allocated if omitted), the query-major dQ kernel and the
+    key-major dK/dV kernel (the reference's TK backward,
+    ``kernel_examples/attention/mha_h100.cu:253-303,482-642``, computes the
+    same gradients with dQ by atomic adds)."""
+    import torch
+
+    if q.dim() != 4 or not (q.shape == k.shape == v.shape == o.shape == do.shape):
+        raise ValueError("attention_backward: q, k, v, o, do must share one [B, H, S, D] shape")
+    bsz, heads, seq, d = q.shape
+    if d not in (64, 128) or seq % 64:
+        raise ValueError(f"attention_backward: D must be 64 or 128 and S a multiple of 64 (got D={d}, S={seq})")
+    if tuple(lse.shape) != (bsz, heads, seq) or lse.dtype != torch.float32:
+        raise ValueError("attention_backward: lse must be fp32 [B, H, S]")
+    dq = torch.empty_like(q) if dq is None else dq
+    dk = torch.empty_like(k) if dk is None else dk
+    dv = torch.empty_like(v) if dv is None else dv
+    dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device=q.device) if dvec is None else dvec
+    kernels.handle(f"mha_bwd_prep_d{d}")(O=o, dO=do, Dv=dvec)
+    kernels.handle(f"mha_bwd_dq_d{d}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq)
+    kernels.handle(f"mha_bwd_dkdv_d{d}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dK=dk, dV=dv)
+    return dq, dk, dv
+
+
+def attention_backward_flops(bsz: int, heads: int, seq: int, d: int) -> float:
+    """Matmul FLOPs of attention backward counted as the five S x S x D
+    products of the standard algorithm (S, dP, dV, dK, dQ): 10*B*H*S^2*D.
+    These kernels run seven (dQ recomputes S and dP instead of atomics)."""
+    return 10.0 * bsz * heads * seq * seq * d
+
+
 def attention_flops(bsz: int, heads: int, seq: int, d: int, causal: bool = False) -> float:
     """Matmul FLOPs of attention forward: 4*B*H*S^2*D (halved when causal)."""
     f = 4.0 * bsz * heads * seq * seq * d
@@ -165,4 +200,5 @@ def _loops(kernel):
     return (op for op in kernel.body if isinstance(op, ForOp))
 
 
-__all__ = ["gemm", "gemm_split_k", "splitk_count", "gemm_variant", "attention_forward", "attention_flops"]
+__all__ = ["gemm", "gemm_split_k", "splitk_count", "gemm_variant", "attention_forward", "attention_backward",
+           "attention_flops", "attention_backward_flops"]

@@ -293,6 +293,15 @@ struct RVec {
   float v[RB];
 };
 
+// Row vector of a lane = row tile (one value per column, shared by all rows):
+// v[cb][i] is the value of the column that C register i of column block cb
+// holds in this lane, i.e. column cb*MS + ccol<MS>(i, lane / MS).
+template <int MS, int C>
+struct CVec {
+  static constexpr int CB = C / MS;
+  float v[CB][MF<MS>::CREGS];
+};
+
 template <int MS, int R, int C>
 __device__ __forceinline__ void fill(RTile<MS, R, C>& t, float x) {
 #pragma unroll
@@ -767,6 +776,82 @@ __device__ __forceinline__ void map2(RTile<MS, R, C>& out, const RTile<MS, R, C>
     for (int rb = 0; rb < out.RB; ++rb)
 #pragma unroll
       for (int i = 0; i < MF<MS>::CREGS; ++i) out.f[cb][rb][i] = fn(a.f[cb][rb][i], b.f[cb][rb][i]);
+}
+
+template <int MS, int C, class F>
+__device__ __forceinline__ void cvmap(CVec<MS, C>& out, const CVec<MS, C>& in, F fn) {
+#pragma unroll
+  for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+    for (int i = 0; i < MF<MS>::CREGS; ++i) out.v[cb][i] = fn(in.v[cb][i]);
+}
+
+template <int MS, int C, class F>
+__device__ __forceinline__ void cvmap2(CVec<MS, C>& out, const CVec<MS, C>& a, const CVec<MS, C>& b, F fn) {
+#pragma unroll
+  for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+    for (int i = 0; i < MF<MS>::CREGS; ++i) out.v[cb][i] = fn(a.v[cb][i], b.v[cb][i]);
+}
+
+// out[r, c] = fn(t[r, c], v[c]).
+template <int MS, int R, int C, class F>
+__device__ __forceinline__ void col_apply(RTile<MS, R, C>& out, const RTile<MS, R, C>& t, const CVec<MS, C>& v, F fn) {
+#pragma unroll
+  for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < out.RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < MF<MS>::CREGS; ++i) out.f[cb][rb][i] = fn(t.f[cb][rb][i], v.v[cb][i]);
+}
+
+// Per-column values from an fp32 vector global [b, d, n] (unit column):
+// columns col0.. of this wavefront's tile; indices >= n read 0.
+template <int MS, int C>
+__device__ __forceinline__ void load_cvec(CVec<MS, C>& out, const gl<float>& g, int b, int d, int col0) {
+  const int lh = lane_id() / MS;
+  const bool bd_ok = (unsigned)b < (unsigned)g.b && (unsigned)d < (unsigned)g.d;
+  const float* base = g.data + (long long)b * g.sb + (long long)d * g.sd;
+#pragma unroll
+  for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+    for (int q = 0; q < MF<MS>::CREGS / 4; ++q) {
+      const int c = col0 + cb * MS + ccol<MS>(4 * q, lh);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        out.v[cb][4 * q + j] = (bd_ok && c + j < g.r) ? base[(long long)(c + j) * g.sr] : 0.f;
+    }
+}
+
+// Per-row values from an fp32 vector global [b, d, n]: rows row0.. of this
+// wavefront's tile (one per row block and lane); indices >= n read 0.
+template <int MS, int R>
+__device__ __forceinline__ void load_rvec(RVec<MS, R>& out, const gl<float>& g, int b, int d, int row0) {
+  const bool bd_ok = (unsigned)b < (unsigned)g.b && (unsigned)d < (unsigned)g.d;
+  const float* base = g.data + (long long)b * g.sb + (long long)d * g.sd;
+#pragma unroll
+  for (int rb = 0; rb < out.RB; ++rb) {
+    const int r = row0 + rb * MS + lane_id() % MS;
+    out.v[rb] = (bd_ok && r < g.r) ? base[(long long)r * g.sr] : 0.f;
+  }
+}
+
+// bf16 LDS tile -> fp32 register tile (lane = row layout): rows row0..,
+// columns col0.. of the tile.
+template <class Tile, int MS, int R, int C>
+__device__ __forceinline__ void load_tile(RTile<MS, R, C>& out, char* tile_base, int row0, int col0) {
+  const int lane = lane_id();
+  const int lr = lane % MS, lh = lane / MS;
+#pragma unroll
+  for (int rb = 0; rb < out.RB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+      for (int q = 0; q < MF<MS>::CREGS / 4; ++q) {
+        const bf16x4 v = row_operand4<Tile>(tile_base, row0 + rb * MS + lr, col0 + cb * MS + ccol<MS>(4 * q, lh));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out.f[cb][rb][4 * q + j] = (float)v[j];
+      }
 }
 
 template <int MS, int R, class F>

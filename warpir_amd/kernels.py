@@ -11,7 +11,8 @@ from typing import Callable, Dict
 
 from warpir_amd.ir import Kernel
 from warpir_amd.passes.modulo_scheduler import gfx950_attention_cost_model, gfx950_cost_model, kernel_pass
-from warpir_amd.workloads import build_attention_kernel, build_gemm_kernel, build_mha_forward_kernel
+from warpir_amd.workloads import (build_attention_kernel, build_gemm_kernel, build_mha_bwd_dkdv_kernel,
+                                  build_mha_bwd_dq_kernel, build_mha_bwd_prep_kernel, build_mha_forward_kernel)
 
 
 def _gemm_mi355x(block_k: int = 32, block_m: int = 256, block_n: int = 256, wave_m: int = 128,
@@ -60,7 +61,18 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_d64_causal_ssa": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
                                                            causal=True, name="mha_fwd_causal"),
     "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True),
+    # FlashAttention backward: Dv = rowsum(dO * O); query-major dQ; key-major dK, dV.
+    "mha_bwd_prep_d128": lambda: build_mha_bwd_prep_kernel(d=128, block_q=128, wave_rows=32),
+    "mha_bwd_dq_d128": lambda: _bwd(build_mha_bwd_dq_kernel(d=128, block_q=128, block_kv=64, wave_rows=32), 128),
+    "mha_bwd_dkdv_d128": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=128, block_kv=128, block_q=64, wave_rows=32), 128),
+    "mha_bwd_prep_d64": lambda: build_mha_bwd_prep_kernel(d=64, block_q=128, wave_rows=32),
+    "mha_bwd_dq_d64": lambda: _bwd(build_mha_bwd_dq_kernel(d=64, block_q=128, block_kv=64, wave_rows=32), 64),
+    "mha_bwd_dkdv_d64": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=64, block_kv=128, block_q=64, wave_rows=32), 64),
 }
+
+
+def _bwd(kernel: Kernel, d: int) -> Kernel:
+    return kernel_pass(kernel, cost_model=gfx950_attention_cost_model(128, 64, d))
 
 
 def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_budget: int = 64 * 1024,
@@ -69,6 +81,21 @@ def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_
                                  name="mha_fwd_causal" if causal else "mha_fwd")
     return kernel_pass(k, cost_model=gfx950_attention_cost_model(block_q, block_kv, d, lds_budget=lds_budget,
                                                                  min_stages=min_stages))
+
+# Lowering options of variants that differ from the defaults.
+TARGETS: Dict[str, dict] = {
+    # two accumulators + two hoisted fragment sets + four score-sized tiles:
+    # at two waves per SIMD the D=64 key-major backward spills
+    "mha_bwd_dkdv_d64": {"waves_per_eu": 1},
+}
+
+
+def lowerer(name: str):
+    """The ``CDNA4Lowerer`` variant *name* is built with."""
+    from warpir_amd.lowering import CDNA4Lowerer, CDNA4Target
+
+    return CDNA4Lowerer(CDNA4Target(**TARGETS.get(name, {})))
+
 
 _handles: Dict[str, object] = {}
 
@@ -82,7 +109,7 @@ def handle(name: str):
     from warpir_amd.runtime import compile_kernel
 
     if name not in _handles:
-        _handles[name] = compile_kernel(VARIANTS[name]())
+        _handles[name] = compile_kernel(VARIANTS[name](), lowerer(name))
     return _handles[name]
 
 
@@ -93,12 +120,11 @@ def build_all(verbose: bool = False, prune: bool = True) -> Dict[str, str]:
     """
     import os
 
-    from warpir_amd.lowering import CDNA4Lowerer
     from warpir_amd.runtime import CACHE_DIR, compile_source, resource_usage
 
     out = {}
     for name, make in VARIANTS.items():
-        src = CDNA4Lowerer().lower(make())
+        src = lowerer(name).lower(make())
         out[name] = compile_source(src, force=True)
         if verbose:
             u = resource_usage(src)

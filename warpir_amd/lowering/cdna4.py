@@ -46,13 +46,13 @@ from typing import Dict, List, Optional, Sequence, Tuple, Union
 
 from warpir_amd.ir.ops import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, CopyOp, DivRowOp, Exp2Op, ForOp,
-    IntAffineOp, Kernel, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp, NegInftyOp,
-    Op, RowMaxOp, RowSumOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
+    IntAffineOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp, NegInftyOp,
+    Op, RowMaxOp, RowSumOp, SubColOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
     WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
 from warpir_amd.ir.ops import SlotViewOp
 from warpir_amd.ir.types import (
-    ColVecType, GPUType, GlobalType, IntType, RegTileType, ScalarType, SharedBufferType,
+    ColVecType, GPUType, GlobalType, IntType, RegTileType, RowVecType, ScalarType, SharedBufferType,
     SharedTileType,
 )
 
@@ -236,7 +236,7 @@ class CDNA4Lowerer:
     def _geometry(self, kernel: Kernel) -> _Geometry:
         mmas = [op for op in _walk(kernel.body) if isinstance(op, (MMAOp, MMABufOp))]
         if not mmas:
-            raise LoweringError("kernel has no MMA: nothing sets the wavefront layout")
+            return self._geometry_from_copies(kernel)
         nw = nw_c = None
         dims = []
         for op in mmas:
@@ -275,25 +275,74 @@ class CDNA4Lowerer:
             raise LoweringError(f"register tiles {sorted(set(dims))} are not multiples of the MFMA shape {ms}")
         if nw * 64 > 1024:
             raise LoweringError(f"{nw} wavefronts exceed the 1024-thread workgroup limit")
-        wpe = self.target.waves_per_eu
-        if wpe is None:
+        return _Geometry(nw=nw, nw_c=nw_c, ms=ms, waves_per_eu=self._waves_per_eu(kernel))
+
+    def _waves_per_eu(self, kernel: Kernel) -> int:
+        """1 when the loop-carried fp32 register tiles (accumulators) and the
+        loop-invariant MMA fragments of one wavefront need more than 96
+        registers per lane, else 2 (GEMM 128x128 waves: 128 -> 1; 64x64: 64
+        -> 2; FA forward: 64 + 32 -> 2; FA backward dQ: 64 + 64 -> 1)."""
+        if self.target.waves_per_eu is not None:
+            return self.target.waves_per_eu
+        acc_regs = 0
+        for op in _walk(kernel.body):
+            if isinstance(op, ForOp):
+                carried = sum(ia.block_arg.type.rows * ia.block_arg.type.cols // 64 for ia in op.iter_args
+                              if isinstance(ia.block_arg.type, RegTileType)
+                              and ia.block_arg.type.data_type == GPUType.fp32)
+                # loop-invariant MMA row operands are kept as bf16 fragments in registers
+                loaded = {o.result.name for o in _walk(op.body) if isinstance(o, TMALoadOp)}
+                hoisted = {}
+                for o in _walk(op.body):
+                    if isinstance(o, MMAOp) and o.transpose_b and isinstance(o.a.type, SharedTileType) \
+                            and o.a.name not in loaded:
+                        hoisted[o.a.name] = o.result.type.rows * o.a.type.cols // 128
+                acc_regs = max(acc_regs, carried + sum(hoisted.values()))
+        if acc_regs == 0:   # no loop: the largest fp32 register tile
             acc_regs = max((v.type.rows * v.type.cols // 64
                             for op in _walk(kernel.body) for v in _values_in(vars(op).get("result"))
                             if isinstance(v.type, RegTileType) and v.type.data_type == GPUType.fp32),
                            default=0)
-            wpe = 1 if acc_regs > 64 else 2
-        return _Geometry(nw=nw, nw_c=nw_c, ms=ms, waves_per_eu=wpe)
+        return 1 if acc_regs > 96 else 2
+
+    def _geometry_from_copies(self, kernel: Kernel) -> _Geometry:
+        """Wavefront layout of an MMA-free kernel from its shared -> register
+        copies: the block tile split into the register tile's wave slices."""
+        nw = nw_c = None
+        dims = []
+        for op in _walk(kernel.body):
+            if isinstance(op, CopyOp) and isinstance(op.input.type, SharedTileType) \
+                    and isinstance(op.result.type, RegTileType):
+                sh, rg = op.input.type, op.result.type
+                if sh.rows % rg.rows or sh.cols % rg.cols:
+                    raise LoweringError(f"copy {op.result.name}: {sh.rows}x{sh.cols} does not split into "
+                                        f"{rg.rows}x{rg.cols}")
+                this = (sh.rows // rg.rows * (sh.cols // rg.cols), sh.cols // rg.cols)
+                if nw is not None and (nw, nw_c) != this:
+                    raise LoweringError("copies disagree on the wavefront layout")
+                nw, nw_c = this
+                dims += [rg.rows, rg.cols]
+        if nw is None:
+            raise LoweringError("kernel has no MMA and no shared -> register copy: wavefront count unknown")
+        ms = self.target.mfma or (32 if all(d % 32 == 0 for d in dims) else 16)
+        return _Geometry(nw=nw, nw_c=nw_c, ms=ms, waves_per_eu=self._waves_per_eu(kernel))
 
     def _assign_roles(self, ops) -> None:
         """ROWREAD for tiles read along k by rows, TRREAD for [K][N] tiles read across k."""
         def use(v: Value, role: int) -> None:
+            # A tile read both by rows and transposed (e.g. K in attention
+            # backward) takes the TRREAD swizzle: every read is correct under
+            # either swizzle, and the transposed reads are twice as many
+            # instructions per byte, so they get the conflict-free layout.
             key = self._lds_key(v)
             if key is None:
                 return
             if self.roles.setdefault(key, role) != role:
-                raise LoweringError(f"shared tile {v.name} is read both by rows and transposed")
+                self.roles[key] = TRREAD
 
         for op in _walk(ops):
+            if isinstance(op, CopyOp) and isinstance(op.input.type, SharedTileType):
+                use(op.input, ROWREAD)
             if isinstance(op, MMAOp):
                 use(op.a, ROWREAD)
                 use(op.b, ROWREAD if op.transpose_b else TRREAD)
@@ -445,6 +494,8 @@ class CDNA4Lowerer:
             return f"wir::{kind}<{ms}, {t.rows}, {t.cols}>"
         if isinstance(t, ColVecType):
             return f"wir::RVec<{ms}, {t.rows}>"
+        if isinstance(t, RowVecType):
+            return f"wir::CVec<{ms}, {t.cols}>"
         return None
 
     # ------------------------------------------------------------------
@@ -546,6 +597,12 @@ class CDNA4Lowerer:
             return
         if isinstance(op, CopyOp):
             rt, it = op.result.type, op.input.type
+            if isinstance(it, SharedTileType) and isinstance(rt, RegTileType):
+                if rt.data_type != GPUType.fp32:
+                    raise LoweringError("a shared -> register copy produces an fp32 register tile")
+                ptr, key = self._tile_ptr(op.input)
+                w(f"{pad}wir::load_tile<{self.stile(key)}>({self._var(op.result)}, {ptr}, wave_row0, wave_col0);")
+                return
             if isinstance(rt, RegTileType) and isinstance(it, RegTileType) and rt.data_type != it.data_type:
                 if it.data_type != GPUType.fp32:
                     raise LoweringError("only fp32 -> bf16 register conversion is supported")
@@ -560,11 +617,12 @@ class CDNA4Lowerer:
                 w(f"{pad}wir::map({self._var(op.result)}, {self._var(op.input)}, "
                   f"[](float x, int) {{ return {fn}; }});")
             else:
-                w(f"{pad}wir::vmap({self._var(op.result)}, {self._var(op.input)}, [](float x) {{ return {fn}; }});")
+                vm = "cvmap" if isinstance(op.result.type, RowVecType) else "vmap"
+                w(f"{pad}wir::{vm}({self._var(op.result)}, {self._var(op.input)}, [](float x) {{ return {fn}; }});")
             return
         if isinstance(op, (SubOp, MulOp, AddOp)):
             sym = {SubOp: "-", MulOp: "*", AddOp: "+"}[type(op)]
-            fn = "map2" if isinstance(op.result.type, RegTileType) else "vmap2"
+            fn = {RegTileType: "map2", RowVecType: "cvmap2"}.get(type(op.result.type), "vmap2")
             w(f"{pad}wir::{fn}({self._var(op.result)}, {self._var(op.a)}, {self._var(op.b)}, "
               f"[](float a, float b) {{ return a {sym} b; }});")
             return
@@ -584,6 +642,24 @@ class CDNA4Lowerer:
                 return
             w(f"{pad}wir::row_apply({self._var(op.result)}, {self._var(op.tile)}, {self._var(op.vec)}, "
               f"[](float x, float s) {{ return x - s; }});")
+            return
+        if isinstance(op, SubColOp):
+            w(f"{pad}wir::col_apply({self._var(op.result)}, {self._var(op.tile)}, {self._var(op.vec)}, "
+              f"[](float x, float s) {{ return x - s; }});")
+            return
+        if isinstance(op, LoadVecOp):
+            src = op.source
+            if src.type.data_type != GPUType.fp32 or src.type.sub_tile_type.cols != 1:
+                raise LoweringError(f"load_vec reads an fp32 global with L x 1 sub tiles, not {src.type}")
+            n = src.type.sub_tile_type.rows
+            b, d, rt, _ct = (self._int(c) for c in op.coords)
+            g = f"globals.{_cname(src.name)[2:]}"
+            if isinstance(op.result.type, RowVecType):
+                w(f"{pad}wir::load_cvec({self._var(op.result)}, {g}, {b}, {d}, ({rt}) * {n} + wave_col0);")
+            elif isinstance(op.result.type, ColVecType):
+                w(f"{pad}wir::load_rvec({self._var(op.result)}, {g}, {b}, {d}, ({rt}) * {n} + wave_row0);")
+            else:
+                raise LoweringError(f"load_vec into {op.result.type}")
             return
         if isinstance(op, CausalMaskOp):
             t = op.tile.type
@@ -1123,19 +1199,22 @@ class CDNA4Lowerer:
                 "}", ""]
         return "\n".join(src + body + tail)
 
-    def _wave_rows(self) -> int:
+    def _wave_tile(self) -> RegTileType:
+        """The register tile shape that sets the wavefront slices: the first
+        MMA's result, or in an MMA-free kernel the first shared -> register copy."""
         for op in _walk(self.kernel.body):
             if isinstance(op, (MMAOp, MMABufOp)):
-                t = op.result.type if isinstance(op.result.type, RegTileType) else self._rtype(op.accum)
-                return t.rows
-        raise LoweringError("no MMA")
+                return op.result.type if isinstance(op.result.type, RegTileType) else self._rtype(op.accum)
+        for op in _walk(self.kernel.body):
+            if isinstance(op, CopyOp) and isinstance(op.input.type, SharedTileType):
+                return op.result.type
+        raise LoweringError("no MMA and no shared -> register copy")
+
+    def _wave_rows(self) -> int:
+        return self._wave_tile().rows
 
     def _wave_cols(self) -> int:
-        for op in _walk(self.kernel.body):
-            if isinstance(op, (MMAOp, MMABufOp)):
-                t = op.result.type if isinstance(op.result.type, RegTileType) else self._rtype(op.accum)
-                return t.cols
-        raise LoweringError("no MMA")
+        return self._wave_tile().cols
 
 
 # ----------------------------------------------------------------------
