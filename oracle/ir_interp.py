@@ -22,7 +22,8 @@ pipelined IR relies on it (``warpir/lowering/lowering.py``):
   to bf16; a ``CopyOp`` of a shared tile into a register tile is a plain
   read (the tile is already fp32 here);
 * ``LoadVecOp`` reads ``L`` consecutive rows of an ``L x 1``-tiled global
-  (zeros outside), as a block-level vector: a col_vec's length is its
+  (zeros outside), or with no coordinates the fp32 ``L x 1`` shared tile
+  it names, as a block-level vector: a col_vec's length is its
   block's rows, a row_vec's its tile's columns; ``SubColOp`` subtracts a
   row_vec from every row.
 
@@ -226,6 +227,8 @@ class Interpreter:
             s(op.result, self._int(op.input) * op.mul + op.add)
         elif isinstance(op, SubColOp):
             s(op.result, g(op.tile) - g(op.vec).reshape(1, -1))
+        elif isinstance(op, LoadVecOp) and not op.coords:
+            s(op.result, g(op.source)[:, 0].clone())   # from an fp32 L x 1 shared tile
         elif isinstance(op, LoadVecOp):
             gl = _as4d(self.tensors[op.source.name], op.source.type)
             n = op.source.type.sub_tile_type.rows

@@ -155,6 +155,12 @@ __device__ __forceinline__ void dma16_v(const void* gaddr, unsigned lds_addr) {
 }
 #pragma clang diagnostic pop
 
+// 4 bytes per lane, per-lane 64-bit address (lane l writes M0 + 4*l).
+__device__ __forceinline__ void dma4_v(const void* gaddr, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(gaddr), "s"(lds_addr) : "memory", "m0");
+}
+
 __device__ __forceinline__ unsigned lds_addr(char* p) {
   return (unsigned)(size_t)(lds_char*)p;
 }
@@ -239,6 +245,29 @@ struct Loader {
   // Whether `g` qualifies for the kernel's ALIGNED specialisation.
   static __device__ __forceinline__ bool aligned(const gl<bf16>& g) {
     return g.r % Tile::ROWS == 0 && g.c % Tile::COLS == 0 && (long long)Tile::ROWS * g.sr < (1ll << 30);
+  }
+};
+
+// fp32 vector tile of N elements in LDS (a per-row statistic such as the
+// log-sum-exp), loaded asynchronously like the bf16 tiles: each of the NW
+// wavefronts issues one global_load_lds_dword moving N / NW elements
+// (lanes beyond that are masked off).  Elements outside the tensor read the
+// zero page.  One DMA instruction per wavefront, the count the lowering
+// uses for its vmcnt waits.
+template <int N, int NW>
+struct VecLoader {
+  static constexpr int PER = N / NW;
+  static_assert(N % NW == 0 && PER <= 64, "vector must split into at most 64 elements per wavefront");
+
+  template <bool ALIGNED>
+  static __device__ __forceinline__ void load(char* tile_base, const gl<float>& g, int b, int d, int row0, int wave) {
+    const int lane = lane_id();
+    const int r = row0 + wave * PER + lane;
+    const bool ok = (unsigned)b < (unsigned)g.b && (unsigned)d < (unsigned)g.d && (unsigned)r < (unsigned)g.r;
+    const float* src = ok ? g.data + (long long)b * g.sb + (long long)d * g.sd + (long long)r * g.sr
+                          : (const float*)zero_page;
+    const unsigned dst = lds_addr(tile_base + wave * PER * 4);
+    if (PER == 64 || lane < PER) dma4_v(src, dst);
   }
 };
 
@@ -834,6 +863,29 @@ __device__ __forceinline__ void load_rvec(RVec<MS, R>& out, const gl<float>& g, 
     const int r = row0 + rb * MS + lane_id() % MS;
     out.v[rb] = (bd_ok && r < g.r) ? base[(long long)r * g.sr] : 0.f;
   }
+}
+
+// Per-column / per-row values from an fp32 vector tile in LDS (see load_cvec
+// and load_rvec for the register layout).
+template <int MS, int C>
+__device__ __forceinline__ void load_cvec_lds(CVec<MS, C>& out, char* vec_base, int col0) {
+  const int lh = lane_id() / MS;
+#pragma unroll
+  for (int cb = 0; cb < out.CB; ++cb)
+#pragma unroll
+    for (int q = 0; q < MF<MS>::CREGS / 4; ++q) {
+      const int c = col0 + cb * MS + ccol<MS>(4 * q, lh);
+      const f32x4 v = *(__attribute__((address_space(3))) f32x4*)(lds(vec_base) + c * 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out.v[cb][4 * q + j] = v[j];
+    }
+}
+
+template <int MS, int R>
+__device__ __forceinline__ void load_rvec_lds(RVec<MS, R>& out, char* vec_base, int row0) {
+#pragma unroll
+  for (int rb = 0; rb < out.RB; ++rb)
+    out.v[rb] = *(__attribute__((address_space(3))) float*)(lds(vec_base) + (row0 + rb * MS + lane_id() % MS) * 4);
 }
 
 // bf16 LDS tile -> fp32 register tile (lane = row layout): rows row0..,

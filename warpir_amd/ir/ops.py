@@ -273,7 +273,10 @@ class LoadVecOp(Op):
     """*Additive.* Synchronous load of a register vector from an fp32 global.
 
     The global's sub tile is ``L x 1``; ``coords = (batch, depth, tile, 0)``
-    select elements ``tile*L .. tile*L + L - 1`` along its rows.  A col_vec
+    select elements ``tile*L .. tile*L + L - 1`` along its rows.  With a
+    shared fp32 ``L x 1`` tile as ``source`` (loaded by ``tma_load`` like any
+    tile, so it can be pipelined) and empty ``coords``, the vector is read
+    from that tile.  A col_vec
     result takes them as per-row values of its tile, a row_vec result as
     per-column values.  Elements outside the tensor read 0.  (Statistics
     saved by the forward pass, e.g. the log-sum-exp, for the backward.)

@@ -382,11 +382,11 @@ class CDNA4Lowerer:
                 continue
             if key in self.lds_off:
                 continue
-            if t.data_type != GPUType.bf16:
-                raise LoweringError(f"shared tile {key} must be bf16")
+            if t.data_type != GPUType.bf16 and not _is_vec_tile(t):
+                raise LoweringError(f"shared tile {key} must be bf16 (or an fp32 L x 1 vector)")
             self.roles.setdefault(key, ROWREAD)
             self.lds_off[key] = off
-            off += _align(t.rows * t.cols * 2, 1024) * count
+            off += _tile_bytes(t) * count
         self.lds_total = off
         if off > self.target.lds_bytes:
             raise LoweringError(f"LDS use {off} B exceeds the {self.target.lds_bytes} B per workgroup")
@@ -434,6 +434,11 @@ class CDNA4Lowerer:
         return f"wir::STile<{t.rows}, {t.cols}, {self.roles.get(key, ROWREAD)}>"
 
     def loads_per_wave(self, tile: SharedTileType) -> int:
+        if _is_vec_tile(tile):   # one global_load_lds_dword per wavefront
+            if tile.rows % self.geo.nw or tile.rows // self.geo.nw > 64:
+                raise LoweringError(f"vector tile {tile}: {tile.rows} elements do not split into "
+                                    f"{self.geo.nw} wavefronts of at most 64")
+            return 1
         chunks = tile.rows * tile.cols * 2 // 16
         if chunks % 64:
             raise LoweringError(f"tile {tile} is not a multiple of 1 KiB (64 LDS-DMA chunks)")
@@ -470,8 +475,7 @@ class CDNA4Lowerer:
         view = self._views().get(name)
         if view is not None:
             key = self.resolve(view.buf.name)
-            t = self.tile_type_of(key)
-            stride = _align(t.rows * t.cols * 2, 1024)
+            stride = _tile_bytes(self.tile_type_of(key))
             return f"(smem + {self.lds_off[key]} + {self._slot(view.slot)} * {stride})", key
         if name not in self.lds_off:
             raise LoweringError(f"{v.name} is not a shared tile")
@@ -479,8 +483,7 @@ class CDNA4Lowerer:
 
     def _buf_ptr(self, buf: Value, slot) -> Tuple[str, str]:
         key = self.resolve(buf.name)
-        t = self.tile_type_of(key)
-        stride = _align(t.rows * t.cols * 2, 1024)
+        stride = _tile_bytes(self.tile_type_of(key))
         return f"(smem + {self.lds_off[key]} + {self._slot(slot)} * {stride})", key
 
     def _var(self, v: Value) -> str:
@@ -647,6 +650,15 @@ class CDNA4Lowerer:
             w(f"{pad}wir::col_apply({self._var(op.result)}, {self._var(op.tile)}, {self._var(op.vec)}, "
               f"[](float x, float s) {{ return x - s; }});")
             return
+        if isinstance(op, LoadVecOp) and isinstance(op.source.type, SharedTileType):
+            ptr, _key = self._tile_ptr(op.source)
+            if isinstance(op.result.type, RowVecType):
+                w(f"{pad}wir::load_cvec_lds({self._var(op.result)}, {ptr}, wave_col0);")
+            elif isinstance(op.result.type, ColVecType):
+                w(f"{pad}wir::load_rvec_lds({self._var(op.result)}, {ptr}, wave_row0);")
+            else:
+                raise LoweringError(f"load_vec into {op.result.type}")
+            return
         if isinstance(op, LoadVecOp):
             src = op.source
             if src.type.data_type != GPUType.fp32 or src.type.sub_tile_type.cols != 1:
@@ -682,6 +694,10 @@ class CDNA4Lowerer:
         src = op.source
         sub = src.type.sub_tile_type
         b, d, rt, ct = (self._int(c) for c in op.coords)
+        t = self.tile_type_of(key)
+        if _is_vec_tile(t):
+            return (f"wir::VecLoader<{t.rows}, {self.geo.nw}>::{fn}{ptr}, globals.{_cname(src.name)[2:]}, "
+                    f"{b}, {d}, ({rt}) * {sub.rows}, wir_wave")
         self._aligned_checks.add((self.stile(key), _cname(src.name)[2:]))
         return (f"wir::Loader<{self.stile(key)}, {self.geo.nw}>::{fn}{ptr}, globals.{_cname(src.name)[2:]}, "
                 f"{b}, {d}, ({rt}) * {sub.rows}, ({ct}) * {sub.cols}, wir_wave")
@@ -1369,6 +1385,18 @@ def _as4d(shape) -> Tuple[int, int, int, int]:
     while len(s) < 4:
         s = (1,) + s
     return s
+
+
+def _is_vec_tile(t) -> bool:
+    """An fp32 ``L x 1`` shared tile: a vector (e.g. per-query statistics) in LDS."""
+    return isinstance(t, SharedTileType) and t.data_type == GPUType.fp32 and t.cols == 1
+
+
+def _tile_bytes(t) -> int:
+    """LDS bytes of one shared tile (ring slot stride)."""
+    if _is_vec_tile(t):
+        return _align(t.rows * 4, 256)
+    return _align(t.rows * t.cols * 2, 1024)
 
 
 def _align(x: int, a: int) -> int:

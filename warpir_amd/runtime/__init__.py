@@ -280,7 +280,11 @@ class KernelHandle:
                     raise ValueError("all tensors must be on one device")
                 shape, strides = _global_view(v, x)
                 esz = x.element_size()
-                if v.name in self._loaded_globals or shape[3] > 1:
+                vector = v.type.data_type == GPUType.fp32 and v.type.sub_tile_type.cols == 1
+                if vector:   # fp32 L x 1 vectors move 4 bytes per lane
+                    if x.data_ptr() % 4:
+                        raise ValueError(f"{v.name}: must be 4-byte aligned")
+                elif v.name in self._loaded_globals or shape[3] > 1:
                     if x.data_ptr() % 16 or (strides[2] * esz) % 16 or (shape[3] * esz) % 16:
                         raise ValueError(f"{v.name}: rows must be 16-byte aligned and a multiple of 16 bytes "
                                          "(the tile-load granule)")

@@ -378,7 +378,8 @@ def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 
     """``dK`` and ``dV`` of attention forward, key-major: one program per key
     tile ``(blockIdx.x, head, batch)``; the loop walks query tiles.  Scores
     are computed transposed (``S^T = K Q^T``), so the per-query LSE and Dv
-    are row_vecs loaded per query tile."""
+    are row_vecs, read from fp32 ``block_q x 1`` shared tiles that are loaded
+    (and pipelined) with the query tile."""
     scale = 1.0 / math.sqrt(d)
     kv_glob, vec_glob, kv_tile = _bwd_globals(d, block_kv)
     q_glob, qvec_glob, q_tile = _bwd_globals(d, block_q)
@@ -397,6 +398,8 @@ def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 
         return Value(n, t)
 
     k_sh, v_sh, q_sh, do_sh = v("k_shared", kv_tile), v("v_shared", kv_tile), v("q_shared", q_tile), v("do_shared", q_tile)
+    qvec_tile = qvec_glob.sub_tile_type
+    lse_sh, dv_sh = v("lse_shared", qvec_tile), v("dvec_shared", qvec_tile)
     i = v("i", IntType())
     lse, lse2, dvec = v("lse", rvec), v("lse_log2", rvec), v("d_vec", rvec)
     dk_init, dk_acc, dk_new, dk_final, dk_out = (v(n, acc) for n in ("dk_init", "dk_accum", "dk_new", "dk_final", "dk_out"))
@@ -410,9 +413,11 @@ def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 
         body=(
             TMALoadOp(result=q_sh, source=Q, coords=(*bh, i, 0)),
             TMALoadOp(result=do_sh, source=dO, coords=(*bh, i, 0)),
-            WaitOp(values=(q_sh, do_sh)),
-            LoadVecOp(result=lse, source=L, coords=(*bh, i, 0)),
-            LoadVecOp(result=dvec, source=Dv, coords=(*bh, i, 0)),
+            TMALoadOp(result=lse_sh, source=L, coords=(*bh, i, 0)),
+            TMALoadOp(result=dv_sh, source=Dv, coords=(*bh, i, 0)),
+            WaitOp(values=(q_sh, do_sh, lse_sh, dv_sh)),
+            LoadVecOp(result=lse, source=lse_sh, coords=()),
+            LoadVecOp(result=dvec, source=dv_sh, coords=()),
             ZeroOp(result=zero),
             MMAOp(result=st, a=k_sh, b=q_sh, accum=zero, transpose_b=True),
             MulScalarOp(result=st_sc, input=st, scalar=scale * LOG2E),
