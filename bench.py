@@ -170,7 +170,8 @@ def bench_extra(steps: int, warmup: int):
 
     GEMM 4096^3 (config 2), skinny GEMM M=128 N=K=8192 (config 3', judged
     on the HBM roofline: 2(MK+KN+MN) bytes), causal FA B8 H32 S8192 D64
-    (config 5, matmul flops halved for the mask).
+    (config 5, matmul flops halved for the mask), and FlashAttention
+    backward at the config-4 shape (prep + dQ + dK/dV kernels).
     """
     import torch
 
@@ -203,6 +204,20 @@ def bench_extra(steps: int, warmup: int):
     tf = api.attention_flops(bsz, heads, seq, d, causal=True) / (ms * 1e-3) / 1e12
     out["fa_fwd_causal_b8_h32_s8192_d64"] = {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
                                              "kernel": "mha_d64_causal"}
+    del q, k, v, o, lse
+    # FlashAttention backward at the config-4 shape (next step after the forward)
+    bsz, heads, seq, d = 16, 16, 4096, 128
+    q, k, v, do = (seeded_normal((bsz, heads, seq, d), s).cuda() for s in (10, 11, 12, 13))
+    o, lse = api.attention_forward(q, k, v)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
+    ms, _ = _time_launches(lambda: api.attention_backward(q, k, v, o, lse, do, dq, dk, dv, dvec),
+                           max(3, steps // 2), max(1, warmup // 2), stream)
+    tf = api.attention_backward_flops(bsz, heads, seq, d) / (ms * 1e-3) / 1e12
+    out["fa_bwd_b16_h16_s4096_d128"] = {
+        "ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
+        "kernels": ["mha_bwd_prep_d128", "mha_bwd_dq_d128", "mha_bwd_dkdv_d128"],
+        "flops": "10*B*H*S^2*D (the five S x S x D products); the kernels run seven (dQ recomputes S and dP)"}
     return out
 
 
