@@ -1,0 +1,164 @@
+"""register_counter and memory_annotator passes (CPU).
+
+Pins (beyond restating the passes):
+* register_counter's waves-per-SIMD choice is checked against what hipcc
+  does with the generated code: every variant it gives two waves compiles
+  under the two-wave register limit (256 per lane) with no VGPR spill, and
+  every variant it gives one wave really uses more than 256 registers per
+  lane (VGPRs + AGPRs) when allowed the whole file -- i.e. two waves would
+  have forced spills.  Numbers come from hipcc's kernel-resource-usage
+  remarks for the gfx950 build.
+* hand-derived footprints of the reference GEMM and attention kernels.
+* memory_annotator: removing every ``wait`` from the hand-written kernels
+  and re-annotating gives kernels that pass the wait checker, whose loop
+  bodies match the hand-written ones after pipelining, and that are
+  idempotent under a second pass; a kernel missing a wait is rejected.
+"""
+import dataclasses
+import os
+import shutil
+
+import pytest
+
+from warpir_amd import kernels, workloads
+from warpir_amd.ir import ForOp, WaitOp
+from warpir_amd.passes.memory_annotator import (MissingWaitError, check_memory_annotations,
+                                                process_memory_annotations)
+from warpir_amd.passes.modulo_scheduler import gfx950_attention_cost_model, kernel_pass
+from warpir_amd.passes.register_counter import OVERHEAD, count_registers, value_registers
+from warpir_amd.printing.printer import format_kernel
+
+HAVE_HIPCC = shutil.which("hipcc") is not None or os.path.exists("/opt/rocm/bin/hipcc")
+
+
+# ---------------------------------------------------------------------------
+# register_counter
+# ---------------------------------------------------------------------------
+def test_value_registers_layout():
+    from warpir_amd.ir import ColVecType, GPUType, RegTileType, RowVecType
+    assert value_registers(RegTileType(GPUType.fp32, 32, 128)) == 64      # 4096 fp32 / 64 lanes
+    assert value_registers(RegTileType(GPUType.bf16, 32, 64)) == 16       # 2048 bf16, two per register
+    assert value_registers(ColVecType(GPUType.fp32, 32, 64)) == 1         # one row per lane
+    assert value_registers(RowVecType(GPUType.fp32, 32, 64)) == 32        # 16 of every 32 columns per lane
+
+
+def test_reference_gemm_footprint_by_hand():
+    # reference GEMM: per wave a 16x64 fp32 accumulator = 16 registers; the
+    # MMA result, the yield and the loop result share its storage (the MFMA
+    # accumulates in place), so nothing else is live.
+    r = count_registers(workloads.build_gemm_kernel())
+    assert r.peak == 16
+    assert r.waves_per_simd == 2
+
+
+def test_reference_attention_footprint_by_hand():
+    # 16x64 fp32 O accumulator (16) + max/norm col vectors (1 each), plus at
+    # the busiest point the 16x64 score tile and its successors; the hoisted
+    # Q fragments are 16 rows x 64 cols bf16 = 8 registers.
+    r = count_registers(workloads.build_attention_kernel())
+    assert r.hoisted == {"q_shared": 8}
+    assert 16 + 2 + 8 < r.peak < 128
+    assert r.waves_per_simd == 2
+
+
+@pytest.mark.skipif(not HAVE_HIPCC, reason="hipcc not available")
+@pytest.mark.parametrize("name", sorted(kernels.VARIANTS))
+def test_waves_choice_matches_hipcc(name):
+    from warpir_amd.runtime import compile_source, resource_usage
+    kern = kernels.kernel(name)
+    report = count_registers(kern)
+    src = kernels.lowerer(name).lower(kern)
+    compile_source(src)
+    usage = resource_usage(src)
+    assert usage, "no resource-usage remarks in the compile log"
+    assert usage["occupancy"] >= report.waves_per_simd
+    if report.waves_per_simd == 2:
+        assert usage["vgpr"] + usage.get("agpr", 0) <= 256
+        assert usage.get("vgpr_spill", 0) == 0
+    else:
+        assert usage["vgpr"] + usage.get("agpr", 0) > 256, usage
+
+
+def test_counter_drives_lowering_launch_bounds():
+    src_gemm = kernels.lowerer("gemm_256_k64").lower(kernels.kernel("gemm_256_k64"))
+    src_mha = kernels.lowerer("mha_d128").lower(kernels.kernel("mha_d128"))
+    assert count_registers(kernels.kernel("gemm_256_k64")).need > 256
+    assert "amdgpu_waves_per_eu(1" in src_gemm
+    assert count_registers(kernels.kernel("mha_d128")).need <= 256
+    assert "amdgpu_waves_per_eu(2" in src_mha
+    assert OVERHEAD > 0
+
+
+# ---------------------------------------------------------------------------
+# memory_annotator
+# ---------------------------------------------------------------------------
+def _strip(ops):
+    out = []
+    for op in ops:
+        if isinstance(op, WaitOp):
+            continue
+        if isinstance(op, ForOp):
+            op = dataclasses.replace(op, body=tuple(_strip(op.body)))
+        out.append(op)
+    return tuple(out)
+
+
+_BUILDERS = {
+    "gemm": (workloads.build_gemm_kernel, None),
+    "attention": (workloads.build_attention_kernel, None),
+    "mha_d128": (workloads.build_mha_forward_kernel, gfx950_attention_cost_model(128, 64, 128)),
+    "mha_bwd_prep": (workloads.build_mha_bwd_prep_kernel, None),
+    "mha_bwd_dq": (workloads.build_mha_bwd_dq_kernel, gfx950_attention_cost_model(128, 64, 128)),
+    "mha_bwd_dkdv": (workloads.build_mha_bwd_dkdv_kernel, gfx950_attention_cost_model(128, 64, 128)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(_BUILDERS))
+def test_hand_written_kernels_pass_the_checker_and_are_fixed_points(name):
+    k = _BUILDERS[name][0]()
+    check_memory_annotations(k)
+    assert format_kernel(process_memory_annotations(k)) == format_kernel(k)
+
+
+@pytest.mark.parametrize("name", sorted(_BUILDERS))
+def test_stripped_kernels_are_rejected_then_repaired(name):
+    build, cost = _BUILDERS[name]
+    k = build()
+    stripped = dataclasses.replace(k, body=_strip(k.body))
+    with pytest.raises(MissingWaitError):
+        check_memory_annotations(stripped)
+    fixed = process_memory_annotations(stripped)
+    check_memory_annotations(fixed)
+    again = process_memory_annotations(fixed)
+    assert format_kernel(again) == format_kernel(fixed)
+    # each load is waited on exactly once
+    def waited(ops):
+        names = []
+        for op in ops:
+            if isinstance(op, WaitOp):
+                names += [v.name for v in op.values]
+            if isinstance(op, ForOp):
+                names += waited(op.body)
+        return names
+    w = waited(fixed.body)
+    assert sorted(w) == sorted(set(w)) == sorted(waited(k.body))
+    # after pipelining, the loops of the repaired kernel equal the hand-written kernel's
+    if name in ("gemm", "mha_d128", "mha_bwd_dq", "mha_bwd_dkdv"):
+        a, b = kernel_pass(k, cost), kernel_pass(fixed, cost)
+        loops_a = [format_kernel(dataclasses.replace(a, body=(op,))) for op in a.body if isinstance(op, ForOp)]
+        loops_b = [format_kernel(dataclasses.replace(b, body=(op,))) for op in b.body if isinstance(op, ForOp)]
+        assert loops_a and loops_a == loops_b
+
+
+def test_wait_goes_before_first_use_not_after_load():
+    k = workloads.build_attention_kernel()
+    fixed = process_memory_annotations(dataclasses.replace(k, body=_strip(k.body)))
+    loop = next(op for op in fixed.body if isinstance(op, ForOp))
+    kinds = [type(op).__name__ for op in loop.body]
+    first_mma = kinds.index("MMAOp")
+    # the K tile is waited on right before the QK^T MMA, the V tile right before the PV MMA
+    assert kinds[first_mma - 1] == "WaitOp"
+    assert [v.name for v in loop.body[first_mma - 1].values] == ["k_shared"]
+    last_mma = len(kinds) - 1 - kinds[::-1].index("MMAOp")
+    assert kinds[last_mma - 1] == "WaitOp"
+    assert [v.name for v in loop.body[last_mma - 1].values] == ["v_shared"]

@@ -83,11 +83,7 @@ def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_
                                                                  min_stages=min_stages))
 
 # Lowering options of variants that differ from the defaults.
-TARGETS: Dict[str, dict] = {
-    # two accumulators + two hoisted fragment sets + four score-sized tiles:
-    # at two waves per SIMD the D=64 key-major backward spills
-    "mha_bwd_dkdv_d64": {"waves_per_eu": 1},
-}
+TARGETS: Dict[str, dict] = {}
 
 
 def lowerer(name: str):

@@ -70,8 +70,10 @@ class LoweringError(ValueError):
 class CDNA4Target:
     """Machine parameters and code-generation choices for gfx950.
 
-    ``waves_per_eu`` = None picks 1 when a wavefront's accumulators exceed
-    128 registers per lane and 2 otherwise.  ``mfma`` = None picks the
+    ``waves_per_eu`` = None takes the waves per SIMD from the
+    ``register_counter`` pass (2 when a wavefront's estimated footprint fits
+    256 registers per lane, else 1), at least enough for the workgroup's
+    waves on four SIMDs.  ``mfma`` = None picks the
     32x32x16 MFMA when every register tile is a multiple of 32 rows and
     columns, else 16x16x32.
     """
@@ -275,35 +277,14 @@ class CDNA4Lowerer:
             raise LoweringError(f"register tiles {sorted(set(dims))} are not multiples of the MFMA shape {ms}")
         if nw * 64 > 1024:
             raise LoweringError(f"{nw} wavefronts exceed the 1024-thread workgroup limit")
-        return _Geometry(nw=nw, nw_c=nw_c, ms=ms, waves_per_eu=self._waves_per_eu(kernel))
+        return _Geometry(nw=nw, nw_c=nw_c, ms=ms, waves_per_eu=self._waves_for(kernel, nw))
 
-    def _waves_per_eu(self, kernel: Kernel) -> int:
-        """1 when the loop-carried fp32 register tiles (accumulators) and the
-        loop-invariant MMA fragments of one wavefront need more than 96
-        registers per lane, else 2 (GEMM 128x128 waves: 128 -> 1; 64x64: 64
-        -> 2; FA forward: 64 + 32 -> 2; FA backward dQ: 64 + 64 -> 1)."""
+    def _waves_for(self, kernel: Kernel, nw: int) -> int:
         if self.target.waves_per_eu is not None:
             return self.target.waves_per_eu
-        acc_regs = 0
-        for op in _walk(kernel.body):
-            if isinstance(op, ForOp):
-                carried = sum(ia.block_arg.type.rows * ia.block_arg.type.cols // 64 for ia in op.iter_args
-                              if isinstance(ia.block_arg.type, RegTileType)
-                              and ia.block_arg.type.data_type == GPUType.fp32)
-                # loop-invariant MMA row operands are kept as bf16 fragments in registers
-                loaded = {o.result.name for o in _walk(op.body) if isinstance(o, TMALoadOp)}
-                hoisted = {}
-                for o in _walk(op.body):
-                    if isinstance(o, MMAOp) and o.transpose_b and isinstance(o.a.type, SharedTileType) \
-                            and o.a.name not in loaded:
-                        hoisted[o.a.name] = o.result.type.rows * o.a.type.cols // 128
-                acc_regs = max(acc_regs, carried + sum(hoisted.values()))
-        if acc_regs == 0:   # no loop: the largest fp32 register tile
-            acc_regs = max((v.type.rows * v.type.cols // 64
-                            for op in _walk(kernel.body) for v in _values_in(vars(op).get("result"))
-                            if isinstance(v.type, RegTileType) and v.type.data_type == GPUType.fp32),
-                           default=0)
-        return 1 if acc_regs > 96 else 2
+        from warpir_amd.passes.register_counter import count_registers
+
+        return max(count_registers(kernel).waves_per_simd, -(-nw // 4))
 
     def _geometry_from_copies(self, kernel: Kernel) -> _Geometry:
         """Wavefront layout of an MMA-free kernel from its shared -> register
@@ -325,7 +306,7 @@ class CDNA4Lowerer:
         if nw is None:
             raise LoweringError("kernel has no MMA and no shared -> register copy: wavefront count unknown")
         ms = self.target.mfma or (32 if all(d % 32 == 0 for d in dims) else 16)
-        return _Geometry(nw=nw, nw_c=nw_c, ms=ms, waves_per_eu=self._waves_per_eu(kernel))
+        return _Geometry(nw=nw, nw_c=nw_c, ms=ms, waves_per_eu=self._waves_for(kernel, nw))
 
     def _assign_roles(self, ops) -> None:
         """ROWREAD for tiles read along k by rows, TRREAD for [K][N] tiles read across k."""
