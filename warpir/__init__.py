@@ -14,6 +14,7 @@ _ALIASED = (
     "ir", "ir.ops", "ir.types",
     "printing", "printing.printer",
     "passes", "passes.modulo_scheduler", "passes.warp_assigner",
+    "passes.register_counter", "passes.memory_annotator",
     "lowering", "runtime",
 )
 
