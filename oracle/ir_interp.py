@@ -41,7 +41,7 @@ import torch
 from warpir_amd.ir import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, ColVecType, CopyOp, DivRowOp, Exp2Op,
     ForOp, GPUType, IntAffineOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp,
-    NegInftyOp, RegTileType, RowMaxOp, RowSumOp, RowVecType, SlotViewOp, SubColOp, SubOp, SubRowOp,
+    NegInftyOp, RegTileType, RowMaxOp, RowSumOp, RowVecType, SlotViewOp, SubColOp, SubOp, SubRowOp, LazyMaxOp,
     TMALoadBufOp, TMALoadOp, TMAStoreOp, Value, WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
 
@@ -227,6 +227,9 @@ class Interpreter:
             s(op.result, self._int(op.input) * op.mul + op.add)
         elif isinstance(op, SubColOp):
             s(op.result, g(op.tile) - g(op.vec).reshape(1, -1))
+        elif isinstance(op, LazyMaxOp):
+            prev, cand = g(op.prev), g(op.cand)
+            s(op.result, torch.where(cand > prev + op.slack, cand, prev))
         elif isinstance(op, LoadVecOp) and not op.coords:
             s(op.result, g(op.source)[:, 0].clone())   # from an fp32 L x 1 shared tile
         elif isinstance(op, LoadVecOp):

@@ -31,7 +31,7 @@ def test_reference_attention_ir(gpu, n):
     assert rel_err(o.cpu(), ref) <= TOL
 
 
-@pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp"])
+@pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp", "mha_d128_lazy", "mha_d128_ovl"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 1, 64)])
 def test_mha_d128(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")
@@ -43,7 +43,7 @@ def test_mha_d128(gpu, variant, b, h, s):
     assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-3 * ref_lse.abs().max().item() + 1e-3
 
 
-@pytest.mark.parametrize("variant", ["mha_d64_causal", "mha_d64_causal_ssa"])
+@pytest.mark.parametrize("variant", ["mha_d64_causal", "mha_d64_causal_ssa", "mha_d64_causal_lazy", "mha_d64_causal_ovl"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 2, 512), (1, 2, 1024), (1, 1, 192)])
 def test_mha_d64_causal(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")
@@ -51,6 +51,22 @@ def test_mha_d64_causal(gpu, variant, b, h, s):
     o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda(), causal=True, variant=variant)
     torch.cuda.synchronize()
     ref, ref_lse = attention_ref(q, k, v, causal=True)
+    assert rel_err(o.cpu(), ref) <= TOL
+    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-3 * ref_lse.abs().max().item() + 1e-3
+
+
+@pytest.mark.parametrize("variant,d,causal", [("mha_d128_lazy", 128, False), ("mha_d64_causal_lazy", 64, True),
+                                                    ("mha_d128_ovl", 128, False), ("mha_d64_causal_ovl", 64, True)])
+def test_mha_lazy_rescale_with_growing_scores(gpu, variant, d, causal):
+    """Keys grow along the sequence, so the running max moves by more than
+    the slack on later tiles and the rescale path runs too."""
+    b, h, s = 1, 2, 1024
+    announce(f"{variant} growing keys B={b} H={h} S={s}")
+    q, k, v = (seeded_normal((b, h, s, d), sd) for sd in (6, 7, 8))
+    k = (k.float() * torch.linspace(0.5, 6.0, s).view(1, 1, s, 1)).to(torch.bfloat16)
+    o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda(), causal=causal, variant=variant)
+    torch.cuda.synchronize()
+    ref, ref_lse = attention_ref(q, k, v, causal=causal)
     assert rel_err(o.cpu(), ref) <= TOL
     assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-3 * ref_lse.abs().max().item() + 1e-3
 

@@ -81,6 +81,24 @@ def test_attention_hoists_resident_q_fragments():
     assert "mma_ABt_frags" in src and "mma_rAB" in src
 
 
+def test_attention_overlap_form():
+    from warpir_amd.lowering.cdna4 import CDNA4Target
+    plain = CDNA4Lowerer().lower(kernels.kernel("mha_d128"))
+    assert "mma_ABt_frags_slots" not in plain.split('extern "C"')[-1]
+    for name in ("mha_d128_ovl", "mha_d64_causal_ovl"):
+        src = kernels.lowerer(name).lower(kernels.kernel(name))
+        body = src[src.rindex('extern "C" __global__'):]
+        # unaligned tensors keep the plain loop; aligned ones take the pipeline
+        assert "if constexpr (!WIR_AL)" in body
+        assert body.count("wir::mma_ABt_frags_slots") == 3     # unrolled pair + remainder step
+        assert body.count("wir::mma_rAB_slots") == 3
+        assert "wir::e_pairs<0, 16>" in body                   # the peeled last tile
+        assert ("causal_mask" in body) == ("causal" in name)
+    # eight-wave kernels are not matched
+    src = CDNA4Lowerer(CDNA4Target(attn_overlap=True)).lower(kernels.kernel("mha_d128_pp"))
+    assert "mma_ABt_frags_slots" not in src[src.rindex('extern "C" __global__'):]
+
+
 def test_kernarg_layout_matches_globals_struct():
     assert ctypes.sizeof(GL) == 48
     s = kernarg_struct(build_gemm_kernel())

@@ -79,6 +79,37 @@ def test_mha_ir_interpreted_with_lse(causal):
     assert (lse - ref_lse).abs().max().item() <= 1e-3
 
 
+def _mha_interp(q, k, v, causal, slack):
+    b, h, s, d = q.shape
+    o = torch.zeros(b, h, s, d, dtype=torch.bfloat16)
+    lse = torch.zeros(b, h, s, dtype=torch.float32)
+    kern = build_mha_forward_kernel(d=d, block_q=128, block_kv=64, wave_rows=32, causal=causal,
+                                    rescale_slack=slack)
+    run_kernel(kern, {"Q": q, "K": k, "V": v, "O": o, "L": lse}, {"N": s})
+    return o, lse
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_mha_lazy_rescale_interpreted(causal):
+    b, h, s, d = 1, 2, 256, 64
+    q, k, v = (seeded_normal((b, h, s, d), sd) for sd in (3, 4, 5))
+    # keys grow along the sequence, so later tiles raise the row maxima by
+    # more than the slack and the rescale path runs too
+    k = (k.float() * torch.linspace(0.5, 6.0, s).view(1, 1, s, 1)).to(torch.bfloat16)
+    o, lse = _mha_interp(q, k, v, causal, 8.0)
+    ref, ref_lse = attention_ref(q, k, v, causal=causal)
+    assert rel_err(o, ref) <= 1e-2
+    assert (lse - ref_lse).abs().max().item() <= 1e-3
+
+
+def test_lazy_max_with_zero_slack_is_the_plain_max():
+    # cand = max(prev, rowmax) >= prev, so slack 0 selects exactly the running max
+    q, k, v = (seeded_normal((1, 1, 256, 64), sd) for sd in (6, 7, 8))
+    o0, l0 = _mha_interp(q, k, v, False, 0.0)
+    o1, l1 = _mha_interp(q, k, v, False, None)
+    assert torch.equal(o0, o1) and torch.equal(l0, l1)
+
+
 def test_attention_ref_closed_forms():
     s, d = 64, 64
     q = seeded_normal((s, d), 1)

@@ -785,6 +785,134 @@ __device__ __forceinline__ void mma_rAB(RTile<MS, R, C>& acc, const BTile<MS, R,
 }
 
 // ---------------------------------------------------------------------------
+// Software-pipelined attention (the lowering's overlapped form).
+//
+// Per KV tile i the lowering emits S_{i+1} = Q K_{i+1}^T through
+// mma_ABt_frags_slots and O += P_i V_i through mma_rAB_slots, and passes
+// each a `slot` functor.  After every MFMA (group) the functor is called
+// with the group's index as a compile-time constant and issues that slot's
+// share of the work that does not depend on the MFMAs in flight: the
+// softmax of tile i, the running-max update of tile i+1, the DMAs of the
+// next tiles.  sched_barrier pins "MFMA, then its slot's VALU": a wave
+// keeps issuing independent VALU instructions while its MFMA runs (measured
+// on gfx950: up to ~5 per 32-cycle 32x32x16 MFMA at no cost to the MFMA
+// rate), where the unpipelined loop leaves the MFMA pipe idle during the
+// softmax unless the other wave on the SIMD happens to be in its MFMA phase.
+template <int N>
+struct ic {
+  static constexpr int value = N;
+};
+
+template <int T, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (T < N) {
+    f(ic<T>{});
+    static_for<T + 1, N>(f);
+  }
+}
+
+template <int MS, int R, int C, class TB, int KS, class SlotF>
+__device__ __forceinline__ void mma_ABt_frags_slots(RTile<MS, R, C>& acc, const RowFrags<MS, R / MS, KS>& a,
+                                                    char* b_base, int b_row0, SlotF&& slot) {
+  static_assert(TB::COLS == KS * MF<MS>::KSTEP, "inner dimensions differ");
+  constexpr int CB = RTile<MS, R, C>::CB, RB = RTile<MS, R, C>::RB;
+  constexpr int LOOK = KS < 2 ? KS : 2;
+  bf16x8 ring[LOOK + 1][CB];
+#pragma unroll
+  for (int p = 0; p < LOOK; ++p)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) ring[p][cb] = row_operand<TB, MS>(b_base, b_row0 + cb * MS, p);
+  static_for<0, KS>([&](auto ksc) {
+    constexpr int ks = decltype(ksc)::value;
+    if constexpr (ks + LOOK < KS) {
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+        ring[(ks + LOOK) % (LOOK + 1)][cb] = row_operand<TB, MS>(b_base, b_row0 + cb * MS, ks + LOOK);
+    }
+    static_for<0, CB>([&](auto cbc) {
+      constexpr int cb = decltype(cbc)::value;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const typename MF<MS>::cvec c0 = ks == 0 ? typename MF<MS>::cvec{} : acc.f[cb][rb];
+        acc.f[cb][rb] = MF<MS>::mma(ring[ks % (LOOK + 1)][cb], a.f[rb][ks], c0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      slot(ic<ks * CB + cb>{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  });
+}
+
+template <int MS, int R, int K, int C, class TB, class SlotF>
+__device__ __forceinline__ void mma_rAB_slots(RTile<MS, R, C>& acc, const BTile<MS, R, K>& a, char* b_base,
+                                              int b_col0, SlotF&& slot) {
+  static_assert(TB::ROWS == K, "inner dimensions differ");
+  constexpr int G = BTile<MS, R, K>::G;
+  constexpr int NG = (K / MS) * G;
+  static_assert(NG % 2 == 0, "k extent must fill whole MFMAs");
+  constexpr int CB = RTile<MS, R, C>::CB, RB = RTile<MS, R, C>::RB;
+  constexpr int ITEMS = (NG / 2) * CB;
+  constexpr int LOOK = ITEMS < 4 ? ITEMS : 4;
+  const int lane = lane_id();
+  const int lh = lane / MS;
+  const int ngrp = (lane % MS) & ~15;
+  auto read = [&](int t) {
+    const int q = 2 * (t / CB), cb = t % CB;
+    const int kb0 = q / G, g0 = q % G, kb1 = (q + 1) / G, g1 = (q + 1) % G;
+    const int k0 = kb0 * MS + g0 * 4 * MF<MS>::LG + 4 * lh;
+    const int k1 = kb1 * MS + g1 * 4 * MF<MS>::LG + 4 * lh;
+    const int n0 = b_col0 + cb * MS + ngrp;
+    return cat(tr_operand4<TB>(b_base, k0, n0), tr_operand4<TB>(b_base, k1, n0));
+  };
+  bf16x8 ring[LOOK + 1];
+#pragma unroll
+  for (int p = 0; p < LOOK; ++p) ring[p] = read(p);
+  static_for<0, ITEMS>([&](auto tc) {
+    constexpr int t = decltype(tc)::value;
+    if constexpr (t + LOOK < ITEMS) ring[(t + LOOK) % (LOOK + 1)] = read(t + LOOK);
+    constexpr int q = 2 * (t / CB), cb = t % CB;
+    constexpr int kb0 = q / G, g0 = q % G, kb1 = (q + 1) / G, g1 = (q + 1) % G;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      acc.f[cb][rb] = MF<MS>::mma(ring[t % (LOOK + 1)], cat(a.f[kb0][rb][g0], a.f[kb1][rb][g1]), acc.f[cb][rb]);
+    __builtin_amdgcn_sched_barrier(0);
+    slot(ic<t>{});
+    __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
+// Element pairs [P0, P1) of a lane = row tile (pair p = registers 2p, 2p+1
+// in (cb, rb, i) order): p = fn(s, rb) in fp32, added to the lane's partial
+// row sums and packed to bf16 into `pb`.
+template <int P0, int P1, int MS, int R, int C, class F>
+__device__ __forceinline__ void e_pairs(const RTile<MS, R, C>& s, BTile<MS, R, C>& pb, float (&rsum)[R / MS],
+                                        F fn) {
+  constexpr int RB = R / MS, CR = MF<MS>::CREGS;
+#pragma unroll
+  for (int p = P0; p < P1; ++p) {
+    const int e = 2 * p;
+    const int cb = e / (RB * CR), rb = (e / CR) % RB, i = e % CR;
+    const float x0 = fn(s.f[cb][rb][i], rb), x1 = fn(s.f[cb][rb][i + 1], rb);
+    rsum[rb] += x0;
+    rsum[rb] += x1;
+    pb.f[cb][rb][i / 4][i % 4] = (bf16)x0;
+    pb.f[cb][rb][i / 4][i % 4 + 1] = (bf16)x1;
+  }
+}
+
+// Partial row reduction over elements [E0, E1) (in (cb, rb, i) order) into
+// lane-local accumulators; row_finish completes it across the lane groups.
+template <int E0, int E1, int MS, int R, int C, class F>
+__device__ __forceinline__ void row_partial(float (&acc)[R / MS], const RTile<MS, R, C>& t, F op) {
+  constexpr int RB = R / MS, CR = MF<MS>::CREGS;
+#pragma unroll
+  for (int e = E0; e < E1; ++e) {
+    const int cb = e / (RB * CR), rb = (e / CR) % RB, i = e % CR;
+    acc[rb] = op(acc[rb], t.f[cb][rb][i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Element-wise and row operations on lane = row tiles.
 template <int MS, int R, int C, class F>
 __device__ __forceinline__ void map(RTile<MS, R, C>& out, const RTile<MS, R, C>& in, F fn) {
@@ -949,6 +1077,14 @@ __device__ __forceinline__ void row_reduce(RVec<MS, R>& out, const RTile<MS, R, 
   }
 }
 
+// out[r] = op(reduced lane partials of row r, prev[r]) (see row_partial).
+template <int MS, int R, class F>
+__device__ __forceinline__ void row_finish(RVec<MS, R>& out, const float (&part)[R / MS], const RVec<MS, R>& prev,
+                                           F op) {
+#pragma unroll
+  for (int rb = 0; rb < R / MS; ++rb) out.v[rb] = op(lane_group_reduce<MS>(part[rb], op), prev.v[rb]);
+}
+
 template <int MS, int R, int C, class F>
 __device__ __forceinline__ void row_apply(RTile<MS, R, C>& out, const RTile<MS, R, C>& t, const RVec<MS, R>& v,
                                           F fn) {
@@ -997,6 +1133,10 @@ __device__ __forceinline__ void to_bf16(BTile<MS, R, C>& out, const RTile<MS, R,
 template <int MS, int R, int C>
 __device__ __forceinline__ void causal_mask(RTile<MS, R, C>& out, const RTile<MS, R, C>& t, int row_g0,
                                             int col_g0) {
+  if (col_g0 + C - 1 <= row_g0) {  // wholly on or below the diagonal (wave-uniform)
+    out = t;
+    return;
+  }
   const int lane = lane_id();
   const int lr = lane % MS, lh = lane / MS;
   const float ninf = -__builtin_inff();

@@ -269,6 +269,24 @@ class SubColOp(Op):
 
 
 @dataclass(frozen=True)
+class LazyMaxOp(Op):
+    """*Additive.* ``result = cand if cand > prev + slack else prev`` element-wise.
+
+    The online-softmax running max with a slack: the stabiliser only moves
+    when the new maximum exceeds it by more than ``slack`` (in the units of
+    ``prev``), so the rescale of the accumulators (``exp2(prev - result)``)
+    is exactly 1 on most steps.  Softmax is invariant to the constant
+    subtracted, so only rounding differs; the exponentials stay below
+    ``2**(slack * scale)`` with ``scale`` the factor applied before ``exp2``.
+    """
+
+    result: Value
+    prev: Value
+    cand: Value
+    slack: float
+
+
+@dataclass(frozen=True)
 class LoadVecOp(Op):
     """*Additive.* Synchronous load of a register vector from an fp32 global.
 

@@ -7,7 +7,7 @@ every entry into the code-object cache, so GPU runs load prebuilt
 """
 from __future__ import annotations
 
-from typing import Callable, Dict
+from typing import Callable, Dict, Optional
 
 from warpir_amd.ir import Kernel
 from warpir_amd.passes.modulo_scheduler import gfx950_attention_cost_model, gfx950_cost_model, kernel_pass
@@ -61,6 +61,12 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_d64_causal_ssa": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
                                                            causal=True, name="mha_fwd_causal"),
     "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True),
+    # running max moves only by more than 2**8: the O rescale is skipped on most steps
+    "mha_d128_lazy": lambda: _mha(128, 128, 64, 32, causal=False, rescale_slack=8.0),
+    "mha_d64_causal_lazy": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=8.0),
+    # software-pipelined attention loop (QK of tile i+1 and PV of tile i carry tile i's softmax)
+    "mha_d128_ovl": lambda: _mha(128, 128, 64, 32, causal=False, rescale_slack=8.0),
+    "mha_d64_causal_ovl": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=8.0, lds_budget=32 * 1024),
     # FlashAttention backward: Dv = rowsum(dO * O); query-major dQ; key-major dK, dV.
     "mha_bwd_prep_d128": lambda: build_mha_bwd_prep_kernel(d=128, block_q=128, wave_rows=32),
     "mha_bwd_dq_d128": lambda: _bwd(build_mha_bwd_dq_kernel(d=128, block_q=128, block_kv=64, wave_rows=32), 128),
@@ -76,14 +82,17 @@ def _bwd(kernel: Kernel, d: int) -> Kernel:
 
 
 def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_budget: int = 64 * 1024,
-         min_stages: int = 2) -> Kernel:
+         min_stages: int = 2, rescale_slack: Optional[float] = None) -> Kernel:
     k = build_mha_forward_kernel(d=d, block_q=block_q, block_kv=block_kv, wave_rows=wave_rows, causal=causal,
-                                 name="mha_fwd_causal" if causal else "mha_fwd")
+                                 name="mha_fwd_causal" if causal else "mha_fwd", rescale_slack=rescale_slack)
     return kernel_pass(k, cost_model=gfx950_attention_cost_model(block_q, block_kv, d, lds_budget=lds_budget,
                                                                  min_stages=min_stages))
 
 # Lowering options of variants that differ from the defaults.
-TARGETS: Dict[str, dict] = {}
+TARGETS: Dict[str, dict] = {
+    "mha_d128_ovl": {"attn_overlap": True},
+    "mha_d64_causal_ovl": {"attn_overlap": True},
+}
 
 
 def lowerer(name: str):

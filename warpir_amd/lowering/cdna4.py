@@ -47,7 +47,7 @@ from typing import Dict, List, Optional, Sequence, Tuple, Union
 from warpir_amd.ir.ops import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, CopyOp, DivRowOp, Exp2Op, ForOp,
     IntAffineOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp, NegInftyOp,
-    Op, RowMaxOp, RowSumOp, SubColOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
+    LazyMaxOp, Op, RowMaxOp, RowSumOp, SubColOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
     WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
 from warpir_amd.ir.ops import SlotViewOp
@@ -92,6 +92,10 @@ class CDNA4Target:
     mve: bool = True
     # Final bf16 stores of register tiles go through LDS as whole rows.
     staged_stores: bool = True
+    # Attention loops (4 wavefronts, 2-slot K/V ring) as a software pipeline:
+    # S_{i+1} = Q K_{i+1}^T and O += P_i V_i each carry, MFMA by MFMA, a
+    # share of the softmax and running-max VALU work of the other tile.
+    attn_overlap: bool = False
 
 
 @dataclass
@@ -195,6 +199,7 @@ class CDNA4Lowerer:
         self._slot_shift: Dict[str, int] = {}   # induction var -> offset added to its ring slots
         self._fused_loads: Dict[int, List[Op]] = {}
         self._fused_ids: set = set()
+        self._var_override: Dict[str, str] = {}  # resolved value name -> C++ variable
 
     def _build_aliases(self, ops) -> None:
         """iter_arg init / loop results / yielded values -> block arg (``lowering.py:87-100``)."""
@@ -468,7 +473,8 @@ class CDNA4Lowerer:
         return f"(smem + {self.lds_off[key]} + {self._slot(slot)} * {stride})", key
 
     def _var(self, v: Value) -> str:
-        return _cname(self.resolve(v.name))
+        name = self.resolve(v.name)
+        return self._var_override.get(name) or _cname(name)
 
     def _reg_decl(self, v: Value) -> Optional[str]:
         t = v.type
@@ -609,6 +615,11 @@ class CDNA4Lowerer:
             fn = {RegTileType: "map2", RowVecType: "cvmap2"}.get(type(op.result.type), "vmap2")
             w(f"{pad}wir::{fn}({self._var(op.result)}, {self._var(op.a)}, {self._var(op.b)}, "
               f"[](float a, float b) {{ return a {sym} b; }});")
+            return
+        if isinstance(op, LazyMaxOp):
+            fn = {RowVecType: "cvmap2"}.get(type(op.result.type), "vmap2")
+            w(f"{pad}wir::{fn}({self._var(op.result)}, {self._var(op.prev)}, {self._var(op.cand)}, "
+              f"[](float p, float c) {{ return c > p + {_flt(op.slack)} ? c : p; }});")
             return
         if isinstance(op, (RowMaxOp, RowSumOp)):
             red = "wir::OpMax()" if isinstance(op, RowMaxOp) else "wir::OpAdd()"
@@ -797,6 +808,8 @@ class CDNA4Lowerer:
         if op.tile_size:
             stop = f"(({stop}) + {op.tile_size - 1}) / {op.tile_size}"
         iv = self._var(op.induction_var)
+        if self._emit_attention_overlap(op, stop, out, depth):
+            return
         if self._emit_attention_pingpong(op, stop, out, depth):
             return
         if self._setup_pingpong(op, out, depth):
@@ -997,6 +1010,380 @@ class CDNA4Lowerer:
         out.append(f"{pad}}}")
         out.append(f"{pad}if (wir_grp == 0) wir::barrier();")
         out.append(f"{pad[:-2]}}}")
+        return True
+
+    def _attention_overlap_plan(self, loop: ForOp):
+        """Match the prefetch-form attention loop for the overlapped emitter.
+
+        Required: four wavefronts; body = wait on slot i, slot views, S = Q K^T
+        with hoisted Q, one prefetch per ring into slot i + 1 of a 2-slot
+        ring, the softmax ops, O += P V last (P a bf16 register tile, O
+        carried in place).  The softmax ops split into
+          E: the element-wise chain S -> P_fp32 (mul_scalar / sub_row /
+             mul_row / exp2), consumed only by one row_sum and one bf16 copy;
+          R: the rescale of the carried O and of row_sum's carried prev;
+          M: everything else (running max, its scaled copies, the
+             correction, a causal mask of S), which may read only S, the
+             carried values, constants and other M results.
+        Every loop-carried value must be updated in place.
+        """
+        if not self.target.attn_overlap or self.geo.nw != 4 or loop not in list(self.kernel.body):
+            return None
+        body = list(loop.body)
+        if len(body) < 4 or not isinstance(body[0], WaitBufOp) or not isinstance(body[-1], YieldOp):
+            return None
+        if loop.start != 0 or loop.step != 1:
+            return None
+        mmas = [o for o in body if isinstance(o, MMAOp)]
+        if len(mmas) != 2:
+            return None
+        qk, pv = mmas
+        if not qk.transpose_b or pv.transpose_b or body[-2] is not pv:
+            return None
+        if self.resolve(qk.a.name) not in self._hoisted:
+            return None
+        pa = pv.a.type
+        if not (isinstance(pa, RegTileType) and pa.data_type == GPUType.bf16):
+            return None
+        # two key column blocks: the PV MFMAs of the first block run while the
+        # second block's probabilities are still being computed
+        if qk.result.type.cols != 2 * self.geo.ms or pa.cols != qk.result.type.cols:
+            return None
+        R = self.resolve
+        views = self._views()
+        vk, vv = views.get(R(qk.b.name)), views.get(R(pv.b.name))
+        if vk is None or vv is None or R(vk.buf.name) == R(vv.buf.name):
+            return None
+        ivn = R(loop.induction_var.name)
+        loads = [o for o in body if isinstance(o, TMALoadBufOp)]
+        if sorted(R(o.buf.name) for o in loads) != sorted([R(vk.buf.name), R(vv.buf.name)]):
+            return None
+        mods = {o.slot.modulus for o in loads} | {vk.slot.modulus, vv.slot.modulus, body[0].slot.modulus}
+        if mods != {2}:
+            return None
+        affine = [o for o in body if isinstance(o, IntAffineOp)]
+        if len(affine) != 1 or affine[0].mul != 1 or affine[0].add != 1 or R(affine[0].input.name) != ivn:
+            return None
+        for o in loads:
+            if not (isinstance(o.slot, BufSlotExpr) and o.slot.value is not None and R(o.slot.value.name) == ivn
+                    and o.slot.offset % 2 == 1):
+                return None
+            b, d, rt, ct = o.coords
+            if not (isinstance(rt, Value) and R(rt.name) == R(affine[0].result.name)) or ct != 0:
+                return None
+            if any(isinstance(c, Value) and R(c.name) == ivn for c in (b, d)):
+                return None
+        for v in (vk, vv):
+            if v.slot.value is None or R(v.slot.value.name) != ivn or v.slot.offset % 2:
+                return None
+        skip = (TMALoadBufOp, IntAffineOp, SlotViewOp)
+        mid = [o for o in body[body.index(qk) + 1: body.index(pv)] if not isinstance(o, skip)]
+        if any(isinstance(o, (TMALoadOp, WaitOp, WaitBufOp, MMAOp, MMABufOp, ForOp)) for o in mid):
+            return None
+        producers = {}
+        for o in mid:
+            r = vars(o).get("result")
+            if isinstance(r, Value):
+                producers[R(r.name)] = o
+        rowsums = [o for o in mid if isinstance(o, RowSumOp)]
+        if len(rowsums) != 1:
+            return None
+        rs = rowsums[0]
+        p_name = R(rs.tile.name)
+        cvts = [o for o in mid if isinstance(o, CopyOp) and R(o.input.name) == p_name]
+        if len(cvts) != 1 or R(cvts[0].result.name) != R(pv.a.name):
+            return None
+        cvt = cvts[0]
+        chain, cur = [], rs.tile
+        while True:
+            prod = producers.get(R(cur.name))
+            if not isinstance(prod, (MulScalarOp, SubRowOp, Exp2Op, MulRowOp)):
+                break
+            src = prod.input if isinstance(prod, (MulScalarOp, Exp2Op)) else prod.tile
+            if not isinstance(src.type, RegTileType) or not isinstance(prod.result.type, RegTileType):
+                break
+            chain.insert(0, prod)
+            cur = src
+        if not chain:
+            return None
+        start = cur
+        mask = producers.get(R(start.name))
+        if mask is not None:
+            if not isinstance(mask, CausalMaskOp) or R(mask.tile.name) != R(qk.result.name):
+                return None
+        elif R(start.name) != R(qk.result.name):
+            return None
+        acc_prod = producers.get(R(pv.accum.name))
+        prev_prod = producers.get(R(rs.prev.name))
+        r_ops = [o for o in (prev_prod, acc_prod) if o is not None]
+        if not isinstance(acc_prod, MulRowOp):
+            return None
+        carried = {R(ia.block_arg.name) for ia in loop.iter_args}
+        if R(acc_prod.tile.name) not in carried:
+            return None
+        if prev_prod is not None and not any(isinstance(x, Value) and R(x.name) in carried
+                                             for x in vars(prev_prod).values()):
+            return None
+        e_ids = {id(o) for o in chain} | {id(rs), id(cvt)}
+        r_ids = {id(o) for o in r_ops}
+        m_ops = [o for o in mid if id(o) not in e_ids and id(o) not in r_ids]
+        e_vals = {R(o.result.name) for o in chain} | {R(cvt.result.name)}
+        r_vals = {R(o.result.name) for o in r_ops} | {R(rs.result.name)}
+        s_vals = {R(qk.result.name), R(start.name)}
+        rowmaxes = [o for o in m_ops if isinstance(o, RowMaxOp)]
+        if len(rowmaxes) != 1 or R(rowmaxes[0].tile.name) != R(start.name):
+            return None
+        for o in m_ops:
+            for name, x in vars(o).items():
+                if name == "result" or not isinstance(x, Value):
+                    continue
+                n = R(x.name)
+                if n in e_vals or n in r_vals:
+                    return None
+                if isinstance(x.type, RegTileType) and n not in s_vals:
+                    return None
+                if n in s_vals and not isinstance(o, (RowMaxOp, CausalMaskOp)):
+                    return None
+        # chain values other than P feed only the next chain op
+        uses: Dict[str, int] = {}
+        for o in mid + [pv, body[-1]]:
+            for name, x in vars(o).items():
+                for v in _values_in(x) if name != "result" else ():
+                    uses[R(v.name)] = uses.get(R(v.name), 0) + 1
+        for o in chain[:-1]:
+            if uses.get(R(o.result.name), 0) != 1:
+                return None
+        if uses.get(p_name, 0) != 2:
+            return None
+        yld = body[-1]
+        for k, v in enumerate(yld.values):
+            if self._var(v) != self._var(loop.iter_args[k].block_arg):
+                return None
+        if self._var(pv.result) != self._var(pv.accum) and self._var(pv.result) not in {
+                self._var(ia.block_arg) for ia in loop.iter_args}:
+            return None
+        k_load = next(o for o in loads if R(o.buf.name) == R(vk.buf.name))
+        v_load = next(o for o in loads if R(o.buf.name) == R(vv.buf.name))
+        return dict(qk=qk, pv=pv, chain=chain, rs=rs, cvt=cvt, start=start, mask=mask, r_ops=r_ops,
+                    m_ops=m_ops, rowmax=rowmaxes[0], k_load=k_load, v_load=v_load)
+
+    def _emit_attention_overlap(self, loop: ForOp, stop: str, out: List[str], depth: int) -> bool:
+        """Software-pipelined attention loop (see ``CDNA4Target.attn_overlap``).
+
+        Tile j's scores S_j are computed one step ahead.  Step j (j + 1 < n):
+          wait + barrier (K_{j+1} and V_j landed; every wave is done with
+          step j - 1), R ops of tile j (rescale O and the running sum);
+          S_{j+1} = Q K_{j+1}^T, its 16 MFMAs carrying the E chain of
+          S_j (exp, partial row sums, bf16 P) and the DMAs of K_{j+2} and
+          V_{j+1} (into the slots that K_j and V_{j-1} have left);
+          O += P_j V_j, its first MFMAs carrying the rest of E, the later
+          ones the causal mask and the running max of S_{j+1} (M ops).
+        The K ring runs one tile ahead of the V ring.  S alternates between
+        two register tiles (the loop is unrolled by two); the last tile is
+        peeled.  Tensors that are not tile-aligned take the plain loop.
+        """
+        plan = self._attention_overlap_plan(loop)
+        if plan is None:
+            return False
+        R = self.resolve
+        pad = "  " * depth
+        ms = self.geo.ms
+        qk, pv, rs = plan["qk"], plan["pv"], plan["rs"]
+        st = qk.result.type
+        rb_n = st.rows // ms
+        cregs = 16 if ms == 32 else 4
+        n_pairs = (st.rows * st.cols // 64) // 2
+        iv = self._var(loop.induction_var)
+        kl, vl = plan["k_load"], plan["v_load"]
+        kkey, vkey = R(kl.buf.name), R(vl.buf.name)
+        kt, vt = kl.buf.type.tile_type, vl.buf.type.tile_type
+        kstile, vstile = self.stile(kkey), self.stile(vkey)
+        kper, vper = self.loads_per_wave(kt), self.loads_per_wave(vt)
+        kstride, vstride = _tile_bytes(kt), _tile_bytes(vt)
+
+        def kptr(slot: int) -> str:
+            return f"(smem + {self.lds_off[kkey]} + {slot} * {kstride})"
+
+        def vptr(slot: int) -> str:
+            return f"(smem + {self.lds_off[vkey]} + {slot} * {vstride})"
+
+        def src(ld, tile_expr: str) -> Tuple[str, str]:
+            g = f"globals.{_cname(ld.source.name)[2:]}"
+            sub = ld.source.type.sub_tile_type
+            b, d = self._int(ld.coords[0]), self._int(ld.coords[1])
+            self._aligned_checks.add((self.stile(R(ld.buf.name)), _cname(ld.source.name)[2:]))
+            return g, f"{b}, {d}, ({tile_expr}) * {sub.rows}, 0"
+
+        kg, _ = src(kl, "0")
+        vg, _ = src(vl, "0")
+        kload = f"wir::Loader<{kstile}, 4>"
+        vload = f"wir::Loader<{vstile}, 4>"
+        hf_var, hf_ks = self._hoisted[R(qk.a.name)]
+        s_names = {R(qk.result.name), R(plan["start"].name)}
+        p_var = self._var(pv.a)
+        o_var = self._var(pv.result)
+        acc_var = self._var(pv.accum)
+        a_t = pv.a.type
+        res_t = pv.result.type
+
+        def with_s(var: str):
+            for n in s_names:
+                self._var_override[n] = var
+
+        def clear_s():
+            for n in s_names:
+                self._var_override.pop(n, None)
+
+        def qk_plain(dst: List[str], d: int, svar: str, slot: int) -> None:
+            dst.append(f"{'  ' * d}wir::mma_ABt_frags<{ms}, {st.rows}, {st.cols}, {kstile}, {hf_ks}>"
+                       f"({svar}, {hf_var}, {kptr(slot)}, wave_col0);")
+
+        def m_ops(dst: List[str], d: int, tile_index: str, svar: str, partial: bool) -> None:
+            """The M ops for the tile in `svar` (its index `tile_index`)."""
+            p_ = "  " * d
+            dst.append(f"{p_}{{")
+            dst.append(f"{p_}  const int {iv} = {tile_index};")
+            dst.append(f"{p_}  (void){iv};")
+            with_s(svar)
+            for o in plan["m_ops"]:
+                if partial and o is plan["mask"]:
+                    continue
+                if partial and o is plan["rowmax"]:
+                    dst.append(f"{p_}  wir::row_finish({self._var(o.result)}, wir_mx, {self._var(o.prev)}, "
+                               f"wir::OpMax());")
+                    continue
+                self._emit_op(o, dst, d + 1)
+            clear_s()
+            dst.append(f"{p_}}}")
+
+        def r_ops(dst: List[str], d: int) -> None:
+            # the rescale of the carried O is done in place (O = O * corr),
+            # so no copy of the accumulator exists on either path of its skip test
+            for o in plan["r_ops"]:
+                if isinstance(o, MulRowOp) and R(o.result.name) == R(pv.accum.name) and \
+                        self._var(o.tile) == o_var:
+                    dst.append(f"{'  ' * d}wir::row_scale({o_var}, {o_var}, {self._var(o.vec)});")
+                    continue
+                self._emit_op(o, dst, d)
+                if R(o.result.name) == R(pv.accum.name) and acc_var != o_var:
+                    dst.append(f"{'  ' * d}{o_var} = {acc_var};")
+
+        def step(dst: List[str], d: int, j: str, par: int, cur: str, nxt: str) -> None:
+            p_ = "  " * d
+            p2 = p_ + "  "
+            dst.append(f"{p_}{{")
+            dst.append(f"{p2}wir::wait_vm_barrier<0>();")
+            r_ops(dst, d + 1)
+            _, kc = src(kl, f"({j}) + 2")
+            _, vc = src(vl, f"({j}) + 1")
+            dst.append(f"{p2}const auto wir_ks = {kload}::prep<WIR_AL>({kg}, {kc});")
+            dst.append(f"{p2}const auto wir_vs = {vload}::prep<WIR_AL>({vg}, {vc});")
+            dst.append(f"{p2}for (int r_ = 0; r_ < {rb_n}; ++r_) wir_rs[r_] = 0.f;")
+            dst.append(f"{p2}wir::mma_ABt_frags_slots<{ms}, {st.rows}, {st.cols}, {kstile}, {hf_ks}>"
+                       f"({nxt}, {hf_var}, {kptr((par + 1) % 2)}, wave_col0, [&](auto t_) {{")
+            dst.append(f"{p2}  constexpr int T = decltype(t_)::value;")
+            dst.append(f"{p2}  constexpr int P0 = (T * {n_pairs} + WIR_NS - 1) / WIR_NS, "
+                       f"P1 = ((T + 1) * {n_pairs} + WIR_NS - 1) / WIR_NS;")
+            dst.append(f"{p2}  wir::e_pairs<P0, P1>({cur}, {p_var}, wir_rs, wir_ef);")
+            dst.append(f"{p2}  if constexpr (T % 2 == 0 && T / 2 < {kper}) "
+                       f"{kload}::issue<WIR_AL>(T / 2, {kptr(par)}, {kg}, wir_ks, wir_wave);")
+            dst.append(f"{p2}  if constexpr (T % 2 == 1 && T / 2 < {vper}) "
+                       f"{vload}::issue<WIR_AL>(T / 2, {vptr((par + 1) % 2)}, {vg}, wir_vs, wir_wave);")
+            dst.append(f"{p2}}});")
+            dst.append(f"{p2}wir::mma_rAB_slots<{ms}, {a_t.rows}, {a_t.cols}, {res_t.cols}, {vstile}>"
+                       f"({o_var}, {p_var}, {vptr(par)}, wave_col0, [&](auto t_) {{")
+            dst.append(f"{p2}  constexpr int T = decltype(t_)::value + WIR_NA;")
+            dst.append(f"{p2}  if constexpr (T < WIR_NS) {{")
+            dst.append(f"{p2}    constexpr int P0 = (T * {n_pairs} + WIR_NS - 1) / WIR_NS, "
+                       f"P1 = ((T + 1) * {n_pairs} + WIR_NS - 1) / WIR_NS;")
+            dst.append(f"{p2}    wir::e_pairs<P0, P1>({cur}, {p_var}, wir_rs, wir_ef);")
+            dst.append(f"{p2}  }}")
+            dst.append(f"{p2}  if constexpr (T == WIR_NS) {{")
+            dst.append(f"{p2}    wir::row_finish({self._var(rs.result)}, wir_rs, {self._var(rs.prev)}, wir::OpAdd());")
+            dst.append(f"{p2}    for (int r_ = 0; r_ < {rb_n}; ++r_) wir_mx[r_] = -__builtin_inff();")
+            if plan["mask"] is not None:
+                with_s(nxt)
+                dst.append(f"{p2}    {{ const int {iv} = ({j}) + 1; (void){iv};")
+                self._emit_op(plan["mask"], dst, d + 3)
+                dst.append(f"{p2}    }}")
+                clear_s()
+            dst.append(f"{p2}  }}")
+            n_el = 2 * n_pairs
+            for c in range(n_chunks):
+                e0, e1 = n_el * c // n_chunks, n_el * (c + 1) // n_chunks
+                dst.append(f"{p2}  if constexpr (T == WIR_NS + {c + 1}) wir::row_partial<{e0}, {e1}>(wir_mx, {nxt}, "
+                           f"wir::OpMax());")
+            dst.append(f"{p2}  if constexpr (T == WIR_NS + {n_chunks + 1}) {{")
+            m_ops(dst, d + 2, f"({j}) + 1", nxt, True)
+            dst.append(f"{p2}  }}")
+            dst.append(f"{p2}}});")
+            dst.append(f"{p_}}}")
+
+        def last(dst: List[str], d: int, j: str, par: int, cur: str) -> None:
+            p_ = "  " * d
+            p2 = p_ + "  "
+            dst.append(f"{p_}{{")
+            dst.append(f"{p2}wir::wait_vm_barrier<0>();")
+            r_ops(dst, d + 1)
+            dst.append(f"{p2}for (int r_ = 0; r_ < {rb_n}; ++r_) wir_rs[r_] = 0.f;")
+            dst.append(f"{p2}wir::e_pairs<0, {n_pairs}>({cur}, {p_var}, wir_rs, wir_ef);")
+            dst.append(f"{p2}wir::row_finish({self._var(rs.result)}, wir_rs, {self._var(rs.prev)}, wir::OpAdd());")
+            dst.append(f"{p2}wir::mma_rAB<{ms}, {a_t.rows}, {a_t.cols}, {res_t.cols}, {vstile}>"
+                       f"({o_var}, {p_var}, {vptr(par)}, wave_col0);")
+            dst.append(f"{p_}}}")
+
+        # PV slots after the probabilities are done: row-sum finish (+ mask),
+        # the partial maxima of the next tile, then its remaining M ops
+        pv_items = (a_t.cols // ms) * (cregs // 4) // 2 * (res_t.cols // ms)
+        n_chunks = min(4, pv_items // 2 - 2)
+        if n_chunks < 1:
+            return False
+        # the element-wise chain as one per-element function
+        e_lines = []
+        for o in plan["chain"]:
+            if isinstance(o, MulScalarOp):
+                e_lines.append(f"x = x * {_flt(o.scalar)};")
+            elif isinstance(o, SubRowOp):
+                e_lines.append(f"x = x - {self._var(o.vec)}.v[rb];")
+            elif isinstance(o, MulRowOp):
+                e_lines.append(f"x = x * {self._var(o.vec)}.v[rb];")
+            else:
+                e_lines.append("x = __builtin_amdgcn_exp2f(x);")
+        p1 = pad + "  "
+        out.append(f"{pad}if constexpr (!WIR_AL) {{")
+        self._emit_loop(loop, stop, out, depth + 1)
+        out.append(f"{pad}}} else {{")
+        out.append(f"{p1}wir::RTile<{ms}, {st.rows}, {st.cols}> wir_sa, wir_sb;")
+        out.append(f"{p1}float wir_rs[{rb_n}], wir_mx[{rb_n}];")
+        out.append(f"{p1}constexpr int WIR_NA = {hf_ks * (st.cols // ms)};  // slots of S = Q K^T")
+        out.append(f"{p1}constexpr int WIR_NS = WIR_NA + {(a_t.cols // ms) * (cregs // 4) // 2 * (res_t.cols // ms) // 2};"
+                   f"  // slots carrying E")
+        out.append(f"{p1}static_assert((({n_pairs} / 2 - 1) * WIR_NS) / {n_pairs} < WIR_NA, "
+                   f"\"block-0 probabilities must be ready before O += P V starts\");")
+        out.append(f"{p1}static_assert(WIR_NS + {n_chunks + 1} < WIR_NA + 2 * (WIR_NS - WIR_NA), "
+                   f"\"running-max slots must fit\");")
+        out.append(f"{p1}auto wir_ef = [&](float x, int rb) {{ (void)rb; {' '.join(e_lines)} return x; }};")
+        out.append(f"{p1}const int wir_n = {stop};")
+        out.append(f"{p1}if (wir_n > 0) {{")
+        p2 = p1 + "  "
+        _, kc1 = src(kl, "1")
+        out.append(f"{p2}{kload}::load<WIR_AL>({kptr(1)}, {kg}, {kc1}, wir_wave);")
+        out.append(f"{p2}wir::wait_vm_barrier<{kper}>();")
+        qk_plain(out, depth + 2, "wir_sa", 0)
+        m_ops(out, depth + 2, "0", "wir_sa", False)
+        out.append(f"{p2}int wir_j = 0;")
+        out.append(f"{p2}for (; wir_j + 2 < wir_n; wir_j += 2) {{")
+        step(out, depth + 3, "wir_j", 0, "wir_sa", "wir_sb")
+        step(out, depth + 3, "wir_j + 1", 1, "wir_sb", "wir_sa")
+        out.append(f"{p2}}}")
+        out.append(f"{p2}if (wir_j + 1 < wir_n) {{")
+        step(out, depth + 3, "wir_j", 0, "wir_sa", "wir_sb")
+        last(out, depth + 3, "wir_j + 1", 1, "wir_sb")
+        out.append(f"{p2}}} else {{")
+        last(out, depth + 3, "wir_j", 0, "wir_sa")
+        out.append(f"{p2}}}")
+        out.append(f"{p1}}}")
+        out.append(f"{pad}}}")
         return True
 
     def _setup_pingpong(self, loop: ForOp, out: List[str], depth: int) -> bool:

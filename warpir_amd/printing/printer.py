@@ -34,6 +34,7 @@ from warpir_amd.ir.ops import (
     SlotViewOp,
     SubOp,
     SubColOp,
+    LazyMaxOp,
     SubRowOp,
     TMALoadBufOp,
     TMALoadOp,
@@ -128,6 +129,7 @@ _LINE: Dict[type, Callable[[Op], str]] = {
     ),
     SubColOp: lambda op: _call(op, "sub_col", op.tile, op.vec),
     LoadVecOp: lambda op: f"{op.result!r} = load_vec({op.source!r}, {_coords(op.coords)})",
+    LazyMaxOp: lambda op: f"{op.result!r} = lazy_max({op.prev!r}, {op.cand!r}, {op.slack})",
 }
 
 

@@ -13,6 +13,7 @@ skipping -- using only additive ops.
 from __future__ import annotations
 
 import math
+from typing import Optional
 
 from warpir_amd.ir import (
     AddOp,
@@ -28,6 +29,7 @@ from warpir_amd.ir import (
     IntType,
     IterArg,
     Kernel,
+    LazyMaxOp,
     LoadVecOp,
     Log2Op,
     MMAOp,
@@ -133,12 +135,12 @@ def build_attention_kernel(d: int = 64, block: int = 64, warp_rows: int = 16,
     """
     return _attention(name="attention_fwd", d=d, block_q=block, block_kv=block,
                       wave_rows=warp_rows, scale=scale, multi_head=False, causal=False,
-                      with_lse=False)
+                      with_lse=False, rescale_slack=None)
 
 
 def build_mha_forward_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64,
                              wave_rows: int = 32, causal: bool = False, with_lse: bool = True,
-                             name: str = "mha_fwd") -> Kernel:
+                             name: str = "mha_fwd", rescale_slack: Optional[float] = None) -> Kernel:
     """Multi-head FlashAttention forward over ``[B, H, S, D]`` tensors.
 
     Program ``(blockIdx.x, blockIdx.y, blockIdx.z)`` = (query tile, head,
@@ -148,13 +150,19 @@ def build_mha_forward_kernel(d: int = 128, block_q: int = 128, block_kv: int = 6
     ``-sqrt(D)``-scaled variant, ``mha_h100.cu:216-221``).  With ``causal``
     the KV loop stops at the query tile's last row
     (``IntAffineOp``) and the score tile is masked (``CausalMaskOp``).
+
+    ``rescale_slack`` (additive, in exp2 units, e.g. 8.0): the running max
+    only moves when a tile's maximum exceeds it by more than that
+    (``LazyMaxOp``), so the O / l rescale is skipped on most steps and
+    ``P <= 2**slack``.  ``None`` builds the plain online softmax.
     """
     return _attention(name=name, d=d, block_q=block_q, block_kv=block_kv, wave_rows=wave_rows,
                       scale=LOG2E / math.sqrt(d), multi_head=True, causal=causal,
-                      with_lse=with_lse)
+                      with_lse=with_lse, rescale_slack=rescale_slack)
 
 
-def _attention(*, name, d, block_q, block_kv, wave_rows, scale, multi_head, causal, with_lse):
+def _attention(*, name, d, block_q, block_kv, wave_rows, scale, multi_head, causal, with_lse,
+               rescale_slack):
     q_tile = SharedTileType(GPUType.bf16, block_q, d)
     kv_tile = SharedTileType(GPUType.bf16, block_kv, d)
     if multi_head:
@@ -205,9 +213,14 @@ def _attention(*, name, d, block_q, block_kv, wave_rows, scale, multi_head, caus
     if causal:
         scores = v("att_masked", att_f)
         body.append(CausalMaskOp(result=scores, tile=att, row_tile=q_idx, col_tile=i))
+    body.append(CopyOp(result=max_prev, input=max_vec))
+    if rescale_slack is None:
+        body.append(RowMaxOp(result=max_new, tile=scores, prev=max_vec))
+    else:
+        max_cand = v("max_cand", cvec)
+        body += [RowMaxOp(result=max_cand, tile=scores, prev=max_vec),
+                 LazyMaxOp(result=max_new, prev=max_vec, cand=max_cand, slack=rescale_slack / scale)]
     body += [
-        CopyOp(result=max_prev, input=max_vec),
-        RowMaxOp(result=max_new, tile=scores, prev=max_vec),
         MulScalarOp(result=att_scaled, input=scores, scalar=scale),
         MulScalarOp(result=max_new_sc, input=max_new, scalar=scale),
         MulScalarOp(result=max_prev_sc, input=max_prev, scalar=scale),
