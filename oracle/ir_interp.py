@@ -222,7 +222,7 @@ class Interpreter:
             rows, cols = t.shape
             r = torch.arange(rows).unsqueeze(1) + self._int(op.row_tile) * rows
             c = torch.arange(cols).unsqueeze(0) + self._int(op.col_tile) * cols
-            s(op.result, t.masked_fill(c > r, float("-inf")))
+            s(op.result, t.masked_fill((r > c) if op.transposed else (c > r), float("-inf")))
         elif isinstance(op, IntAffineOp):
             s(op.result, self._int(op.input) * op.mul + op.add)
         elif isinstance(op, SubColOp):

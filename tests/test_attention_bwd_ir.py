@@ -21,17 +21,17 @@ from warpir_amd.workloads import (build_mha_bwd_dkdv_kernel, build_mha_bwd_dq_ke
 TOL = 1e-2
 
 
-def _inputs(b, h, s, d, seed=0):
+def _inputs(b, h, s, d, seed=0, causal=False):
     q, k, v, do = (seeded_normal((b, h, s, d), seed + j) for j in range(4))
-    o, lse = attention_ref(q, k, v)
+    o, lse = attention_ref(q, k, v, causal=causal)
     return q, k, v, do, o.to(torch.bfloat16), lse
 
 
-def _bwd_via_ir(q, k, v, do, o, lse, pipelined: bool, d: int):
+def _bwd_via_ir(q, k, v, do, o, lse, pipelined: bool, d: int, causal: bool = False):
     b, h, s, _ = q.shape
     prep = build_mha_bwd_prep_kernel(d=d, block_q=128, wave_rows=32)
-    dq_k = build_mha_bwd_dq_kernel(d=d, block_q=128, block_kv=64, wave_rows=32)
-    dkdv_k = build_mha_bwd_dkdv_kernel(d=d, block_kv=128, block_q=64, wave_rows=32)
+    dq_k = build_mha_bwd_dq_kernel(d=d, block_q=128, block_kv=64, wave_rows=32, causal=causal)
+    dkdv_k = build_mha_bwd_dkdv_kernel(d=d, block_kv=128, block_q=64, wave_rows=32, causal=causal)
     if pipelined:
         dq_k = kernel_pass(dq_k, cost_model=gfx950_attention_cost_model(128, 64, d))
         dkdv_k = kernel_pass(dkdv_k, cost_model=gfx950_attention_cost_model(128, 64, d))
@@ -52,6 +52,32 @@ def test_attention_backward_ir_matches_autograd(pipelined):
     assert torch.allclose(dv_vec, (do.float() * o.float()).sum(-1), rtol=1e-5, atol=1e-5)
     for got, ref in ((dq, rq), (dk, rk), (dv, rv)):
         assert rel_err(got.float(), ref) <= TOL
+
+
+@pytest.mark.parametrize("pipelined", [False, True])
+@pytest.mark.parametrize("s", [256, 192])
+def test_causal_attention_backward_ir_matches_autograd(pipelined, s):
+    q, k, v, do, o, lse = _inputs(1, 2, s, 64, seed=3, causal=True)
+    _, dq, dk, dv = _bwd_via_ir(q, k, v, do, o, lse, pipelined, d=64, causal=True)
+    rq, rk, rv = attention_bwd_ref(q, k, v, do, causal=True)
+    for got, ref in ((dq, rq), (dk, rk), (dv, rv)):
+        assert rel_err(got.float(), ref) <= TOL
+
+
+def test_causal_backward_closed_forms():
+    # The first query sees only the first key: P[0, 0] = 1 and Dv[0] = dO[0].V[0] = dP[0, 0],
+    # so dS[0, 0] = 0 and dQ[0] = 0.  The last key is seen only by the last query, so
+    # dV[-1] = P[-1, -1] dO[-1] and dK[-1] is a multiple of Q[-1].
+    q, k, v, do, o, lse = _inputs(1, 1, 128, 64, seed=5, causal=True)
+    _, dq, dk, dv = _bwd_via_ir(q, k, v, do, o, lse, True, d=64, causal=True)
+    rq, rk, rv = attention_bwd_ref(q, k, v, do, causal=True)
+    s_last = (q[0, 0, -1].double() @ k[0, 0].double().t()) / 8.0
+    p_last = torch.softmax(s_last, dim=0)[-1].item()
+    for dq_, dk_, dv_ in ((dq.float(), dk.float(), dv.float()), (rq, rk, rv)):
+        assert dq_[0, 0, 0].abs().max().item() <= 1e-2 * dq_.abs().max().item()
+        assert torch.allclose(dv_[0, 0, -1], p_last * do[0, 0, -1].float(), rtol=2e-2, atol=2e-3)
+        cos = torch.nn.functional.cosine_similarity(dk_[0, 0, -1], q[0, 0, -1].float(), dim=0).abs()
+        assert cos.item() > 0.99
 
 
 def test_attention_backward_ir_d128_ragged_kv_blocks():

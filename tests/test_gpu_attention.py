@@ -43,6 +43,17 @@ def test_mha_d128(gpu, variant, b, h, s):
     assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-3 * ref_lse.abs().max().item() + 1e-3
 
 
+@pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 2, 512), (1, 1, 192)])
+def test_mha_d128_causal(gpu, b, h, s):
+    announce(f"mha_d128_causal B={b} H={h} S={s}")
+    q, k, v = (seeded_normal((b, h, s, 128), sd) for sd in (3, 4, 5))
+    o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda(), causal=True)
+    torch.cuda.synchronize()
+    ref, ref_lse = attention_ref(q, k, v, causal=True)
+    assert rel_err(o.cpu(), ref) <= TOL
+    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-3 * ref_lse.abs().max().item() + 1e-3
+
+
 @pytest.mark.parametrize("variant", ["mha_d64_causal", "mha_d64_causal_ssa", "mha_d64_causal_lazy", "mha_d64_causal_ovl"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 2, 512), (1, 2, 1024), (1, 1, 192)])
 def test_mha_d64_causal(gpu, variant, b, h, s):
@@ -85,19 +96,20 @@ def test_mha_full_size_sampled(gpu):
         assert (lse[bi, hi] - ref_lse).abs().max().item() <= 1e-2
 
 
+@pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("b,h,s,d", [(1, 1, 128, 128), (2, 3, 256, 128), (1, 2, 192, 128), (1, 1, 1024, 128),
-                                     (1, 2, 256, 64), (1, 1, 64, 64)])
-def test_mha_backward(gpu, b, h, s, d):
+                                     (1, 2, 256, 64), (1, 1, 64, 64), (1, 2, 320, 64)])
+def test_mha_backward(gpu, b, h, s, d, causal):
     from oracle.torch_ref import attention_bwd_ref
-    announce(f"mha backward B={b} H={h} S={s} D={d}")
+    announce(f"mha backward B={b} H={h} S={s} D={d} causal={causal}")
     q, k, v, do = (seeded_normal((b, h, s, d), sd) for sd in (10, 11, 12, 13))
-    if d == 128:
-        o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda())
+    if d == 128 or causal:
+        o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda(), causal=causal)
     else:
         o, lse = _fwd_d64(q, k, v)
-    dq, dk, dv = api.attention_backward(q.cuda(), k.cuda(), v.cuda(), o, lse, do.cuda())
+    dq, dk, dv = api.attention_backward(q.cuda(), k.cuda(), v.cuda(), o, lse, do.cuda(), causal=causal)
     torch.cuda.synchronize()
-    rq, rk, rv = attention_bwd_ref(q, k, v, do)
+    rq, rk, rv = attention_bwd_ref(q, k, v, do, causal=causal)
     for name, got, ref in (("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
         err = rel_err(got.cpu().float(), ref)
         assert err <= TOL, (name, err)

@@ -139,7 +139,8 @@ def attention_forward(q, k, v, causal: bool = False, out=None, lse=None,
         raise ValueError("attention_forward: q, k, v must share one [B, H, S, D] shape")
     bsz, heads, seq, d = q.shape
     if variant is None:
-        variant = {(128, False): "mha_d128", (64, True): "mha_d64_causal"}.get((d, causal))
+        variant = {(128, False): "mha_d128", (64, True): "mha_d64_causal",
+                   (128, True): "mha_d128_causal"}.get((d, causal))
         if variant is None:
             raise ValueError(f"attention_forward: no kernel variant for D={d}, causal={causal}")
     handle = kernels.handle(variant)
@@ -154,10 +155,11 @@ def attention_forward(q, k, v, causal: bool = False, out=None, lse=None,
     return out, lse
 
 
-def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None):
+def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None, causal: bool = False):
     """Gradients ``(dQ, dK, dV)`` of ``attention_forward`` over ``[B, H, S, D]``
-    bf16 (non-causal), from its outputs ``o`` and ``lse`` and the output
-    gradient ``do``; S must be a multiple of 64.  Three WarpIR kernels run
+    bf16, from its outputs ``o`` and ``lse`` and the output gradient ``do``
+    (``causal`` must match the forward); S must be a multiple of 64.  Three
+    WarpIR kernels run
     on the current stream: ``Dv = rowsum(dO * O)`` (into ``dvec``, fp32
     ``[B, H, S]``, allocated if omitted), the query-major dQ kernel and the
     key-major dK/dV kernel (the reference's TK backward,
@@ -177,16 +179,19 @@ def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None
     dv = torch.empty_like(v) if dv is None else dv
     dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device=q.device) if dvec is None else dvec
     kernels.handle(f"mha_bwd_prep_d{d}")(O=o, dO=do, Dv=dvec)
-    kernels.handle(f"mha_bwd_dq_d{d}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq)
-    kernels.handle(f"mha_bwd_dkdv_d{d}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dK=dk, dV=dv)
+    sfx = "_causal" if causal else ""
+    kernels.handle(f"mha_bwd_dq_d{d}{sfx}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq)
+    kernels.handle(f"mha_bwd_dkdv_d{d}{sfx}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dK=dk, dV=dv)
     return dq, dk, dv
 
 
-def attention_backward_flops(bsz: int, heads: int, seq: int, d: int) -> float:
+def attention_backward_flops(bsz: int, heads: int, seq: int, d: int, causal: bool = False) -> float:
     """Matmul FLOPs of attention backward counted as the five S x S x D
-    products of the standard algorithm (S, dP, dV, dK, dQ): 10*B*H*S^2*D.
-    These kernels run seven (dQ recomputes S and dP instead of atomics)."""
-    return 10.0 * bsz * heads * seq * seq * d
+    products of the standard algorithm (S, dP, dV, dK, dQ): 10*B*H*S^2*D,
+    halved when causal.  These kernels run seven (dQ recomputes S and dP
+    instead of atomics)."""
+    f = 10.0 * bsz * heads * seq * seq * d
+    return f / 2 if causal else f
 
 
 def attention_flops(bsz: int, heads: int, seq: int, d: int, causal: bool = False) -> float:

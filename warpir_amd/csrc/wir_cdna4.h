@@ -1130,10 +1130,11 @@ __device__ __forceinline__ void to_bf16(BTile<MS, R, C>& out, const RTile<MS, R,
 
 // Lower-triangular mask: keep (row, col) when col_g <= row_g with
 // row_g = row_tile*BR + row0 + r and col_g = col_tile*BC + c.
-template <int MS, int R, int C>
+template <bool TRANSPOSED, int MS, int R, int C>
 __device__ __forceinline__ void causal_mask(RTile<MS, R, C>& out, const RTile<MS, R, C>& t, int row_g0,
                                             int col_g0) {
-  if (col_g0 + C - 1 <= row_g0) {  // wholly on or below the diagonal (wave-uniform)
+  // every element kept (a wave-uniform test on the tile's corners)
+  if (TRANSPOSED ? row_g0 + R - 1 <= col_g0 : col_g0 + C - 1 <= row_g0) {
     out = t;
     return;
   }
@@ -1148,7 +1149,8 @@ __device__ __forceinline__ void causal_mask(RTile<MS, R, C>& out, const RTile<MS
 #pragma unroll
       for (int i = 0; i < MF<MS>::CREGS; ++i) {
         const int col = col_g0 + cb * MS + ccol<MS>(i, lh);
-        out.f[cb][rb][i] = col <= row ? t.f[cb][rb][i] : ninf;
+        const bool keep = TRANSPOSED ? row <= col : col <= row;
+        out.f[cb][rb][i] = keep ? t.f[cb][rb][i] : ninf;
       }
     }
 }

@@ -250,13 +250,18 @@ class CausalMaskOp(Op):
     together), element ``(r, c)`` keeps its value when
     ``col_tile*C + c <= row_tile*R + r`` and becomes -inf otherwise.
     Mirrors the diagonal-tile masking of the reference's causal FA
-    kernel (``kernel_examples/attention/mha_h100.cu:160-176``).
+    kernel (``kernel_examples/attention/mha_h100.cu:160-176``).  With
+    ``transposed`` the tile holds transposed scores (keys along the rows,
+    as in the key-major backward): ``(r, c)`` keeps its value when
+    ``row_tile*R + r <= col_tile*C + c`` (``make_causal_t``,
+    ``mha_h100.cu:391-403``).
     """
 
     result: Value
     tile: Value
     row_tile: Union[Value, int]
     col_tile: Union[Value, int]
+    transposed: bool = False
 
 
 @dataclass(frozen=True)

@@ -61,6 +61,7 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_d64_causal_ssa": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
                                                            causal=True, name="mha_fwd_causal"),
     "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True),
+    "mha_d128_causal": lambda: _mha(128, 128, 64, 32, causal=True),
     # running max moves only by more than 2**8: the O rescale is skipped on most steps
     "mha_d128_lazy": lambda: _mha(128, 128, 64, 32, causal=False, rescale_slack=8.0),
     "mha_d64_causal_lazy": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=8.0),
@@ -74,6 +75,15 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_bwd_prep_d64": lambda: build_mha_bwd_prep_kernel(d=64, block_q=128, wave_rows=32),
     "mha_bwd_dq_d64": lambda: _bwd(build_mha_bwd_dq_kernel(d=64, block_q=128, block_kv=64, wave_rows=32), 64),
     "mha_bwd_dkdv_d64": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=64, block_kv=128, block_q=64, wave_rows=32), 64),
+    # causal backward: dq stops at the diagonal; dkdv starts at it (transposed mask)
+    "mha_bwd_dq_d128_causal": lambda: _bwd(build_mha_bwd_dq_kernel(d=128, block_q=128, block_kv=64, wave_rows=32,
+                                                                   causal=True, name="mha_bwd_dq_causal"), 128),
+    "mha_bwd_dkdv_d128_causal": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=128, block_kv=128, block_q=64, wave_rows=32,
+                                                                       causal=True, name="mha_bwd_dkdv_causal"), 128),
+    "mha_bwd_dq_d64_causal": lambda: _bwd(build_mha_bwd_dq_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
+                                                                  causal=True, name="mha_bwd_dq_causal"), 64),
+    "mha_bwd_dkdv_d64_causal": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=64, block_kv=128, block_q=64, wave_rows=32,
+                                                                      causal=True, name="mha_bwd_dkdv_causal"), 64),
 }
 
 

@@ -668,7 +668,8 @@ class CDNA4Lowerer:
         if isinstance(op, CausalMaskOp):
             t = op.tile.type
             br, bc = t.rows * (self.geo.nw // self.geo.nw_c), t.cols * self.geo.nw_c
-            w(f"{pad}wir::causal_mask({self._var(op.result)}, {self._var(op.tile)}, "
+            w(f"{pad}wir::causal_mask<{'true' if op.transposed else 'false'}>({self._var(op.result)}, "
+              f"{self._var(op.tile)}, "
               f"({self._int(op.row_tile)}) * {br} + wave_row0, ({self._int(op.col_tile)}) * {bc} + wave_col0);")
             return
         if isinstance(op, IntAffineOp):
@@ -1545,8 +1546,14 @@ class CDNA4Lowerer:
                 fields.append(f"  int {_cname(v.name)[2:]};")
         uses = {c.name for op in _walk(kernel.body) for f in vars(op).values() for c in _values_in(f)}
         dims = 3 if "blockIdx.z" in uses else 2
-        causal_x = any(isinstance(op, IntAffineOp) and isinstance(op.input, Value)
-                       and op.input.name == "blockIdx.x" for op in _walk(kernel.body))
+        # programs whose loop *stop* grows with blockIdx.x (causal query-major
+        # loops) run longest first; a loop *start* that grows with it (causal
+        # key-major loops) already makes the natural order longest first
+        from_x = {self.resolve(op.result.name) for op in _walk(kernel.body)
+                  if isinstance(op, IntAffineOp) and isinstance(op.input, Value)
+                  and op.input.name == "blockIdx.x" and op.mul > 0}
+        causal_x = any(isinstance(op, ForOp) and isinstance(op.stop, Value) and self.resolve(op.stop.name) in from_x
+                       for op in _walk(kernel.body))
         wpe = self.geo.waves_per_eu
         nt = self.geo.nw * 64
         pid = _pid_code(dims, self.target, reverse_x=causal_x)

@@ -387,17 +387,23 @@ def _prefetch_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
     stages = max(cost.min_stages, stages)
     if cost.max_stages is not None:
         stages = max(2, min(stages, cost.max_stages))
-    if not isinstance(loop.start, int):
-        raise PipelineError("the prefetch form needs a constant loop start")
+    if loop.step != 1:
+        raise PipelineError("the prefetch form needs a unit step")
     iv = loop.induction_var
     ring = {ld.result: Value(f"{ld.source.name.lower()}_bufs",
                              SharedBufferType(tile_type=ld.result.type, count=stages)) for ld in loads}
     all_rings = tuple(ring[ld.result] for ld in loads)
     out: List[Op] = [AllocSharedOp(result=ring[ld.result]) for ld in loads]
     for p in range(stages - 1):
-        tile = loop.start + p * (loop.step if isinstance(loop.step, int) else 1)
+        if isinstance(loop.start, int):
+            tile, slot = loop.start + p, (loop.start + p) % stages
+        else:
+            # a run-time start (e.g. the first query tile of a causal key-major loop)
+            tile = Value(f"{iv.name}_p{p}", iv.type)
+            out.append(IntAffineOp(result=tile, input=loop.start, mul=1, add=p))
+            slot = BufSlotExpr(value=loop.start, offset=p, modulus=stages)
         for ld in loads:
-            out.append(TMALoadBufOp(buf=ring[ld.result], slot=tile % stages, source=ld.source,
+            out.append(TMALoadBufOp(buf=ring[ld.result], slot=slot, source=ld.source,
                                     coords=ld.substitute({iv: tile}).coords))
     nxt = Value(f"{iv.name}_pf", iv.type)
     body: List[Op] = [WaitBufOp(bufs=all_rings, slot=BufSlotExpr(value=iv, offset=0, modulus=stages)),

@@ -121,7 +121,8 @@ _LINE: Dict[type, Callable[[Op], str]] = {
     AddOp: lambda op: _call(op, "add", op.a, op.b),
     Log2Op: lambda op: _call(op, "log2", op.input),
     CausalMaskOp: lambda op: (
-        f"{op.result!r} = causal_mask({op.tile!r}, {_coord(op.row_tile)}, {_coord(op.col_tile)})"
+        f"{op.result!r} = causal_mask({op.tile!r}, {_coord(op.row_tile)}, {_coord(op.col_tile)}"
+        + (", transposed=True" if op.transposed else "") + ")"
     ),
     SlotViewOp: lambda op: f"{op.result!r} = slot_view({op.buf.name}[{_slot(op.slot)}])",
     IntAffineOp: lambda op: (

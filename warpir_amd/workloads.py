@@ -323,9 +323,11 @@ def build_mha_bwd_prep_kernel(d: int = 128, block_q: int = 128, wave_rows: int =
 
 
 def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64, wave_rows: int = 32,
-                            name: str = "mha_bwd_dq") -> Kernel:
+                            name: str = "mha_bwd_dq", causal: bool = False) -> Kernel:
     """``dQ`` of attention forward, query-major: one program per query tile
-    ``(blockIdx.x, head, batch)``; the loop walks key tiles."""
+    ``(blockIdx.x, head, batch)``; the loop walks key tiles.  With
+    ``causal`` it stops at the query tile's last row and masks the scores
+    as the causal forward does."""
     scale = 1.0 / math.sqrt(d)
     q_glob, vec_glob, q_tile = _bwd_globals(d, block_q)
     kv_glob, _, kv_tile = _bwd_globals(d, block_kv)
@@ -349,8 +351,14 @@ def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64
     zero, s_t, s_sc, s_sh, p = (v(n, att_f) for n in ("s_zero", "s", "s_scaled", "s_shifted", "p"))
     dp_zero, dp, dp_sub, ds = (v(n, att_f) for n in ("dp_zero", "dp", "dp_minus_d", "ds"))
     ds_b = v("ds_bf16", att_b)
+    stop, prologue, scores, mask = n_kv, [], s_t, []
+    if causal:
+        stop = v("kv_stop", IntType())
+        prologue = [IntAffineOp(result=stop, input=q_idx, mul=block_q, add=block_q)]
+        scores = v("s_masked", att_f)
+        mask = [CausalMaskOp(result=scores, tile=s_t, row_tile=q_idx, col_tile=i)]
     loop = ForOp(
-        induction_var=i, start=0, stop=n_kv, step=1, tile_size=block_kv,
+        induction_var=i, start=0, stop=stop, step=1, tile_size=block_kv,
         iter_args=(IterArg(block_arg=dq_acc, init=dq_init),),
         body=(
             TMALoadOp(result=k_sh, source=K, coords=(*bh, i, 0)),
@@ -358,7 +366,8 @@ def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64
             WaitOp(values=(k_sh, v_sh)),
             ZeroOp(result=zero),
             MMAOp(result=s_t, a=q_sh, b=k_sh, accum=zero, transpose_b=True),
-            MulScalarOp(result=s_sc, input=s_t, scalar=scale * LOG2E),
+            *mask,
+            MulScalarOp(result=s_sc, input=scores, scalar=scale * LOG2E),
             SubRowOp(result=s_sh, tile=s_sc, vec=lse2),
             Exp2Op(result=p, input=s_sh),
             ZeroOp(result=dp_zero),
@@ -379,6 +388,7 @@ def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64
         LoadVecOp(result=dvec, source=Dv, coords=(*bh, q_idx, 0)),
         MulScalarOp(result=lse2, input=lse, scalar=LOG2E),
         ZeroOp(result=dq_init),
+        *prologue,
         loop,
         MulScalarOp(result=dq_out, input=dq_final, scalar=scale),
         TMAStoreOp(source=dq_out, dest=dQ, coords=(*bh, q_idx, 0)),
@@ -387,12 +397,14 @@ def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64
 
 
 def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 64, wave_rows: int = 32,
-                              name: str = "mha_bwd_dkdv") -> Kernel:
+                              name: str = "mha_bwd_dkdv", causal: bool = False) -> Kernel:
     """``dK`` and ``dV`` of attention forward, key-major: one program per key
     tile ``(blockIdx.x, head, batch)``; the loop walks query tiles.  Scores
     are computed transposed (``S^T = K Q^T``), so the per-query LSE and Dv
     are row_vecs, read from fp32 ``block_q x 1`` shared tiles that are loaded
-    (and pipelined) with the query tile."""
+    (and pipelined) with the query tile.  With ``causal`` the loop starts at
+    the first query tile that sees the key tile (``mha_h100.cu:525``) and the
+    transposed scores are masked (``CausalMaskOp(transposed=True)``)."""
     scale = 1.0 / math.sqrt(d)
     kv_glob, vec_glob, kv_tile = _bwd_globals(d, block_kv)
     q_glob, qvec_glob, q_tile = _bwd_globals(d, block_q)
@@ -420,8 +432,16 @@ def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 
     zero, st, st_sc, st_sh, pt = (v(n, st_f) for n in ("st_zero", "st", "st_scaled", "st_shifted", "pt"))
     dpt_zero, dpt, dpt_sub, dst = (v(n, st_f) for n in ("dpt_zero", "dpt", "dpt_minus_d", "dst"))
     pt_b, dst_b = v("pt_bf16", st_b), v("dst_bf16", st_b)
+    start, prologue, scores, mask = 0, [], st, []
+    if causal:
+        if block_kv % block_q:
+            raise ValueError("causal key-major loop needs block_kv to be a multiple of block_q")
+        start = v("q_start", IntType())
+        prologue = [IntAffineOp(result=start, input=kv_idx, mul=block_kv // block_q, add=0)]
+        scores = v("st_masked", st_f)
+        mask = [CausalMaskOp(result=scores, tile=st, row_tile=kv_idx, col_tile=i, transposed=True)]
     loop = ForOp(
-        induction_var=i, start=0, stop=n_q, step=1, tile_size=block_q,
+        induction_var=i, start=start, stop=n_q, step=1, tile_size=block_q,
         iter_args=(IterArg(block_arg=dk_acc, init=dk_init), IterArg(block_arg=dv_acc, init=dv_init)),
         body=(
             TMALoadOp(result=q_sh, source=Q, coords=(*bh, i, 0)),
@@ -433,7 +453,8 @@ def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 
             LoadVecOp(result=dvec, source=dv_sh, coords=()),
             ZeroOp(result=zero),
             MMAOp(result=st, a=k_sh, b=q_sh, accum=zero, transpose_b=True),
-            MulScalarOp(result=st_sc, input=st, scalar=scale * LOG2E),
+            *mask,
+            MulScalarOp(result=st_sc, input=scores, scalar=scale * LOG2E),
             MulScalarOp(result=lse2, input=lse, scalar=LOG2E),
             SubColOp(result=st_sh, tile=st_sc, vec=lse2),
             Exp2Op(result=pt, input=st_sh),
@@ -455,6 +476,7 @@ def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 
         WaitOp(values=(k_sh, v_sh)),
         ZeroOp(result=dk_init),
         ZeroOp(result=dv_init),
+        *prologue,
         loop,
         MulScalarOp(result=dk_out, input=dk_final, scalar=scale),
         TMAStoreOp(source=dk_out, dest=dK, coords=(*bh, kv_idx, 0)),
