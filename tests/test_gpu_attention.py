@@ -31,7 +31,8 @@ def test_reference_attention_ir(gpu, n):
     assert rel_err(o.cpu(), ref) <= TOL
 
 
-@pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp", "mha_d128_lazy", "mha_d128_ovl"])
+@pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp", "mha_d128_pp_swapped",
+                                     "mha_d128_lazy", "mha_d128_ovl"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 1, 64)])
 def test_mha_d128(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")

@@ -99,6 +99,25 @@ def test_attention_overlap_form():
     assert "mma_ABt_frags_slots" not in src[src.rindex('extern "C" __global__'):]
 
 
+def test_attention_pingpong_groups_follow_the_warp_assignment():
+    from warpir_amd.lowering.cdna4 import CDNA4Target
+    from warpir_amd.passes.warp_assigner import assign_waves
+    k = kernels.kernel("mha_d128_pp")
+    sol = assign_waves(k, num_warps=2)
+    k_group = sol.type_warp["k_load"]
+    assert sol.type_warp["v_load"] == 1 - k_group
+
+    def group_line(target):
+        src = CDNA4Lowerer(target).lower(k)
+        return [l.strip() for l in src.split("\n") if "const int wir_grp =" in l]
+
+    assert group_line(CDNA4Target()) == [f"const int wir_grp = (wir_wave >> 2) ^ {k_group}, wir_gw = wir_wave & 3;"
+                                         f"  // wave group issuing K: {k_group}"]
+    assert "^ 1," in group_line(CDNA4Target(wave_groups={"k": 1, "v": 0}))[0]
+    # both streams on one group cannot be realised by the ping-pong form
+    assert group_line(CDNA4Target(wave_groups={"k": 0, "v": 0})) == []
+
+
 def test_kernarg_layout_matches_globals_struct():
     assert ctypes.sizeof(GL) == 48
     s = kernarg_struct(build_gemm_kernel())

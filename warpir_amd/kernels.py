@@ -58,6 +58,8 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_d128_q256": lambda: _mha(128, 256, 64, 32, causal=False),
     # The same with a 3-slot K/V ring, lowered in 8-wavefront ping-pong form.
     "mha_d128_pp": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=96 * 1024, min_stages=3),
+    # the same with the K and V streams on the opposite wave groups from the warp assigner's answer
+    "mha_d128_pp_swapped": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=96 * 1024, min_stages=3),
     "mha_d64_causal_ssa": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
                                                            causal=True, name="mha_fwd_causal"),
     "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True),
@@ -101,6 +103,7 @@ def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_
 # Lowering options of variants that differ from the defaults.
 TARGETS: Dict[str, dict] = {
     "mha_d128_ovl": {"attn_overlap": True},
+    "mha_d128_pp_swapped": {"wave_groups": {"k": 1, "v": 0}},
     "mha_d64_causal_ovl": {"attn_overlap": True},
 }
 

@@ -96,6 +96,10 @@ class CDNA4Target:
     # S_{i+1} = Q K_{i+1}^T and O += P_i V_i each carry, MFMA by MFMA, a
     # share of the softmax and running-max VALU work of the other tile.
     attn_overlap: bool = False
+    # Wave group (0 or 1) that issues each load stream (named by its ring,
+    # e.g. "k", "v") in the 8-wavefront attention ping-pong.  None: take it
+    # from the warp assigner's solution for the kernel (passes.warp_assigner).
+    wave_groups: Optional[Dict[str, int]] = None
 
 
 @dataclass
@@ -930,6 +934,25 @@ class CDNA4Lowerer:
         return dict(S=S, qk=qk, pv=pv, softmax=softmax, k_load=k_load, v_load=v_load, affine=affine[0],
                     yld=yld)
 
+    def _pingpong_group_swap(self, plan) -> Optional[int]:
+        """Which physical wave group (0: waves 0-3, 1: waves 4-7) issues the K
+        stream -- the role that runs its MFMA phase first -- as the warp
+        assignment says.  The V stream must be on the other group; None
+        when it is not (the ping-pong form cannot realise that assignment)."""
+        def stream(ld) -> str:
+            return ld.buf.name[:-len("_bufs")] if ld.buf.name.endswith("_bufs") else ld.buf.name
+        ks, vs = stream(plan["k_load"]), stream(plan["v_load"])
+        groups = self.target.wave_groups
+        if groups is None:
+            from warpir_amd.passes.warp_assigner import assign_waves
+            sol = assign_waves(self.kernel, num_warps=2)
+            if sol is None:
+                return None
+            groups = {t[:-len("_load")]: w for t, w in sol.type_warp.items() if t.endswith("_load")}
+        if ks not in groups or vs not in groups or groups[ks] == groups[vs]:
+            return None
+        return groups[ks]
+
     def _emit_attention_pingpong(self, loop: ForOp, stop: str, out: List[str], depth: int) -> bool:
         """Eight-wavefront attention in ping-pong form.
 
@@ -945,6 +968,9 @@ class CDNA4Lowerer:
         """
         plan = self._attention_pingpong_plan(loop)
         if plan is None:
+            return False
+        swap = self._pingpong_group_swap(plan)
+        if swap is None:
             return False
         pad = "  " * depth
         p1 = pad + "  "
@@ -975,7 +1001,8 @@ class CDNA4Lowerer:
         self._emit_loop(loop, stop, out, depth + 1)
         out.append(f"{pad}}} else {{")
         pad, p1, depth = pad + "  ", p1 + "  ", depth + 1
-        out.append(f"{pad}const int wir_grp = wir_wave >> 2, wir_gw = wir_wave & 3;")
+        out.append(f"{pad}const int wir_grp = (wir_wave >> 2) ^ {swap}, wir_gw = wir_wave & 3;"
+                   f"  // wave group issuing K: {swap}")
         out.append(f"{pad}asm volatile(\"s_waitcnt vmcnt(0) lgkmcnt(0)\" ::: \"memory\");")
         out.append(f"{pad}wir::barrier();")
         out.append(f"{pad}if (wir_grp == 1) wir::barrier();  // group 1 runs one phase behind")
