@@ -218,6 +218,20 @@ def bench_extra(steps: int, warmup: int):
         "ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
         "kernels": ["mha_bwd_prep_d128", "mha_bwd_dq_d128", "mha_bwd_dkdv_d128"],
         "flops": "10*B*H*S^2*D (the five S x S x D products); the kernels run seven (dQ recomputes S and dP)"}
+    # causal forward and backward at the same shape
+    o, lse = api.attention_forward(q, k, v, causal=True)
+    ms, _ = _time_launches(lambda: api.attention_forward(q, k, v, causal=True, out=o, lse=lse), steps, warmup,
+                           stream)
+    tf = api.attention_flops(bsz, heads, seq, d, causal=True) / (ms * 1e-3) / 1e12
+    out["fa_fwd_causal_b16_h16_s4096_d128"] = {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
+                                               "kernel": "mha_d128_causal"}
+    ms, _ = _time_launches(lambda: api.attention_backward(q, k, v, o, lse, do, dq, dk, dv, dvec, causal=True),
+                           max(3, steps // 2), max(1, warmup // 2), stream)
+    tf = api.attention_backward_flops(bsz, heads, seq, d, causal=True) / (ms * 1e-3) / 1e12
+    out["fa_bwd_causal_b16_h16_s4096_d128"] = {
+        "ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
+        "kernels": ["mha_bwd_prep_d128", "mha_bwd_dq_d128_causal", "mha_bwd_dkdv_d128_causal"],
+        "flops": "5*B*H*S^2*D (the five products, halved by the causal mask)"}
     return out
 
 
