@@ -40,7 +40,7 @@ import torch
 
 from warpir_amd.ir import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, ColVecType, CopyOp, DivRowOp, Exp2Op,
-    ForOp, GPUType, IntAffineOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp,
+    ForOp, GPUType, IntAffineOp, IntDivOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp,
     NegInftyOp, RegTileType, RowMaxOp, RowSumOp, RowVecType, SlotViewOp, SubColOp, SubOp, SubRowOp, LazyMaxOp,
     TMALoadBufOp, TMALoadOp, TMAStoreOp, Value, WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
@@ -223,6 +223,8 @@ class Interpreter:
             r = torch.arange(rows).unsqueeze(1) + self._int(op.row_tile) * rows
             c = torch.arange(cols).unsqueeze(0) + self._int(op.col_tile) * cols
             s(op.result, t.masked_fill((r > c) if op.transposed else (c > r), float("-inf")))
+        elif isinstance(op, IntDivOp):
+            s(op.result, self._int(op.input) // self._int(op.divisor))
         elif isinstance(op, IntAffineOp):
             s(op.result, self._int(op.input) * op.mul + op.add)
         elif isinstance(op, SubColOp):

@@ -116,6 +116,40 @@ def test_mha_backward(gpu, b, h, s, d, causal):
         assert err <= TOL, (name, err)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("b,hq,hkv,s,d", [(1, 4, 2, 256, 128), (2, 8, 2, 192, 128), (1, 6, 1, 320, 64),
+                                          (1, 4, 4, 128, 64)])
+def test_grouped_query_attention(gpu, b, hq, hkv, s, d, causal):
+    """GQA forward and backward against autograd through the head expansion."""
+    if d == 64 and not causal:
+        pytest.skip("no D=64 non-causal forward variant")
+    announce(f"gqa B={b} Hq={hq} Hkv={hkv} S={s} D={d} causal={causal}")
+    hr = hq // hkv
+    q, do = seeded_normal((b, hq, s, d), 31), seeded_normal((b, hq, s, d), 34)
+    k, v = seeded_normal((b, hkv, s, d), 32), seeded_normal((b, hkv, s, d), 33)
+    o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda(), causal=causal)
+    dq, dk, dv = api.attention_backward(q.cuda(), k.cuda(), v.cuda(), o, lse, do.cuda(), causal=causal)
+    torch.cuda.synchronize()
+    ref_o, ref_lse = attention_ref(q, k.repeat_interleave(hr, 1), v.repeat_interleave(hr, 1), causal=causal)
+    assert rel_err(o.cpu(), ref_o) <= TOL
+    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-3 * ref_lse.abs().max().item() + 1e-3
+    qf, kf, vf = (t.float().requires_grad_(True) for t in (q, k, v))
+    sc = qf @ kf.repeat_interleave(hr, 1).transpose(-1, -2) / math.sqrt(d)
+    if causal:
+        sc = sc.masked_fill(torch.ones(s, s, dtype=torch.bool).triu(1), float("-inf"))
+    (torch.softmax(sc, -1) @ vf.repeat_interleave(hr, 1)).backward(do.float())
+    for name, got, ref in (("dQ", dq, qf.grad), ("dK", dk, kf.grad), ("dV", dv, vf.grad)):
+        err = rel_err(got.cpu().float(), ref)
+        assert err <= TOL, (name, err)
+
+
+def test_grouped_query_rejects_bad_head_counts(gpu):
+    q = torch.zeros(1, 6, 128, 128, dtype=torch.bfloat16, device="cuda")
+    k = torch.zeros(1, 4, 128, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        api.attention_forward(q, k, k)
+
+
 def _fwd_d64(q, k, v):
     """Forward outputs for D=64 (no non-causal D=64 forward variant): the oracle's, as bf16 / fp32 on the GPU."""
     o, lse = attention_ref(q, k, v)

@@ -135,14 +135,15 @@ def attention_forward(q, k, v, causal: bool = False, out=None, lse=None,
     """
     import torch
 
-    if q.dim() != 4 or q.shape != k.shape or k.shape != v.shape:
-        raise ValueError("attention_forward: q, k, v must share one [B, H, S, D] shape")
     bsz, heads, seq, d = q.shape
+    hr = _head_ratio("attention_forward", q, k, v)
     if variant is None:
         variant = {(128, False): "mha_d128", (64, True): "mha_d64_causal",
                    (128, True): "mha_d128_causal"}.get((d, causal))
         if variant is None:
             raise ValueError(f"attention_forward: no kernel variant for D={d}, causal={causal}")
+        if hr > 1:
+            variant += "_gqa"
     handle = kernels.handle(variant)
     kv_tile = next(o for o in _loops(handle.kernel)).tile_size
     if seq % kv_tile:
@@ -151,15 +152,35 @@ def attention_forward(q, k, v, causal: bool = False, out=None, lse=None,
         out = torch.empty_like(q)
     if lse is None:
         lse = torch.empty(bsz, heads, seq, dtype=torch.float32, device=q.device)
-    handle(Q=q, K=k, V=v, N=seq, O=out, L=lse)
+    if any(v_.name == "HR" for v_ in handle.kernel.inputs):
+        handle(Q=q, K=k, V=v, N=seq, HR=hr, O=out, L=lse)
+    elif hr > 1:
+        raise ValueError(f"attention_forward: variant {variant} takes no grouped-query heads")
+    else:
+        handle(Q=q, K=k, V=v, N=seq, O=out, L=lse)
     return out, lse
 
 
-def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None, causal: bool = False):
+def _head_ratio(fn: str, q, k, v) -> int:
+    """Query heads per key/value head (grouped-query attention); 1 for plain MHA."""
+    if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape or q.shape[0] != k.shape[0] \
+            or q.shape[2:] != k.shape[2:]:
+        raise ValueError(f"{fn}: q [B, H, S, D] and k, v [B, H_kv, S, D] shapes do not match")
+    if k.shape[1] < 1 or q.shape[1] % k.shape[1]:
+        raise ValueError(f"{fn}: {q.shape[1]} query heads are not a multiple of {k.shape[1]} key/value heads")
+    return q.shape[1] // k.shape[1]
+
+
+def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None, causal: bool = False,
+                       workspace=None):
     """Gradients ``(dQ, dK, dV)`` of ``attention_forward`` over ``[B, H, S, D]``
     bf16, from its outputs ``o`` and ``lse`` and the output gradient ``do``
-    (``causal`` must match the forward); S must be a multiple of 64.  Three
-    WarpIR kernels run
+    (``causal`` must match the forward); S must be a multiple of 64.  With
+    grouped-query K and V (``[B, H_kv, S, D]``) the key-major kernel writes
+    each query head's fp32 dK / dV contribution into ``workspace`` (fp32, at
+    least ``2 * B * H * S * D`` elements, allocated if omitted) and a HIP
+    reduction sums the ``H / H_kv`` contributions of every key/value head
+    into bf16 ``dK`` / ``dV``.  Three WarpIR kernels run
     on the current stream: ``Dv = rowsum(dO * O)`` (into ``dvec``, fp32
     ``[B, H, S]``, allocated if omitted), the query-major dQ kernel and the
     key-major dK/dV kernel (the reference's TK backward,
@@ -167,8 +188,9 @@ def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None
     same gradients with dQ by atomic adds)."""
     import torch
 
-    if q.dim() != 4 or not (q.shape == k.shape == v.shape == o.shape == do.shape):
-        raise ValueError("attention_backward: q, k, v, o, do must share one [B, H, S, D] shape")
+    if q.dim() != 4 or not (q.shape == o.shape == do.shape):
+        raise ValueError("attention_backward: q, o, do must share one [B, H, S, D] shape")
+    hr = _head_ratio("attention_backward", q, k, v)
     bsz, heads, seq, d = q.shape
     if d not in (64, 128) or seq % 64:
         raise ValueError(f"attention_backward: D must be 64 or 128 and S a multiple of 64 (got D={d}, S={seq})")
@@ -180,9 +202,51 @@ def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None
     dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device=q.device) if dvec is None else dvec
     kernels.handle(f"mha_bwd_prep_d{d}")(O=o, dO=do, Dv=dvec)
     sfx = "_causal" if causal else ""
-    kernels.handle(f"mha_bwd_dq_d{d}{sfx}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq)
-    kernels.handle(f"mha_bwd_dkdv_d{d}{sfx}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dK=dk, dV=dv)
+    if hr == 1:
+        kernels.handle(f"mha_bwd_dq_d{d}{sfx}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq)
+        kernels.handle(f"mha_bwd_dkdv_d{d}{sfx}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dK=dk, dV=dv)
+        return dq, dk, dv
+    numel = q.numel()
+    if workspace is None:
+        workspace = torch.empty(2 * numel, dtype=torch.float32, device=q.device)
+    if workspace.dtype != torch.float32 or workspace.numel() < 2 * numel or not workspace.is_contiguous():
+        raise ValueError(f"attention_backward: workspace must be contiguous fp32 with >= {2 * numel} elements")
+    dk_part = workspace[:numel].view(q.shape)
+    dv_part = workspace[numel:2 * numel].view(q.shape)
+    kernels.handle(f"mha_bwd_dq_d{d}{sfx}_gqa")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, HR=hr, dQ=dq)
+    kernels.handle(f"mha_bwd_dkdv_d{d}{sfx}_gqa")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, HR=hr,
+                                                  dK_part=dk_part, dV_part=dv_part)
+    _group_reduce(dk_part, dk, hr)
+    _group_reduce(dv_part, dv, hr)
     return dq, dk, dv
+
+
+_group_reduce_kernel = None
+
+
+def _group_reduce(partials, out, splits: int) -> None:
+    """``out[g] = bf16(sum_r partials[g * splits + r])`` over the key/value head
+    groups of a ``[B, H, S, D]`` fp32 contribution tensor (``splitk_reduce.hip``)."""
+    import ctypes
+
+    from warpir_amd.runtime import RawKernel
+
+    global _group_reduce_kernel
+    if _group_reduce_kernel is None:
+        _group_reduce_kernel = RawKernel("splitk_reduce.hsaco", "wir_group_reduce")
+
+    class Args(ctypes.Structure):
+        _fields_ = [("partials", ctypes.c_void_p), ("out", ctypes.c_void_p), ("n", ctypes.c_longlong),
+                    ("groups", ctypes.c_longlong), ("splits", ctypes.c_int)]
+
+    if not out.is_contiguous() or out.dtype.itemsize != 2:
+        raise ValueError("attention_backward: dk / dv must be contiguous bf16")
+    n = out.shape[-2] * out.shape[-1]
+    groups = out.numel() // n
+    if n % 8 or partials.numel() != groups * splits * n:
+        raise ValueError("attention_backward: grouped reduction needs S * D % 8 == 0 and matching shapes")
+    args = Args(partials.data_ptr(), out.data_ptr(), n, groups, splits)
+    _group_reduce_kernel.launch(((groups * n // 8 + 255) // 256, 1, 1), (256, 1, 1), args)
 
 
 def attention_backward_flops(bsz: int, heads: int, seq: int, d: int, causal: bool = False) -> float:

@@ -1,4 +1,6 @@
-// splitk_reduce.hip -- the reduction step of split-K GEMM.
+// splitk_reduce.hip -- fp32 partial sums rounded once to bf16: the reduction
+// step of split-K GEMM (wir_splitk_reduce) and of the grouped-query
+// attention backward (wir_group_reduce).
 //
 // The split-K GEMM kernel (warpir_amd.workloads.build_gemm_kernel with
 // split_k=True) writes S fp32 partial products [S][M][N]; this kernel sums
@@ -25,6 +27,40 @@ extern "C" __global__ void __launch_bounds__(256) wir_splitk_reduce(const wr_arg
   wr_f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < args.splits; ++s) {
     const float* p = args.partials + s * args.split_stride + e;
+    lo += *(const wr_f32x4*)p;
+    hi += *(const wr_f32x4*)(p + 4);
+  }
+  wr_bf16x8 v;
+  for (int j = 0; j < 4; ++j) {
+    v[j] = (__bf16)lo[j];
+    v[4 + j] = (__bf16)hi[j];
+  }
+  *(wr_bf16x8*)(args.out + e) = v;
+}
+
+// Grouped-query attention backward: the key-major dK / dV kernel writes one
+// fp32 contribution per query head, [B, H, S, D] with H = G * splits heads
+// grouped by key/value head (query head h belongs to key/value head
+// h / splits).  out[g][e] = bf16(sum_r partials[(g * splits + r) * n + e]),
+// summed in head order, for the G = B * H_kv groups of n = S * D elements.
+// Each thread owns 8 consecutive elements of one group; n must be a multiple
+// of 8.
+struct wg_args {
+  const float* partials;   // [groups][splits][n]
+  __bf16* out;             // [groups][n]
+  long long n;
+  long long groups;
+  int splits;
+};
+
+extern "C" __global__ void __launch_bounds__(256) wir_group_reduce(const wg_args args) {
+  const long long e = ((long long)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e >= args.n * args.groups) return;
+  const long long g = e / args.n, off = e % args.n;
+  wr_f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
+  const float* base = args.partials + g * args.splits * args.n + off;
+  for (int r = 0; r < args.splits; ++r) {
+    const float* p = base + r * args.n;
     lo += *(const wr_f32x4*)p;
     hi += *(const wr_f32x4*)(p + 4);
   }

@@ -324,6 +324,19 @@ class IntAffineOp(Op):
     add: int = 0
 
 
+@dataclass(frozen=True)
+class IntDivOp(Op):
+    """*Additive.* Integer ``result = input // divisor`` (non-negative operands).
+
+    Maps a query head to its key/value head under grouped-query attention,
+    ``kv_head = head // (query heads per kv head)`` (``mha_h100.cu:74,519``).
+    """
+
+    result: Value
+    input: Union[Value, int]
+    divisor: Union[Value, int]
+
+
 # --- buffer operations (post-pipeline form) --------------------------------
 
 @dataclass(frozen=True)

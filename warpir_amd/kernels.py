@@ -77,6 +77,14 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_bwd_prep_d64": lambda: build_mha_bwd_prep_kernel(d=64, block_q=128, wave_rows=32),
     "mha_bwd_dq_d64": lambda: _bwd(build_mha_bwd_dq_kernel(d=64, block_q=128, block_kv=64, wave_rows=32), 64),
     "mha_bwd_dkdv_d64": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=64, block_kv=128, block_q=64, wave_rows=32), 64),
+    # grouped-query attention (K / V with H / HR heads): forward, and backward with per-query-head
+    # fp32 dK / dV contributions that api.attention_backward sums per key/value head
+    "mha_d128_gqa": lambda: _mha(128, 128, 64, 32, causal=False, gqa=True),
+    "mha_d128_causal_gqa": lambda: _mha(128, 128, 64, 32, causal=True, gqa=True),
+    "mha_d64_causal_gqa": lambda: _mha(64, 128, 64, 32, causal=True, gqa=True),
+    **{f"mha_bwd_{part}_d{d}{'_causal' if c else ''}_gqa": (
+        lambda part=part, d=d, c=c: _bwd(_BWD_BUILDERS[part](d, c, True), d))
+       for part in ("dq", "dkdv") for d in (128, 64) for c in (False, True)},
     # causal backward: dq stops at the diagonal; dkdv starts at it (transposed mask)
     "mha_bwd_dq_d128_causal": lambda: _bwd(build_mha_bwd_dq_kernel(d=128, block_q=128, block_kv=64, wave_rows=32,
                                                                    causal=True, name="mha_bwd_dq_causal"), 128),
@@ -89,14 +97,25 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
 }
 
 
+_BWD_BUILDERS = {
+    "dq": lambda d, causal, gqa: build_mha_bwd_dq_kernel(
+        d=d, block_q=128, block_kv=64, wave_rows=32, causal=causal, gqa=gqa,
+        name="mha_bwd_dq" + ("_causal" if causal else "") + ("_gqa" if gqa else "")),
+    "dkdv": lambda d, causal, gqa: build_mha_bwd_dkdv_kernel(
+        d=d, block_kv=128, block_q=64, wave_rows=32, causal=causal, gqa=gqa,
+        name="mha_bwd_dkdv" + ("_causal" if causal else "") + ("_gqa" if gqa else "")),
+}
+
+
 def _bwd(kernel: Kernel, d: int) -> Kernel:
     return kernel_pass(kernel, cost_model=gfx950_attention_cost_model(128, 64, d))
 
 
 def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_budget: int = 64 * 1024,
-         min_stages: int = 2, rescale_slack: Optional[float] = None) -> Kernel:
+         min_stages: int = 2, rescale_slack: Optional[float] = None, gqa: bool = False) -> Kernel:
+    name = ("mha_fwd_causal" if causal else "mha_fwd") + ("_gqa" if gqa else "")
     k = build_mha_forward_kernel(d=d, block_q=block_q, block_kv=block_kv, wave_rows=wave_rows, causal=causal,
-                                 name="mha_fwd_causal" if causal else "mha_fwd", rescale_slack=rescale_slack)
+                                 name=name, rescale_slack=rescale_slack, gqa=gqa)
     return kernel_pass(k, cost_model=gfx950_attention_cost_model(block_q, block_kv, d, lds_budget=lds_budget,
                                                                  min_stages=min_stages))
 

@@ -46,7 +46,7 @@ from typing import Dict, List, Optional, Sequence, Tuple, Union
 
 from warpir_amd.ir.ops import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, CopyOp, DivRowOp, Exp2Op, ForOp,
-    IntAffineOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp, NegInftyOp,
+    IntAffineOp, IntDivOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp, NegInftyOp,
     LazyMaxOp, Op, RowMaxOp, RowSumOp, SubColOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
     WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
@@ -678,6 +678,9 @@ class CDNA4Lowerer:
             return
         if isinstance(op, IntAffineOp):
             w(f"{pad}const int {self._var(op.result)} = ({self._int(op.input)}) * {op.mul} + {op.add};")
+            return
+        if isinstance(op, IntDivOp):
+            w(f"{pad}const int {self._var(op.result)} = ({self._int(op.input)}) / ({self._int(op.divisor)});")
             return
         if isinstance(op, TMAStoreOp):
             self._emit_store(op, out, depth)
@@ -1741,6 +1744,8 @@ class _Sim:
                     self.drain = (self.drain + 1) % op.a_slot.modulus
             elif isinstance(op, IntAffineOp):
                 self.env[low.resolve(op.result.name)] = self.val(op.input) * op.mul + op.add
+            elif isinstance(op, IntDivOp):
+                self.env[low.resolve(op.result.name)] = self.val(op.input) // max(1, self.val(op.divisor))
             elif isinstance(op, ForOp):
                 start = self.val(op.start)
                 step = self.val(op.step) or 1

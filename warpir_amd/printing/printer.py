@@ -19,6 +19,7 @@ from warpir_amd.ir.ops import (
     Exp2Op,
     ForOp,
     IntAffineOp,
+    IntDivOp,
     LoadVecOp,
     Kernel,
     Log2Op,
@@ -131,6 +132,7 @@ _LINE: Dict[type, Callable[[Op], str]] = {
     SubColOp: lambda op: _call(op, "sub_col", op.tile, op.vec),
     LoadVecOp: lambda op: f"{op.result!r} = load_vec({op.source!r}, {_coords(op.coords)})",
     LazyMaxOp: lambda op: f"{op.result!r} = lazy_max({op.prev!r}, {op.cand!r}, {op.slack})",
+    IntDivOp: lambda op: f"{op.result!r} = int_div({_coord(op.input)}, {_coord(op.divisor)})",
 }
 
 

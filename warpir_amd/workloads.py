@@ -26,6 +26,7 @@ from warpir_amd.ir import (
     GPUType,
     GlobalType,
     IntAffineOp,
+    IntDivOp,
     IntType,
     IterArg,
     Kernel,
@@ -135,12 +136,13 @@ def build_attention_kernel(d: int = 64, block: int = 64, warp_rows: int = 16,
     """
     return _attention(name="attention_fwd", d=d, block_q=block, block_kv=block,
                       wave_rows=warp_rows, scale=scale, multi_head=False, causal=False,
-                      with_lse=False, rescale_slack=None)
+                      with_lse=False, rescale_slack=None, gqa=False)
 
 
 def build_mha_forward_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64,
                              wave_rows: int = 32, causal: bool = False, with_lse: bool = True,
-                             name: str = "mha_fwd", rescale_slack: Optional[float] = None) -> Kernel:
+                             name: str = "mha_fwd", rescale_slack: Optional[float] = None,
+                             gqa: bool = False) -> Kernel:
     """Multi-head FlashAttention forward over ``[B, H, S, D]`` tensors.
 
     Program ``(blockIdx.x, blockIdx.y, blockIdx.z)`` = (query tile, head,
@@ -155,14 +157,18 @@ def build_mha_forward_kernel(d: int = 128, block_q: int = 128, block_kv: int = 6
     only moves when a tile's maximum exceeds it by more than that
     (``LazyMaxOp``), so the O / l rescale is skipped on most steps and
     ``P <= 2**slack``.  ``None`` builds the plain online softmax.
+
+    ``gqa`` (additive): grouped-query attention.  K and V have ``H / HR``
+    heads (an extra int input ``HR`` after ``N``); query head ``h`` reads
+    key/value head ``h // HR`` (``mha_h100.cu:74``).
     """
     return _attention(name=name, d=d, block_q=block_q, block_kv=block_kv, wave_rows=wave_rows,
                       scale=LOG2E / math.sqrt(d), multi_head=True, causal=causal,
-                      with_lse=with_lse, rescale_slack=rescale_slack)
+                      with_lse=with_lse, rescale_slack=rescale_slack, gqa=gqa)
 
 
 def _attention(*, name, d, block_q, block_kv, wave_rows, scale, multi_head, causal, with_lse,
-               rescale_slack):
+               rescale_slack, gqa):
     q_tile = SharedTileType(GPUType.bf16, block_q, d)
     kv_tile = SharedTileType(GPUType.bf16, block_kv, d)
     if multi_head:
@@ -183,6 +189,11 @@ def _attention(*, name, d, block_q, block_kv, wave_rows, scale, multi_head, caus
         bh = (batch, head)
     else:
         bh = (0, 0)
+    head_map, bh_kv, extra_inputs = [], bh, ()
+    if gqa:
+        hr, kv_head = Value("HR", IntType()), Value("kv_head", IntType())
+        head_map = [IntDivOp(result=kv_head, input=head, divisor=hr)]
+        bh_kv, extra_inputs = (batch, kv_head), (hr,)
 
     def v(n, t):
         return Value(n, t)
@@ -204,8 +215,8 @@ def _attention(*, name, d, block_q, block_kv, wave_rows, scale, multi_head, caus
 
     scores = att
     body = [
-        TMALoadOp(result=k_sh, source=K, coords=(*bh, i, 0)),
-        TMALoadOp(result=v_sh, source=V, coords=(*bh, i, 0)),
+        TMALoadOp(result=k_sh, source=K, coords=(*bh_kv, i, 0)),
+        TMALoadOp(result=v_sh, source=V, coords=(*bh_kv, i, 0)),
         WaitOp(values=(k_sh, v_sh)),
         ZeroOp(result=att_zero),
         MMAOp(result=att, a=q_sh, b=k_sh, accum=att_zero, transpose_b=True),
@@ -251,6 +262,7 @@ def _attention(*, name, d, block_q, block_kv, wave_rows, scale, multi_head, caus
         results=(o_final, max_final, norm_final),
     )
     kernel_body = [
+        *head_map,
         TMALoadOp(result=q_sh, source=Q, coords=(*bh, q_idx, 0)),
         WaitOp(values=(q_sh,)),
         ZeroOp(result=o_init),
@@ -275,7 +287,7 @@ def _attention(*, name, d, block_q, block_kv, wave_rows, scale, multi_head, caus
             TMAStoreOp(source=lse, dest=L, coords=(*bh, q_idx, 0)),
         ]
         outputs.append(L)
-    return Kernel(name=name, inputs=(Q, K, V, n_kv), outputs=tuple(outputs), body=tuple(kernel_body))
+    return Kernel(name=name, inputs=(Q, K, V, n_kv, *extra_inputs), outputs=tuple(outputs), body=tuple(kernel_body))
 
 
 # ---------------------------------------------------------------------------
@@ -323,11 +335,12 @@ def build_mha_bwd_prep_kernel(d: int = 128, block_q: int = 128, wave_rows: int =
 
 
 def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64, wave_rows: int = 32,
-                            name: str = "mha_bwd_dq", causal: bool = False) -> Kernel:
+                            name: str = "mha_bwd_dq", causal: bool = False, gqa: bool = False) -> Kernel:
     """``dQ`` of attention forward, query-major: one program per query tile
     ``(blockIdx.x, head, batch)``; the loop walks key tiles.  With
     ``causal`` it stops at the query tile's last row and masks the scores
-    as the causal forward does."""
+    as the causal forward does; with ``gqa`` K and V come from key/value
+    head ``head // HR`` (an extra int input)."""
     scale = 1.0 / math.sqrt(d)
     q_glob, vec_glob, q_tile = _bwd_globals(d, block_q)
     kv_glob, _, kv_tile = _bwd_globals(d, block_kv)
@@ -336,6 +349,11 @@ def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64
     n_kv = Value("N", IntType())
     q_idx, head, batch = (Value(n, IntType()) for n in ("blockIdx.x", "blockIdx.y", "blockIdx.z"))
     bh = (batch, head)
+    head_map, bh_kv, extra_inputs = [], bh, ()
+    if gqa:
+        hr, kv_head = Value("HR", IntType()), Value("kv_head", IntType())
+        head_map = [IntDivOp(result=kv_head, input=head, divisor=hr)]
+        bh_kv, extra_inputs = (batch, kv_head), (hr,)
     att_f = RegTileType(GPUType.fp32, wave_rows, block_kv)
     att_b = RegTileType(GPUType.bf16, wave_rows, block_kv)
     acc = RegTileType(GPUType.fp32, wave_rows, d)
@@ -361,8 +379,8 @@ def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64
         induction_var=i, start=0, stop=stop, step=1, tile_size=block_kv,
         iter_args=(IterArg(block_arg=dq_acc, init=dq_init),),
         body=(
-            TMALoadOp(result=k_sh, source=K, coords=(*bh, i, 0)),
-            TMALoadOp(result=v_sh, source=V, coords=(*bh, i, 0)),
+            TMALoadOp(result=k_sh, source=K, coords=(*bh_kv, i, 0)),
+            TMALoadOp(result=v_sh, source=V, coords=(*bh_kv, i, 0)),
             WaitOp(values=(k_sh, v_sh)),
             ZeroOp(result=zero),
             MMAOp(result=s_t, a=q_sh, b=k_sh, accum=zero, transpose_b=True),
@@ -381,6 +399,7 @@ def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64
         results=(dq_final,),
     )
     body = (
+        *head_map,
         TMALoadOp(result=q_sh, source=Q, coords=(*bh, q_idx, 0)),
         TMALoadOp(result=do_sh, source=dO, coords=(*bh, q_idx, 0)),
         WaitOp(values=(q_sh, do_sh)),
@@ -393,27 +412,43 @@ def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64
         MulScalarOp(result=dq_out, input=dq_final, scalar=scale),
         TMAStoreOp(source=dq_out, dest=dQ, coords=(*bh, q_idx, 0)),
     )
-    return Kernel(name=name, inputs=(Q, K, V, dO, L, Dv, n_kv), outputs=(dQ,), body=body)
+    return Kernel(name=name, inputs=(Q, K, V, dO, L, Dv, n_kv, *extra_inputs), outputs=(dQ,), body=body)
 
 
 def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 64, wave_rows: int = 32,
-                              name: str = "mha_bwd_dkdv", causal: bool = False) -> Kernel:
+                              name: str = "mha_bwd_dkdv", causal: bool = False, gqa: bool = False) -> Kernel:
     """``dK`` and ``dV`` of attention forward, key-major: one program per key
     tile ``(blockIdx.x, head, batch)``; the loop walks query tiles.  Scores
     are computed transposed (``S^T = K Q^T``), so the per-query LSE and Dv
     are row_vecs, read from fp32 ``block_q x 1`` shared tiles that are loaded
     (and pipelined) with the query tile.  With ``causal`` the loop starts at
     the first query tile that sees the key tile (``mha_h100.cu:525``) and the
-    transposed scores are masked (``CausalMaskOp(transposed=True)``)."""
+    transposed scores are masked (``CausalMaskOp(transposed=True)``).
+
+    With ``gqa`` one program runs per (key tile, *query* head): K and V come
+    from key/value head ``head // HR`` (an extra int input) and the outputs
+    are that query head's fp32 contributions ``dK_part`` / ``dV_part``
+    ``[B, H, S, D]``; the ``HR`` contributions of a key/value head are then
+    summed (the reference adds them with TMA reduce-add stores,
+    ``mha_h100.cu:456-479``)."""
     scale = 1.0 / math.sqrt(d)
     kv_glob, vec_glob, kv_tile = _bwd_globals(d, block_kv)
     q_glob, qvec_glob, q_tile = _bwd_globals(d, block_q)
     Q, K, V, dO = Value("Q", q_glob), Value("K", kv_glob), Value("V", kv_glob), Value("dO", q_glob)
     L, Dv = Value("L", qvec_glob), Value("Dv", qvec_glob)
-    dK, dV = Value("dK", kv_glob), Value("dV", kv_glob)
+    if gqa:
+        part_glob = GlobalType(GPUType.fp32, kv_tile)
+        dK, dV = Value("dK_part", part_glob), Value("dV_part", part_glob)
+    else:
+        dK, dV = Value("dK", kv_glob), Value("dV", kv_glob)
     n_q = Value("N", IntType())
     kv_idx, head, batch = (Value(n, IntType()) for n in ("blockIdx.x", "blockIdx.y", "blockIdx.z"))
     bh = (batch, head)
+    head_map, bh_kv, extra_inputs = [], bh, ()
+    if gqa:
+        hr, kv_head = Value("HR", IntType()), Value("kv_head", IntType())
+        head_map = [IntDivOp(result=kv_head, input=head, divisor=hr)]
+        bh_kv, extra_inputs = (batch, kv_head), (hr,)
     st_f = RegTileType(GPUType.fp32, wave_rows, block_q)
     st_b = RegTileType(GPUType.bf16, wave_rows, block_q)
     acc = RegTileType(GPUType.fp32, wave_rows, d)
@@ -471,8 +506,9 @@ def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 
         results=(dk_final, dv_final),
     )
     body = (
-        TMALoadOp(result=k_sh, source=K, coords=(*bh, kv_idx, 0)),
-        TMALoadOp(result=v_sh, source=V, coords=(*bh, kv_idx, 0)),
+        *head_map,
+        TMALoadOp(result=k_sh, source=K, coords=(*bh_kv, kv_idx, 0)),
+        TMALoadOp(result=v_sh, source=V, coords=(*bh_kv, kv_idx, 0)),
         WaitOp(values=(k_sh, v_sh)),
         ZeroOp(result=dk_init),
         ZeroOp(result=dv_init),
@@ -482,4 +518,4 @@ def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 
         TMAStoreOp(source=dk_out, dest=dK, coords=(*bh, kv_idx, 0)),
         TMAStoreOp(source=dv_final, dest=dV, coords=(*bh, kv_idx, 0)),
     )
-    return Kernel(name=name, inputs=(Q, K, V, dO, L, Dv, n_q), outputs=(dK, dV), body=body)
+    return Kernel(name=name, inputs=(Q, K, V, dO, L, Dv, n_q, *extra_inputs), outputs=(dK, dV), body=body)
