@@ -139,7 +139,7 @@ def attention_forward(q, k, v, causal: bool = False, out=None, lse=None,
     hr = _head_ratio("attention_forward", q, k, v)
     if variant is None:
         variant = {(128, False): "mha_d128", (64, True): "mha_d64_causal",
-                   (128, True): "mha_d128_causal"}.get((d, causal))
+                   (128, True): "mha_d128_causal", (64, False): "mha_d64"}.get((d, causal))
         if variant is None:
             raise ValueError(f"attention_forward: no kernel variant for D={d}, causal={causal}")
         if hr > 1:

@@ -64,6 +64,7 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
                                                            causal=True, name="mha_fwd_causal"),
     "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True),
     "mha_d128_causal": lambda: _mha(128, 128, 64, 32, causal=True),
+    "mha_d64": lambda: _mha(64, 128, 64, 32, causal=False),
     # running max moves only by more than 2**8: the O rescale is skipped on most steps
     "mha_d128_lazy": lambda: _mha(128, 128, 64, 32, causal=False, rescale_slack=8.0),
     "mha_d64_causal_lazy": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=8.0),
@@ -82,6 +83,7 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_d128_gqa": lambda: _mha(128, 128, 64, 32, causal=False, gqa=True),
     "mha_d128_causal_gqa": lambda: _mha(128, 128, 64, 32, causal=True, gqa=True),
     "mha_d64_causal_gqa": lambda: _mha(64, 128, 64, 32, causal=True, gqa=True),
+    "mha_d64_gqa": lambda: _mha(64, 128, 64, 32, causal=False, gqa=True),
     **{f"mha_bwd_{part}_d{d}{'_causal' if c else ''}_gqa": (
         lambda part=part, d=d, c=c: _bwd(_BWD_BUILDERS[part](d, c, True), d))
        for part in ("dq", "dkdv") for d in (128, 64) for c in (False, True)},
