@@ -118,6 +118,24 @@ def test_attention_pingpong_groups_follow_the_warp_assignment():
     assert group_line(CDNA4Target(wave_groups={"k": 0, "v": 0})) == []
 
 
+def test_warp_specialized_gemm_form():
+    k = kernels.kernel("gemm_256x128_ws")
+    low = kernels.lowerer("gemm_256x128_ws")
+    src = low.lower(k)
+    body = src[src.rindex('extern "C" __global__'):]
+    assert low.num_threads == 512 and "amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)" in body
+    assert "const bool wir_producer = wir_wave_hw >= 4;" in body
+    # every DMA is issued by a producer wave, every MFMA helper and store by a consumer wave
+    for line in body.split("\n"):
+        if "::load<WIR_AL>(" in line:
+            assert line.strip().startswith("if (wir_producer)"), line
+    assert body.count("if (!wir_producer) {") >= 3
+    assert low.launch_config(k, {"A": (512, 512), "B": (512, 512), "C_global": (512, 512)}).block == (512, 1, 1)
+    # the same kernel without the option is the plain 4-wave form
+    plain = kernels.lowerer("gemm_256x128").lower(kernels.kernel("gemm_256x128"))
+    assert "wir_producer" not in plain
+
+
 def test_kernarg_layout_matches_globals_struct():
     assert ctypes.sizeof(GL) == 48
     s = kernarg_struct(build_gemm_kernel())

@@ -48,6 +48,10 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
                                             lds_budget=80 * 1024, split_k=True),
     # 8 wavefronts (2 per SIMD) of 128x64 in the ping-pong form, K=32 with a 4-slot ring.
     "gemm_256_pp": lambda: _gemm_mi355x(32, wave_m=128, wave_n=64, load_units=12),
+    # warp-specialised: 4 MFMA wavefronts of 128x64 plus 4 DMA-only wavefronts (2 per SIMD)
+    "gemm_256x128_ws": lambda: _gemm_mi355x(64, block_n=128, wave_n=64),
+    "gemm_256x128_ws_k32": lambda: _gemm_mi355x(32, block_n=128, wave_n=64, load_units=12),
+    "gemm_256x128": lambda: _gemm_mi355x(64, block_n=128, wave_n=64),
     # The reference's single-head attention IR (tests/attention_baseline.py:46-186).
     "attn_ref_ssa": lambda: build_attention_kernel(),
     # Multi-head FlashAttention forward, [B, H, S, D] with LSE: SSA form (loads
@@ -125,6 +129,9 @@ def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_
 TARGETS: Dict[str, dict] = {
     "mha_d128_ovl": {"attn_overlap": True},
     "mha_d128_pp_swapped": {"wave_groups": {"k": 1, "v": 0}},
+    # (the rotated pipeline's extra fragment registers do not fit two waves per SIMD)
+    "gemm_256x128_ws": {"warp_specialize": True, "rotate_mma": False, "mve": False},
+    "gemm_256x128_ws_k32": {"warp_specialize": True, "rotate_mma": False},
     "mha_d64_causal_ovl": {"attn_overlap": True},
 }
 

@@ -100,6 +100,12 @@ class CDNA4Target:
     # e.g. "k", "v") in the 8-wavefront attention ping-pong.  None: take it
     # from the warp assigner's solution for the kernel (passes.warp_assigner).
     wave_groups: Optional[Dict[str, int]] = None
+    # Warp specialisation for ring-pipelined MMA loops: the workgroup gets a
+    # second set of wavefronts (waves NW..2NW-1) that only issue the LDS-DMA
+    # loads, while waves 0..NW-1 only read LDS and issue MFMAs.  Both sets pass
+    # every barrier; gfx950 has no setmaxnreg, so both get the same register
+    # allocation (two waves per SIMD: at most 256 per lane).
+    warp_specialize: bool = False
 
 
 @dataclass
@@ -148,6 +154,7 @@ class CDNA4Lowerer:
         self._allocate_lds()
         self._staged = self._staged_stores()
         self.wait_n, self.war_barrier = _schedule(kernel, self)
+        self._ws = self._warp_specialized(kernel)
         body: List[str] = []
         self._emit_ops(kernel.body, body, 1)
         return self._assemble(kernel, body)
@@ -167,11 +174,32 @@ class CDNA4Lowerer:
                 if isinstance(c, Value) and c.name in BUILTINS:
                     axis = BUILTINS.index(c.name)
                     grid[axis] = max(grid[axis], _ceil_div(shape[pos], units[pos]))
-        return LaunchConfig(grid=tuple(grid), block=(self.geo.nw * 64, 1, 1), dyn_lds=0)
+        return LaunchConfig(grid=tuple(grid), block=(self.num_threads, 1, 1), dyn_lds=0)
 
     @property
     def num_threads(self) -> int:
-        return self.geo.nw * 64
+        return self.geo.nw * 64 * (2 if self._ws else 1)
+
+    def _warp_specialized(self, kernel: Kernel) -> bool:
+        """Whether the warp-specialised form applies: requested, four compute
+        wavefronts, and every top-level loop a rotatable ring pipeline (loads
+        and one buffered MMA), so that producer and consumer waves pass the
+        same barriers."""
+        if not self.target.warp_specialize or self.geo.nw != 4:
+            return False
+        def ring(loop: ForOp) -> bool:
+            body = [o for o in loop.body if not isinstance(o, YieldOp)]
+            return bool(body) and isinstance(body[0], WaitBufOp) and isinstance(body[-1], MMABufOp) and all(
+                isinstance(o, TMALoadBufOp) for o in body[1:-1])
+        loops = [op for op in kernel.body if isinstance(op, ForOp)]
+        return bool(loops) and all(ring(lp) for lp in loops) and not any(
+            isinstance(op, (MMAOp, CopyOp)) for op in _walk(kernel.body))
+
+    def _consumer_only(self, lines: List[str], pad: str) -> List[str]:
+        """In the warp-specialised form, wrap *lines* so only MFMA waves run them."""
+        if not self._ws or not lines:
+            return lines
+        return [f"{pad}if (!wir_producer) {{", *[("  " + ln) for ln in lines], f"{pad}}}"]
 
     def lds_bytes(self) -> int:
         return self.lds_total
@@ -204,6 +232,7 @@ class CDNA4Lowerer:
         self._fused_loads: Dict[int, List[Op]] = {}
         self._fused_ids: set = set()
         self._var_override: Dict[str, str] = {}  # resolved value name -> C++ variable
+        self._ws = False                          # warp-specialised form (producer / consumer waves)
 
     def _build_aliases(self, ops) -> None:
         """iter_arg init / loop results / yielded values -> block arg (``lowering.py:87-100``)."""
@@ -510,7 +539,7 @@ class CDNA4Lowerer:
         if isinstance(op, ZeroOp) or isinstance(op, NegInftyOp):
             val = "0.f" if isinstance(op, ZeroOp) else "-__builtin_inff()"
             if isinstance(op.result.type, (RegTileType, ColVecType)):
-                w(f"{pad}wir::fill({self._var(op.result)}, {val});")
+                out.extend(self._consumer_only([f"{pad}wir::fill({self._var(op.result)}, {val});"], pad))
                 return
             raise LoweringError(f"{type(op).__name__} on {op.result.type}")
         if isinstance(op, TMALoadOp) and self.resolve(op.result.name) in self._register_tiles:
@@ -535,7 +564,8 @@ class CDNA4Lowerer:
             src = op.source
             sub = src.type.sub_tile_type
             b, d, rt, ct = (self._int(c) for c in op.coords)
-            w(f"{pad}{self._load_call(op, 'load<WIR_AL>(', ptr, key)});")
+            call = f"{self._load_call(op, 'load<WIR_AL>(', ptr, key)});"
+            w(f"{pad}if (wir_producer) {call}" if self._ws else f"{pad}{call}")
             return
         pp = self._pp_ops.get(id(op))
         if pp is not None and pp[0] == "skip":
@@ -576,13 +606,25 @@ class CDNA4Lowerer:
                     calls.append(f"if (q >= {total} && q < {total + n}) {loader}::issue<WIR_AL>(q - {total}, "
                                  f"{lptr}, {g}, src{n_ld}_, wir_wave);")
                     total += n
-                w(f"{pad}{pipe}.run<{total}>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int q) {{")
-                for c in calls:
-                    w(f"{pad}  {c}")
-                w(f"{pad}}});")
+                if self._ws:
+                    # producers issue this step's DMAs back to back; consumers run the MFMAs
+                    w(f"{pad}if (wir_producer) {{")
+                    w(f"{pad}  for (int q = 0; q < {total}; ++q) {{")
+                    for c in calls:
+                        w(f"{pad}    {c}")
+                    w(f"{pad}  }}")
+                    w(f"{pad}}} else {{")
+                    w(f"{pad}  {pipe}.run<0>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int) {{}});")
+                    w(f"{pad}}}")
+                else:
+                    w(f"{pad}{pipe}.run<{total}>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int q) {{")
+                    for c in calls:
+                        w(f"{pad}  {c}")
+                    w(f"{pad}}});")
             else:
-                w(f"{pad}wir::mma_AB<{ms}, {t.rows}, {t.cols}, {self.stile(a_key)}, {self.stile(b_key)}>"
-                  f"({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0);")
+                out.extend(self._consumer_only(
+                    [f"{pad}wir::mma_AB<{ms}, {t.rows}, {t.cols}, {self.stile(a_key)}, {self.stile(b_key)}>"
+                     f"({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0);"], pad))
             if self._var(op.result) != acc:
                 w(f"{pad}{self._var(op.result)} = {acc};")
             if isinstance(op.a_slot, BufSlotExpr):
@@ -789,12 +831,14 @@ class CDNA4Lowerer:
             if not self._stage_barrier_done:
                 out.append(f"{pad}wir::barrier();  // ring buffers dead: LDS becomes per-wave staging")
                 self._stage_barrier_done = True
-            out.append(f"{pad}wir::store_tile_staged({g}, {self._var(op.source)}, {b}, {d}, "
-                       f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols} + wave_col0, "
-                       f"smem + wir_wave * {self._staged[id(op)]});")
+            out.extend(self._consumer_only(
+                [f"{pad}wir::store_tile_staged({g}, {self._var(op.source)}, {b}, {d}, "
+                 f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols} + wave_col0, "
+                 f"smem + wir_wave * {self._staged[id(op)]});"], pad))
         elif isinstance(st, RegTileType):
-            out.append(f"{pad}wir::store_tile({g}, {self._var(op.source)}, {b}, {d}, "
-                       f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols} + wave_col0);")
+            out.extend(self._consumer_only(
+                [f"{pad}wir::store_tile({g}, {self._var(op.source)}, {b}, {d}, "
+                 f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols} + wave_col0);"], pad))
         elif isinstance(st, ColVecType):
             out.append(f"{pad}if (wave_col0 == 0) wir::store_vec({g}, {self._var(op.source)}, {b}, {d}, "
                        f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols});")
@@ -833,10 +877,11 @@ class CDNA4Lowerer:
                 self._fused_loads[id(mma)] = loads
                 self._fused_ids |= {id(o) for o in loads}
             out.append(f"{pad}{pipe_t} {name};")
-            out.append(f"{pad}{name}.init();")
+            out.extend(self._consumer_only([f"{pad}{name}.init();"], pad))
         self._emit_loop(op, stop, out, depth)
         if rotated is not None:
-            out.append(f"{pad}{self._rotated[id(rotated[0])]}.finish({self._var(rotated[0].accum)});")
+            out.extend(self._consumer_only(
+                [f"{pad}{self._rotated[id(rotated[0])]}.finish({self._var(rotated[0].accum)});"], pad))
 
     def _ring_modulus(self, loop: ForOp) -> Optional[int]:
         """Slot count of the ring slots this loop indexes by its induction variable."""
@@ -1584,8 +1629,8 @@ class CDNA4Lowerer:
                   and op.input.name == "blockIdx.x" and op.mul > 0}
         causal_x = any(isinstance(op, ForOp) and isinstance(op.stop, Value) and self.resolve(op.stop.name) in from_x
                        for op in _walk(kernel.body))
-        wpe = self.geo.waves_per_eu
-        nt = self.geo.nw * 64
+        wpe = max(self.geo.waves_per_eu, 2) if self._ws else self.geo.waves_per_eu
+        nt = self.num_threads
         pid = _pid_code(dims, self.target, reverse_x=causal_x)
         src = [
             "// Generated by warpir_amd.lowering.CDNA4Lowerer for gfx950 -- do not edit.",
@@ -1600,7 +1645,10 @@ class CDNA4Lowerer:
             f"{kernel.name}(const {kernel.name}_globals globals) {{",
             f"  __shared__ __attribute__((aligned(1024))) char smem[{max(self.lds_total, 1024)}];",
             *pid,
-            f"  const int wir_wave = wir::wave_id();",
+            *([f"  const int wir_wave_hw = wir::wave_id();",
+               f"  const bool wir_producer = wir_wave_hw >= {self.geo.nw};  // DMA-only waves",
+               f"  const int wir_wave = wir_wave_hw % {self.geo.nw};"] if self._ws
+              else [f"  const int wir_wave = wir::wave_id();"]),
             f"  const int wave_row0 = (wir_wave / {self.geo.nw_c}) * {self._wave_rows()};",
             f"  const int wave_col0 = (wir_wave % {self.geo.nw_c}) * {self._wave_cols()};",
         ]
