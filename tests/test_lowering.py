@@ -102,10 +102,13 @@ def test_attention_overlap_form():
 def test_attention_pingpong_groups_follow_the_warp_assignment():
     from warpir_amd.lowering.cdna4 import CDNA4Target
     from warpir_amd.passes.warp_assigner import assign_waves
+    from warpir_amd.lowering.cdna4 import ASSIGN_ITERATIONS
     k = kernels.kernel("mha_d128_pp")
-    sol = assign_waves(k, num_warps=2)
+    sol = assign_waves(k, num_warps=2, iterations=ASSIGN_ITERATIONS)
     k_group = sol.type_warp["k_load"]
     assert sol.type_warp["v_load"] == 1 - k_group
+    # the short unroll the lowering uses places the streams as the longer one does
+    assert assign_waves(k, num_warps=2, iterations=4).type_warp == sol.type_warp
 
     def group_line(target):
         src = CDNA4Lowerer(target).lower(k)
@@ -128,9 +131,16 @@ def test_warp_specialized_gemm_form():
     # every DMA is issued by a producer wave, every MFMA helper and store by a consumer wave
     for line in body.split("\n"):
         if "::load<WIR_AL>(" in line:
-            assert line.strip().startswith("if (wir_producer)"), line
+            assert line.strip().startswith(("if (wir_producer)", "if (!wir_producer)")), line
     assert body.count("if (!wir_producer) {") >= 3
     assert low.launch_config(k, {"A": (512, 512), "B": (512, 512), "C_global": (512, 512)}).block == (512, 1, 1)
+    # the warp assigner places A with the MMA and B on another warp: the MFMA waves issue A,
+    # the DMA waves B, and each set waits on its own share of the in-flight DMAs
+    assert "if (!wir_producer) wir::Loader<wir::STile<256, 64, 0>, 4>::load" in body
+    assert "if (wir_producer) wir::Loader<wir::STile<64, 128, 1>, 4>::load" in body
+    assert "if (wir_producer) wir::wait_vm_barrier<4>(); else wir::wait_vm_barrier<8>();" in body
+    allp = kernels.lowerer("gemm_256x128_ws_all").lower(kernels.kernel("gemm_256x128_ws_all"))
+    assert "if (!wir_producer) wir::Loader" not in allp and "wir::wait_vm_barrier<12>();" in allp
     # the same kernel without the option is the plain 4-wave form
     plain = kernels.lowerer("gemm_256x128").lower(kernels.kernel("gemm_256x128"))
     assert "wir_producer" not in plain

@@ -51,6 +51,7 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # warp-specialised: 4 MFMA wavefronts of 128x64 plus 4 DMA-only wavefronts (2 per SIMD)
     "gemm_256x128_ws": lambda: _gemm_mi355x(64, block_n=128, wave_n=64),
     "gemm_256x128_ws_k32": lambda: _gemm_mi355x(32, block_n=128, wave_n=64, load_units=12),
+    "gemm_256x128_ws_all": lambda: _gemm_mi355x(64, block_n=128, wave_n=64),
     "gemm_256x128": lambda: _gemm_mi355x(64, block_n=128, wave_n=64),
     # The reference's single-head attention IR (tests/attention_baseline.py:46-186).
     "attn_ref_ssa": lambda: build_attention_kernel(),
@@ -130,8 +131,12 @@ TARGETS: Dict[str, dict] = {
     "mha_d128_ovl": {"attn_overlap": True},
     "mha_d128_pp_swapped": {"wave_groups": {"k": 1, "v": 0}},
     # (the rotated pipeline's extra fragment registers do not fit two waves per SIMD)
+    # A / B load streams split between the wave sets as the warp assigner places them (A with the
+    # MFMA waves, B on the DMA waves); _all puts both on the DMA waves
     "gemm_256x128_ws": {"warp_specialize": True, "rotate_mma": False, "mve": False},
     "gemm_256x128_ws_k32": {"warp_specialize": True, "rotate_mma": False},
+    "gemm_256x128_ws_all": {"warp_specialize": True, "rotate_mma": False, "mve": False,
+                            "wave_groups": {"a": 1, "b": 1}},
     "mha_d64_causal_ovl": {"attn_overlap": True},
 }
 

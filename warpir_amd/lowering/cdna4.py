@@ -57,6 +57,11 @@ from warpir_amd.ir.types import (
 )
 
 BUILTINS = ("blockIdx.x", "blockIdx.y", "blockIdx.z")
+# Steady-state iterations the warp assigner unrolls when the lowering asks it
+# for a wave-group split: one keeps the exact search to a fraction of a
+# second on every kernel here, and gives the same type -> warp placement as
+# longer unrolls where those finish.
+ASSIGN_ITERATIONS = 1
 HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "csrc",
                            "wir_cdna4.h")
 ROWREAD, TRREAD = 0, 1
@@ -155,6 +160,9 @@ class CDNA4Lowerer:
         self._staged = self._staged_stores()
         self.wait_n, self.war_barrier = _schedule(kernel, self)
         self._ws = self._warp_specialized(kernel)
+        self._ws_producer_streams = self._ws_streams(kernel) if self._ws else set()
+        if self._ws and self._ws_producer_streams is None:
+            self._ws = False
         body: List[str] = []
         self._emit_ops(kernel.body, body, 1)
         return self._assemble(kernel, body)
@@ -194,6 +202,46 @@ class CDNA4Lowerer:
         loops = [op for op in kernel.body if isinstance(op, ForOp)]
         return bool(loops) and all(ring(lp) for lp in loops) and not any(
             isinstance(op, (MMAOp, CopyOp)) for op in _walk(kernel.body))
+
+    def _ws_streams(self, kernel: Kernel):
+        """Ring buffers whose loads the DMA-only waves issue; the MFMA waves
+        issue the others.  The split comes from ``CDNA4Target.wave_groups``
+        (stream -> group; group 1 = DMA waves) or, when that is None, from the
+        warp assigner: a load type placed on the MMA's warp stays with the
+        MFMA waves, one placed on another warp goes to the DMA waves.  None
+        if the vmcnt thresholds do not split between the two sets."""
+        def stream(buf_name: str) -> str:
+            return buf_name[:-len("_bufs")] if buf_name.endswith("_bufs") else buf_name
+        bufs = sorted({self.resolve(op.buf.name) for op in _walk(kernel.body) if isinstance(op, TMALoadBufOp)})
+        groups = self.target.wave_groups
+        if groups is None:
+            from warpir_amd.passes.warp_assigner import assign_waves
+            sol = assign_waves(kernel, num_warps=2, iterations=ASSIGN_ITERATIONS)
+            if sol is None:
+                return None
+            mma_warp = next((w for t, w in sol.type_warp.items() if t.startswith("mma")), 0)
+            groups = {t[:-len("_load")]: int(w != mma_warp) for t, w in sol.type_warp.items() if t.endswith("_load")}
+        producers = {b for b in bufs if groups.get(stream(b), 1) == 1}
+        # per-wave DMA instructions of one ring step, per set
+        per = {b: self.loads_per_wave(self.tile_type_of(b)) for b in bufs}
+        total = sum(per.values())
+        self._ws_share = (sum(per[b] for b in producers), total - sum(per[b] for b in producers), total)
+        for n in self.wait_n.values():
+            if n % total:
+                return None
+        return producers
+
+    def _ws_wait(self, n: int) -> str:
+        """wait_vm_barrier for the two wave sets: each waits on its own share of
+        the n in-flight DMA instructions that one all-loading wave would have."""
+        prod, cons, total = self._ws_share
+        np_, nc = n // total * prod, n // total * cons
+        if np_ == nc:
+            return f"wir::wait_vm_barrier<{np_}>();"
+        return f"if (wir_producer) wir::wait_vm_barrier<{np_}>(); else wir::wait_vm_barrier<{nc}>();"
+
+    def _ws_issuer(self, buf_name: str) -> str:
+        return "wir_producer" if self.resolve(buf_name) in self._ws_producer_streams else "!wir_producer"
 
     def _consumer_only(self, lines: List[str], pad: str) -> List[str]:
         """In the warp-specialised form, wrap *lines* so only MFMA waves run them."""
@@ -565,7 +613,11 @@ class CDNA4Lowerer:
             sub = src.type.sub_tile_type
             b, d, rt, ct = (self._int(c) for c in op.coords)
             call = f"{self._load_call(op, 'load<WIR_AL>(', ptr, key)});"
-            w(f"{pad}if (wir_producer) {call}" if self._ws else f"{pad}{call}")
+            if self._ws:
+                who = self._ws_issuer(op.buf.name) if isinstance(op, TMALoadBufOp) else "wir_producer"
+                w(f"{pad}if ({who}) {call}")
+            else:
+                w(f"{pad}{call}")
             return
         pp = self._pp_ops.get(id(op))
         if pp is not None and pp[0] == "skip":
@@ -577,7 +629,7 @@ class CDNA4Lowerer:
             if isinstance(op, WaitOp) and all(self.resolve(v.name) in self._register_tiles for v in op.values):
                 return
             n = self.wait_n.get(id(op), 0)
-            w(f"{pad}wir::wait_vm_barrier<{n}>();")
+            w(f"{pad}{self._ws_wait(n)}" if self._ws else f"{pad}wir::wait_vm_barrier<{n}>();")
             return
         if isinstance(op, SlotViewOp):
             return  # views are resolved to LDS pointers where they are read
@@ -593,6 +645,7 @@ class CDNA4Lowerer:
             if pipe is not None:
                 loads = self._fused_loads.get(id(op), [])
                 calls, total = [], 0
+                pcalls, ptotal = [], 0   # warp-specialised: the DMA waves' share
                 for n_ld, ld in enumerate(loads):
                     lptr, lkey = self._buf_ptr(ld.buf, ld.slot)
                     n = self.loads_per_wave(ld.buf.type.tile_type)
@@ -603,18 +656,27 @@ class CDNA4Lowerer:
                     self._aligned_checks.add((self.stile(lkey), _cname(ld.source.name)[2:]))
                     w(f"{pad}const auto src{n_ld}_ = {loader}::prep<WIR_AL>({g}, {bb}, {dd}, ({rt}) * {sub.rows}, "
                       f"({ct}) * {sub.cols});")
+                    if self._ws and self.resolve(ld.buf.name) in self._ws_producer_streams:
+                        pcalls.append(f"if (q >= {ptotal} && q < {ptotal + n}) {loader}::issue<WIR_AL>(q - {ptotal}, "
+                                      f"{lptr}, {g}, src{n_ld}_, wir_wave);")
+                        ptotal += n
+                        continue
                     calls.append(f"if (q >= {total} && q < {total + n}) {loader}::issue<WIR_AL>(q - {total}, "
                                  f"{lptr}, {g}, src{n_ld}_, wir_wave);")
                     total += n
                 if self._ws:
-                    # producers issue this step's DMAs back to back; consumers run the MFMAs
+                    # the DMA waves issue their streams back to back; the MFMA waves
+                    # run the MFMAs, spreading any streams assigned to them
                     w(f"{pad}if (wir_producer) {{")
-                    w(f"{pad}  for (int q = 0; q < {total}; ++q) {{")
-                    for c in calls:
+                    w(f"{pad}  for (int q = 0; q < {ptotal}; ++q) {{")
+                    for c in pcalls:
                         w(f"{pad}    {c}")
                     w(f"{pad}  }}")
                     w(f"{pad}}} else {{")
-                    w(f"{pad}  {pipe}.run<0>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int) {{}});")
+                    w(f"{pad}  {pipe}.run<{total}>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int q) {{")
+                    for c in calls:
+                        w(f"{pad}    {c}")
+                    w(f"{pad}  }});")
                     w(f"{pad}}}")
                 else:
                     w(f"{pad}{pipe}.run<{total}>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int q) {{")
@@ -993,7 +1055,7 @@ class CDNA4Lowerer:
         groups = self.target.wave_groups
         if groups is None:
             from warpir_amd.passes.warp_assigner import assign_waves
-            sol = assign_waves(self.kernel, num_warps=2)
+            sol = assign_waves(self.kernel, num_warps=2, iterations=ASSIGN_ITERATIONS)
             if sol is None:
                 return None
             groups = {t[:-len("_load")]: w for t, w in sol.type_warp.items() if t.endswith("_load")}
