@@ -17,7 +17,7 @@ bf16 MFMA peak (2.5 PFLOP/s).  ``cpu_baseline``: the reference's oracle
 path (``torch.matmul`` on fp32, naive fp32 attention) on the host cores,
 on a bounded sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--compare]
 """
 from __future__ import annotations
 
@@ -292,6 +292,49 @@ def mfma_ceiling(iters: int = 20000):
     return out
 
 
+# Schedule alternatives timed by --compare (each is a kernels.VARIANTS entry with its lowering
+# options): the evidence behind the default choices.
+COMPARE_GEMM = ["gemm_256_k64", "gemm_256_k32", "gemm_256_pp", "gemm_256x128", "gemm_256x128_ws_all",
+                "gemm_256x128_ws", "gemm_128_k64"]
+COMPARE_FA = ["mha_d128", "mha_d128_q256", "mha_d128_pp", "mha_d128_ovl", "mha_d128_lazy"]
+
+
+def bench_compare(steps: int, warmup: int):
+    """Time each schedule variant at the headline shapes, one after the other (in the order of
+    COMPARE_GEMM then COMPARE_FA, so a kernel trace of the run can be matched to it)."""
+    import torch
+
+    from oracle.torch_ref import seeded_normal
+    from warpir_amd import kernels
+
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    n = 8192
+    a = seeded_normal((n, n), 0, 0.1).cuda()
+    b = seeded_normal((n, n), 1, 0.1).cuda()
+    c = torch.empty(n, n, dtype=torch.bfloat16, device="cuda")
+    for name in COMPARE_GEMM:
+        h = kernels.handle(name)
+        ms, _ = _time_launches(lambda: h(A=a, B=b, N=n, C_global=c), steps, warmup, stream)
+        lc = h.lowerer.launch_config(h.kernel, {"A": tuple(a.shape), "B": tuple(b.shape), "C_global": tuple(c.shape)})
+        out[name] = {"ms": ms, "tflops": 2.0 * n ** 3 / (ms * 1e-3) / 1e12, "options": kernels.TARGETS.get(name, {}),
+                     "grid": list(lc.grid), "block": lc.block[0]}
+    del a, b, c
+    bsz, heads, seq, d = 16, 16, 4096, 128
+    q, k, v = (seeded_normal((bsz, heads, seq, d), sd).cuda() for sd in (0, 1, 2))
+    o = torch.empty_like(q)
+    lse = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
+    flops = 4.0 * bsz * heads * seq * seq * d
+    for name in COMPARE_FA:
+        h = kernels.handle(name)
+        ms, _ = _time_launches(lambda: h(Q=q, K=k, V=v, N=seq, O=o, L=lse), steps, warmup, stream)
+        lc = h.lowerer.launch_config(h.kernel, {"Q": tuple(q.shape), "K": tuple(k.shape), "V": tuple(v.shape),
+                                                "O": tuple(o.shape), "L": tuple(lse.shape)})
+        out[name] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "options": kernels.TARGETS.get(name, {}),
+                     "grid": list(lc.grid), "block": lc.block[0]}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,6 +343,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["gemm", "fa"], default=None)
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
+    ap.add_argument("--compare", action="store_true",
+                    help="also time the schedule alternatives (COMPARE_GEMM / COMPARE_FA) at the headline shapes")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (read MIB, write MIB) three times, "
                          "the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -332,6 +377,10 @@ def main() -> int:
     if args.only is None and not args.no_extra:
         print("[bench] other configurations", file=sys.stderr, flush=True)
         extra = bench_extra(max(5, args.steps // 2), max(2, args.warmup // 2))
+    compare = None
+    if args.compare:
+        print("[bench] schedule comparison", file=sys.stderr, flush=True)
+        compare = bench_compare(max(5, args.steps // 2), max(2, args.warmup // 2))
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
@@ -356,6 +405,8 @@ def main() -> int:
         line["other_configs"] = extra
     if ceiling is not None:
         line["mfma_ceiling"] = ceiling
+    if compare is not None:
+        line["schedule_comparison"] = compare
     line["device"] = info
     print(json.dumps(line))
     return 0
