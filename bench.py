@@ -351,7 +351,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "both workloads shard with no communication (see DESIGN.md)", file=sys.stderr)
+              "GEMM shards by output rows and attention by (batch, head), with no communication",
+              file=sys.stderr)
         return 2
 
     import torch
