@@ -40,24 +40,28 @@ def _waits(src):
 
 def test_pipelined_gemm_waits_keep_one_stage_in_flight():
     src = CDNA4Lowerer(CDNA4Target(mve=False)).lower(kernels.kernel("gemm_256_k32"))
-    # 256x32 A tile and 32x256 B tile: 16 KiB each = 16 DMA instructions / 4 waves = 4 + 4 per stage
-    assert _waits(src) == [8, 8, 0]
+    # 256x32 A tile and 32x256 B tile: 16 KiB each = 16 DMA instructions / 4 waves = 4 + 4 per stage;
+    # the last wait is the drain before the staged store
+    assert _waits(src) == [8, 8, 0, 0]
 
 
 def test_modulo_variable_expansion_unrolls_by_ring_size():
     src = CDNA4Lowerer().lower(kernels.kernel("gemm_256_k32"))
-    # 3-slot ring: 3 unrolled copies with constant slots + the run-time remainder loop, then 2 drains
-    assert _waits(src) == [8, 8, 8, 8, 8, 0]
+    # 3-slot ring: 3 unrolled copies with constant slots + the run-time remainder loop, then 2 drains,
+    # then the drain before the staged store
+    assert _waits(src) == [8, 8, 8, 8, 8, 0, 0]
     loop = src[src.index("int wir_base_i"):]
     assert "(smem + 0 + 2 * 16384)" in loop and "% 3) * 16384" in loop
-    # the ring's waits already order every slot reuse: the only barrier is the one before the staged store
-    assert src.count("wir::barrier()") == 1 and src.index("wir::barrier()") > src.index("pipe0.finish")
+    # the ring's waits already order every slot reuse: the only other barrier is the drain before
+    # the staged store
+    assert src.count("wir::barrier()") == 0
+    assert src.rindex("wir::wait_vm_barrier<0>()") > src.index("pipe0.finish")
 
 
 def test_final_store_is_staged_through_lds():
     src = CDNA4Lowerer().lower(kernels.kernel("gemm_256_k64"))
     tail = src[src.index("pipe0.finish"):]
-    assert tail.index("wir::barrier()") < tail.index("store_tile_staged") and "wir::store_tile(" not in tail
+    assert tail.index("wir::wait_vm_barrier<0>()") < tail.index("store_tile_staged") and "wir::store_tile(" not in tail
     assert "smem + wir_wave * 32768" in tail        # 128x128 bf16 per wavefront
     plain = CDNA4Lowerer(CDNA4Target(staged_stores=False)).lower(kernels.kernel("gemm_256_k64"))
     plain = plain[plain.rindex('extern "C" __global__'):]
@@ -65,11 +69,19 @@ def test_final_store_is_staged_through_lds():
     # the attention output is staged; its fp32 LSE column vector is stored directly
     fa = CDNA4Lowerer().lower(kernels.kernel("mha_d128"))
     assert "store_tile_staged(globals.O" in fa and "store_vec(globals.L" in fa
+    # the staging area is the K/V ring, into which the loop's last prefetch may still be landing:
+    # every wave drains its DMAs (vmcnt 0) before the barrier that hands the LDS over
+    for name in ("mha_d128", "mha_d64_causal", "mha_d128_pp", "mha_d128_ovl", "mha_bwd_dq_d128", "mha_bwd_dkdv_d128"):
+        src = kernels.lowerer(name).lower(kernels.kernel(name))
+        body = src[src.rindex('extern "C" __global__'):]
+        pre = body[: body.index("wir::store_tile_staged(")]
+        last_sync = max(pre.rfind("wir::barrier()"), pre.rfind("wir::wait_vm_barrier<"))
+        assert pre[last_sync:].startswith("wir::wait_vm_barrier<0>();  // ring buffers dead"), name
 
 
 def test_ssa_gemm_waits_for_everything_and_guards_reuse():
     src = CDNA4Lowerer().lower(build_gemm_kernel())
-    assert _waits(src) == [0]
+    assert _waits(src) == [0, 0]        # every k-step, and the drain before the staged store
     body = src[src.index("for (int v_i"):]
     assert body.index("wir::barrier()") < body.index("Loader")
 

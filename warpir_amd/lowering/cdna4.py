@@ -891,7 +891,9 @@ class CDNA4Lowerer:
         st = self._rtype(op.source)
         if isinstance(st, RegTileType) and id(op) in self._staged:
             if not self._stage_barrier_done:
-                out.append(f"{pad}wir::barrier();  // ring buffers dead: LDS becomes per-wave staging")
+                # the loop's last prefetches (tiles past its end, or past a causal stop) may still be
+                # landing in the ring: drain this wave's DMAs before any wave reuses the LDS
+                out.append(f"{pad}wir::wait_vm_barrier<0>();  // ring buffers dead: LDS becomes per-wave staging")
                 self._stage_barrier_done = True
             out.extend(self._consumer_only(
                 [f"{pad}wir::store_tile_staged({g}, {self._var(op.source)}, {b}, {d}, "
