@@ -49,7 +49,7 @@ def test_reference_gemm_footprint_by_hand():
     # accumulates in place), so nothing else is live.
     r = count_registers(workloads.build_gemm_kernel())
     assert r.peak == 16
-    assert r.waves_per_simd == 2
+    assert r.waves_per_simd == 3            # 16 + 40 fits the 168 registers of three waves
 
 
 def test_reference_attention_footprint_by_hand():
@@ -59,12 +59,13 @@ def test_reference_attention_footprint_by_hand():
     r = count_registers(workloads.build_attention_kernel())
     assert r.hoisted == {"q_shared": 8}
     assert 16 + 2 + 8 < r.peak < 128
-    assert r.waves_per_simd == 2
+    assert r.waves_per_simd == (3 if r.need <= 168 else 2)
 
 
 # both choices, every kernel family (GEMM tiles, forward, causal, backward)
 _WAVES_CASES = ["gemm_ref_ssa", "gemm_256_k64", "gemm_128_k64", "gemm_128x32_k64", "mha_d128", "mha_d64_causal",
-                "mha_bwd_prep_d128", "mha_bwd_dq_d128", "mha_bwd_dkdv_d128", "mha_bwd_dq_d64", "mha_bwd_dkdv_d64"]
+                "mha_d64", "mha_d64_causal_gqa", "mha_bwd_prep_d128", "mha_bwd_dq_d128", "mha_bwd_dkdv_d128",
+                "mha_bwd_dq_d64", "mha_bwd_dkdv_d64"]
 
 
 @pytest.mark.skipif(not HAVE_HIPCC, reason="hipcc not available")
@@ -73,13 +74,21 @@ def test_waves_choice_matches_hipcc(name):
     from warpir_amd.runtime import compile_source, resource_usage
     kern = kernels.kernel(name)
     report = count_registers(kern)
-    src = kernels.lowerer(name).lower(kern)
+    lw = kernels.lowerer(name)
+    src = lw.lower(kern)
+    waves = lw.waves_per_simd
+    # the lowering takes the register count's choice; above two waves it is capped by the
+    # workgroups the LDS holds
+    expected = report.waves_per_simd
+    if expected > 2:
+        expected = max(2, min(expected, 160 * 1024 // lw.lds_total * lw.geo.nw // 4))
+    assert waves == expected
     compile_source(src)
     usage = resource_usage(src)
     assert usage, "no resource-usage remarks in the compile log"
-    assert usage["occupancy"] >= report.waves_per_simd
-    if report.waves_per_simd == 2:
-        assert usage["vgpr"] + usage.get("agpr", 0) <= 256
+    assert usage["occupancy"] >= waves
+    if waves >= 2:
+        assert usage["vgpr"] + usage.get("agpr", 0) <= 512 // waves // 8 * 8
         assert usage.get("vgpr_spill", 0) == 0
     else:
         assert usage["vgpr"] + usage.get("agpr", 0) > 256, usage

@@ -262,6 +262,7 @@ class CDNA4Lowerer:
         self.roles: Dict[str, int] = {}
         self.lds_off: Dict[str, int] = {}
         self.lds_total = 0
+        self.waves_per_simd: Optional[int] = None    # the amdgpu_waves_per_eu the kernel is compiled for
         self._staged: Dict[int, int] = {}
         self._stage_barrier_done = False
         self.globals: List[Value] = []
@@ -1694,6 +1695,12 @@ class CDNA4Lowerer:
         causal_x = any(isinstance(op, ForOp) and isinstance(op.stop, Value) and self.resolve(op.stop.name) in from_x
                        for op in _walk(kernel.body))
         wpe = max(self.geo.waves_per_eu, 2) if self._ws else self.geo.waves_per_eu
+        if wpe > 2 and self.target.waves_per_eu is None:
+            # more than two waves per SIMD only where as many workgroups fit in the LDS, and not in
+            # the overlapped attention form (its second score tile is not in the register count)
+            by_lds = self.target.lds_bytes // max(self.lds_total, 1024) * self.geo.nw // 4
+            wpe = 2 if self.target.attn_overlap else max(2, min(wpe, by_lds))
+        self.waves_per_simd = wpe
         nt = self.num_threads
         pid = _pid_code(dims, self.target, reverse_x=causal_x)
         src = [

@@ -52,9 +52,14 @@ class RegisterReport:
 
     @property
     def waves_per_simd(self) -> int:
-        """Wavefronts of this kernel one SIMD can hold: 2 when the need fits
-        half the register file (256 per lane), else 1."""
-        return 2 if self.need <= FILE // 2 else 1
+        """Wavefronts of this kernel one SIMD can hold by registers, at most 3:
+        the file is split evenly and allocated in blocks of 8, so 3 waves get
+        168 registers per lane, 2 get 256 and 1 gets all 512.  (The lowering
+        also caps this by how many workgroups the LDS holds.)"""
+        for w in (3, 2):
+            if self.need <= FILE // w // 8 * 8:
+                return w
+        return 1
 
 
 def value_registers(t) -> int:
