@@ -99,3 +99,20 @@ def test_api_gemm_routes_short_m_to_split_k(gpu):
     c = api.gemm(a.cuda(), b.cuda())
     torch.cuda.synchronize()
     assert rel_err(c.cpu(), gemm_ref(a, b)) <= TOL
+
+
+def test_gemm_repeated_launches_bitwise_stable(gpu):
+    """GEMM 8192^3 (the headline kernel), 6 launches into the same C: no atomics and a fixed
+    accumulation order, so every launch reproduces the first bit for bit."""
+    n = 8192
+    announce(f"gemm_256_k64 repeated launches {n}^3")
+    a = seeded_normal((n, n), 50, 0.1).cuda()
+    b = seeded_normal((n, n), 51, 0.1).cuda()
+    h = kernels.handle("gemm_256_k64")
+    c = torch.empty(n, n, dtype=torch.bfloat16, device="cuda")
+    h(A=a, B=b, N=n, C_global=c)
+    first = c.clone()
+    for it in range(5):
+        c.fill_(float("nan"))
+        h(A=a, B=b, N=n, C_global=c)
+        assert torch.equal(c, first), it
