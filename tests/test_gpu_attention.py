@@ -108,9 +108,13 @@ def test_mha_full_size_sampled(gpu):
         assert (lse[bi, hi] - ref_lse).abs().max().item() <= 1e-2
 
 
-@pytest.mark.parametrize("causal,shape", [(True, (8, 32, 8192, 64)), (False, (16, 16, 4096, 128))])
-def test_mha_repeated_launches_bitwise_stable(gpu, causal, shape):
-    """Configs 5 and 4 at full size, 12 launches back to back into the same buffers.
+@pytest.mark.parametrize("variant,causal,shape", [
+    (None, True, (8, 32, 8192, 64)), (None, False, (16, 16, 4096, 128)), (None, True, (16, 16, 4096, 128)),
+    ("mha_d128_pp", False, (16, 16, 4096, 128)), ("mha_d128_ovl", False, (16, 16, 4096, 128)),
+    ("mha_d64_causal_ovl", True, (8, 32, 8192, 64))])
+def test_mha_repeated_launches_bitwise_stable(gpu, variant, causal, shape):
+    """Configs 5 and 4 at full size (default kernels and the ping-pong / overlapped
+    schedule forms), 12 launches back to back into the same buffers.
 
     The kernels have no atomics, so every launch must reproduce the first bit
     for bit over all heads.  Regression: the O tile is staged through the LDS
@@ -118,16 +122,16 @@ def test_mha_repeated_launches_bitwise_stable(gpu, causal, shape):
     causal stop) can still be landing there; without a DMA drain before the
     staging barrier a late tile overwrote staged rows now and then.  Two heads
     are also checked against the oracle."""
-    announce(f"mha repeated launches causal={causal} {shape}")
+    announce(f"mha repeated launches {variant or 'default'} causal={causal} {shape}")
     q, k, v = (seeded_normal(shape, sd) for sd in (30, 31, 32))
     qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
-    o, lse = api.attention_forward(qd, kd, vd, causal=causal)
+    o, lse = api.attention_forward(qd, kd, vd, causal=causal, variant=variant)
     o0, lse0 = o.clone(), lse.clone()
     unstable = []
     for it in range(11):
         o.fill_(float("nan"))
         lse.fill_(float("nan"))
-        api.attention_forward(qd, kd, vd, causal=causal, out=o, lse=lse)
+        api.attention_forward(qd, kd, vd, causal=causal, out=o, lse=lse, variant=variant)
         if not (torch.equal(o, o0) and torch.equal(lse, lse0)):
             bad = (o != o0).flatten(2).any(-1).nonzero().tolist()
             unstable.append((it, bad[:8]))
