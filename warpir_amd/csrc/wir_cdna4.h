@@ -99,7 +99,14 @@ __device__ __forceinline__ int ccol(int i, int lh) {
 //              phase: the 16 rows land in 16 distinct 16-byte bank slots;
 //   TRREAD  -- ds_read_b64_tr_b16, per 32 lanes 4 rows x 64 bytes: the 4
 //              rows' 64-byte runs land in 4 disjoint bank ranges.
-enum Role { ROWREAD = 0, TRREAD = 1 };
+//   BOTH    -- a tile read both ways (K in the dQ kernel, Q and dO in the
+//              dK/dV kernel): the row bits that separate the 4 rows of a
+//              transposed read pick the 64-byte run, and the others permute
+//              the 16-byte chunks inside it, so 16 consecutive rows still take
+//              16 distinct chunk slots.  Conflict-free for both patterns in the
+//              256-byte bank space (TRREAD would leave the row reads 4-way
+//              conflicted).
+enum Role { ROWREAD = 0, TRREAD = 1, BOTH = 2 };
 
 template <int CPR, int ROLE>
 __device__ __forceinline__ int swz(int row) {
@@ -109,6 +116,9 @@ __device__ __forceinline__ int swz(int row) {
     if (CPR == 4) return ((row >> 1) ^ (row >> 2)) & 3;
     if (CPR == 2) return (row >> 2) & 1;
     return 0;
+  } else if (ROLE == BOTH && CPR >= 8) {
+    if (CPR >= 16) return ((row & 3) << 2) | ((row >> 2) & 3);
+    return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
   } else {
     if (CPR >= 16) return ((row & 3) << 2) | (row & 2);
     if (CPR == 8) return (row & 3) << 1;

@@ -64,7 +64,7 @@ BUILTINS = ("blockIdx.x", "blockIdx.y", "blockIdx.z")
 ASSIGN_ITERATIONS = 1
 HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "csrc",
                            "wir_cdna4.h")
-ROWREAD, TRREAD = 0, 1
+ROWREAD, TRREAD, BOTH = 0, 1, 2
 
 
 class LoweringError(ValueError):
@@ -396,17 +396,17 @@ class CDNA4Lowerer:
         return _Geometry(nw=nw, nw_c=nw_c, ms=ms, waves_per_eu=self._waves_for(kernel, nw))
 
     def _assign_roles(self, ops) -> None:
-        """ROWREAD for tiles read along k by rows, TRREAD for [K][N] tiles read across k."""
+        """ROWREAD for tiles read along k by rows, TRREAD for [K][N] tiles read across k,
+        BOTH for tiles read both ways."""
         def use(v: Value, role: int) -> None:
-            # A tile read both by rows and transposed (e.g. K in attention
-            # backward) takes the TRREAD swizzle: every read is correct under
-            # either swizzle, and the transposed reads are twice as many
-            # instructions per byte, so they get the conflict-free layout.
+            # A tile read both by rows and transposed (K in the dQ kernel, Q
+            # and dO in the dK/dV kernel) takes the BOTH swizzle, conflict-free
+            # for either read.
             key = self._lds_key(v)
             if key is None:
                 return
             if self.roles.setdefault(key, role) != role:
-                self.roles[key] = TRREAD
+                self.roles[key] = BOTH
 
         for op in _walk(ops):
             if isinstance(op, CopyOp) and isinstance(op.input.type, SharedTileType):
