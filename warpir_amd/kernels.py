@@ -78,10 +78,10 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_d64_causal_ovl": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=8.0, lds_budget=32 * 1024),
     # FlashAttention backward: Dv = rowsum(dO * O); query-major dQ; key-major dK, dV.
     "mha_bwd_prep_d128": lambda: build_mha_bwd_prep_kernel(d=128, block_q=128, wave_rows=32),
-    "mha_bwd_dq_d128": lambda: _bwd(build_mha_bwd_dq_kernel(d=128, block_q=128, block_kv=64, wave_rows=32), 128),
+    "mha_bwd_dq_d128": lambda: _bwd_dq(128, causal=False),
     "mha_bwd_dkdv_d128": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=128, block_kv=128, block_q=64, wave_rows=32), 128),
     "mha_bwd_prep_d64": lambda: build_mha_bwd_prep_kernel(d=64, block_q=128, wave_rows=32),
-    "mha_bwd_dq_d64": lambda: _bwd(build_mha_bwd_dq_kernel(d=64, block_q=128, block_kv=64, wave_rows=32), 64),
+    "mha_bwd_dq_d64": lambda: _bwd_dq(64, causal=False),
     "mha_bwd_dkdv_d64": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=64, block_kv=128, block_q=64, wave_rows=32), 64),
     # grouped-query attention (K / V with H / HR heads): forward, and backward with per-query-head
     # fp32 dK / dV contributions that api.attention_backward sums per key/value head
@@ -93,20 +93,23 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
         lambda part=part, d=d, c=c: _bwd(_BWD_BUILDERS[part](d, c, True), d))
        for part in ("dq", "dkdv") for d in (128, 64) for c in (False, True)},
     # causal backward: dq stops at the diagonal; dkdv starts at it (transposed mask)
-    "mha_bwd_dq_d128_causal": lambda: _bwd(build_mha_bwd_dq_kernel(d=128, block_q=128, block_kv=64, wave_rows=32,
-                                                                   causal=True, name="mha_bwd_dq_causal"), 128),
+    "mha_bwd_dq_d128_causal": lambda: _bwd_dq(128, causal=True),
     "mha_bwd_dkdv_d128_causal": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=128, block_kv=128, block_q=64, wave_rows=32,
                                                                        causal=True, name="mha_bwd_dkdv_causal"), 128),
-    "mha_bwd_dq_d64_causal": lambda: _bwd(build_mha_bwd_dq_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
-                                                                  causal=True, name="mha_bwd_dq_causal"), 64),
+    "mha_bwd_dq_d64_causal": lambda: _bwd_dq(64, causal=True),
     "mha_bwd_dkdv_d64_causal": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=64, block_kv=128, block_q=64, wave_rows=32,
                                                                       causal=True, name="mha_bwd_dkdv_causal"), 64),
 }
 
 
+# The query-major dQ kernel steps over 32-row key tiles: its score, dP and dS tiles are then
+# 32 x 32 per wavefront, which leaves D=128 at two waves per SIMD (254 VGPRs, 32 KiB ring) and
+# D=64 at three, where 64-row key tiles needed the whole register file at D=128.
+DQ_BLOCK_KV = 32
+
 _BWD_BUILDERS = {
     "dq": lambda d, causal, gqa: build_mha_bwd_dq_kernel(
-        d=d, block_q=128, block_kv=64, wave_rows=32, causal=causal, gqa=gqa,
+        d=d, block_q=128, block_kv=DQ_BLOCK_KV, wave_rows=32, causal=causal, gqa=gqa,
         name="mha_bwd_dq" + ("_causal" if causal else "") + ("_gqa" if gqa else "")),
     "dkdv": lambda d, causal, gqa: build_mha_bwd_dkdv_kernel(
         d=d, block_kv=128, block_q=64, wave_rows=32, causal=causal, gqa=gqa,
@@ -115,7 +118,15 @@ _BWD_BUILDERS = {
 
 
 def _bwd(kernel: Kernel, d: int) -> Kernel:
+    if kernel.name.startswith("mha_bwd_dq"):
+        # two-slot ring of 32-row K and V tiles (32 KiB at D=128)
+        return kernel_pass(kernel, cost_model=gfx950_attention_cost_model(128, DQ_BLOCK_KV, d,
+                                                                          lds_budget=32 * 1024))
     return kernel_pass(kernel, cost_model=gfx950_attention_cost_model(128, 64, d))
+
+
+def _bwd_dq(d: int, causal: bool) -> Kernel:
+    return _bwd(_BWD_BUILDERS["dq"](d, causal, False), d)
 
 
 def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_budget: int = 64 * 1024,
