@@ -297,11 +297,13 @@ def mfma_ceiling(iters: int = 20000):
 COMPARE_GEMM = ["gemm_256_k64", "gemm_256_k32", "gemm_256_pp", "gemm_256x128", "gemm_256x128_ws_all",
                 "gemm_256x128_ws", "gemm_128_k64"]
 COMPARE_FA = ["mha_d128", "mha_d128_q256", "mha_d128_pp", "mha_d128_ovl", "mha_d128_lazy"]
+COMPARE_BWD_DQ = ["mha_bwd_dq_d128", "mha_bwd_dq_d128_kv64"]
 
 
 def bench_compare(steps: int, warmup: int):
     """Time each schedule variant at the headline shapes, one after the other (in the order of
-    COMPARE_GEMM then COMPARE_FA, so a kernel trace of the run can be matched to it)."""
+    COMPARE_GEMM, COMPARE_FA, then COMPARE_BWD_DQ, so a kernel trace of the run can be matched
+    to it).  The mha_fwd launches of the last FA variant leave O and LSE for the dQ kernels."""
     import torch
 
     from oracle.torch_ref import seeded_normal
@@ -331,6 +333,19 @@ def bench_compare(steps: int, warmup: int):
         lc = h.lowerer.launch_config(h.kernel, {"Q": tuple(q.shape), "K": tuple(k.shape), "V": tuple(v.shape),
                                                 "O": tuple(o.shape), "L": tuple(lse.shape)})
         out[name] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "options": kernels.TARGETS.get(name, {}),
+                     "grid": list(lc.grid), "block": lc.block[0]}
+    # backward dQ kernel: 3 of the S x S x D products, over the forward's O and LSE
+    do = seeded_normal((bsz, heads, seq, d), 3).cuda()
+    dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
+    kernels.handle("mha_bwd_prep_d128")(O=o, dO=do, Dv=dvec)
+    dq = torch.empty_like(q)
+    for name in COMPARE_BWD_DQ:
+        h = kernels.handle(name)
+        ms, _ = _time_launches(lambda: h(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq), steps, warmup, stream)
+        lc = h.lowerer.launch_config(h.kernel, {"Q": tuple(q.shape), "K": tuple(k.shape), "V": tuple(v.shape),
+                                                "dO": tuple(do.shape), "L": tuple(lse.shape),
+                                                "Dv": tuple(dvec.shape), "dQ": tuple(dq.shape)})
+        out[name] = {"ms": ms, "tflops": 1.5 * flops / (ms * 1e-3) / 1e12, "options": kernels.TARGETS.get(name, {}),
                      "grid": list(lc.grid), "block": lc.block[0]}
     return out
 

@@ -224,3 +224,22 @@ def test_mha_backward_repeated_launches_bitwise_stable(gpu, causal):
         api.attention_backward(q, k, v, o, lse, do, dq, dk, dv, causal=causal)
         for name, t, f in zip(("dQ", "dK", "dV"), (dq, dk, dv), first):
             assert torch.equal(t, f), (it, name)
+
+
+def test_dq_schedule_alternative_agrees(gpu):
+    """The previous dQ schedule (64-row key tiles), kept for the schedule comparison, against the
+    default (32-row key tiles) on the same forward outputs."""
+    b, h, s, d = 2, 3, 256, 128
+    announce(f"mha_bwd_dq_d128_kv64 vs default B={b} H={h} S={s}")
+    q, k, v, do = (seeded_normal((b, h, s, d), sd).cuda() for sd in (60, 61, 62, 63))
+    o, lse = api.attention_forward(q, k, v)
+    dvec = torch.empty(b, h, s, dtype=torch.float32, device="cuda")
+    kernels.handle("mha_bwd_prep_d128")(O=o, dO=do, Dv=dvec)
+    out = {}
+    for name in ("mha_bwd_dq_d128", "mha_bwd_dq_d128_kv64"):
+        dq = torch.full_like(q, float("nan"))
+        kernels.handle(name)(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=s, dQ=dq)
+        out[name] = dq.float().cpu()
+    torch.cuda.synchronize()
+    assert not torch.isnan(out["mha_bwd_dq_d128_kv64"]).any()
+    assert rel_err(out["mha_bwd_dq_d128_kv64"], out["mha_bwd_dq_d128"]) <= TOL

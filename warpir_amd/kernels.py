@@ -79,6 +79,10 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # FlashAttention backward: Dv = rowsum(dO * O); query-major dQ; key-major dK, dV.
     "mha_bwd_prep_d128": lambda: build_mha_bwd_prep_kernel(d=128, block_q=128, wave_rows=32),
     "mha_bwd_dq_d128": lambda: _bwd_dq(128, causal=False),
+    # the previous dQ schedule (64-row key tiles, one wave per SIMD), kept for the schedule comparison
+    "mha_bwd_dq_d128_kv64": lambda: kernel_pass(build_mha_bwd_dq_kernel(d=128, block_q=128, block_kv=64,
+                                                                        wave_rows=32),
+                                                cost_model=gfx950_attention_cost_model(128, 64, 128)),
     "mha_bwd_dkdv_d128": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=128, block_kv=128, block_q=64, wave_rows=32), 128),
     "mha_bwd_prep_d64": lambda: build_mha_bwd_prep_kernel(d=64, block_q=128, wave_rows=32),
     "mha_bwd_dq_d64": lambda: _bwd_dq(64, causal=False),
