@@ -243,3 +243,22 @@ def test_dq_schedule_alternative_agrees(gpu):
     torch.cuda.synchronize()
     assert not torch.isnan(out["mha_bwd_dq_d128_kv64"]).any()
     assert rel_err(out["mha_bwd_dq_d128_kv64"], out["mha_bwd_dq_d128"]) <= TOL
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_grouped_query_backward_repeated_launches_bitwise_stable(gpu, causal):
+    """Grouped-query backward (per-query-head fp32 dK / dV contributions summed by the HIP group
+    reduction in head order), 3 launches into the same buffers: bitwise identical each time."""
+    b, hq, hkv, s, d = 2, 8, 2, 1024, 128
+    announce(f"gqa backward repeated launches causal={causal} B={b} Hq={hq} Hkv={hkv} S={s}")
+    q, do = seeded_normal((b, hq, s, d), 70).cuda(), seeded_normal((b, hq, s, d), 73).cuda()
+    k, v = seeded_normal((b, hkv, s, d), 71).cuda(), seeded_normal((b, hkv, s, d), 72).cuda()
+    o, lse = api.attention_forward(q, k, v, causal=causal)
+    dq, dk, dv = api.attention_backward(q, k, v, o, lse, do, causal=causal)
+    first = [t.clone() for t in (dq, dk, dv)]
+    for it in range(2):
+        for t in (dq, dk, dv):
+            t.fill_(float("nan"))
+        api.attention_backward(q, k, v, o, lse, do, dq, dk, dv, causal=causal)
+        for name, t, f in zip(("dQ", "dK", "dV"), (dq, dk, dv), first):
+            assert torch.equal(t, f), (it, name)

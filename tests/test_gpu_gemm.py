@@ -116,3 +116,21 @@ def test_gemm_repeated_launches_bitwise_stable(gpu):
         c.fill_(float("nan"))
         h(A=a, B=b, N=n, C_global=c)
         assert torch.equal(c, first), it
+
+
+def test_split_k_repeated_launches_bitwise_stable(gpu):
+    """Split-K GEMM (fp32 partials per K slice, HIP reduction in slice order), 4 launches into the
+    same output and workspace: bitwise identical each time."""
+    from warpir_amd import api
+
+    m, n, k, splits = 128, 8192, 8192, 4
+    announce(f"gemm_split_k repeated launches {m}x{n}x{k} splits={splits}")
+    a = seeded_normal((m, k), 80, 0.1).cuda()
+    b = seeded_normal((k, n), 81, 0.1).cuda()
+    ws = torch.empty(splits * m * n, dtype=torch.float32, device="cuda")
+    c = api.gemm_split_k(a, b, splits=splits, workspace=ws)
+    first = c.clone()
+    for it in range(3):
+        c.fill_(float("nan"))
+        api.gemm_split_k(a, b, out=c, splits=splits, workspace=ws)
+        assert torch.equal(c, first), it
