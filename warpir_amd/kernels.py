@@ -86,7 +86,7 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_bwd_dkdv_d128": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=128, block_kv=128, block_q=64, wave_rows=32), 128),
     "mha_bwd_prep_d64": lambda: build_mha_bwd_prep_kernel(d=64, block_q=128, wave_rows=32),
     "mha_bwd_dq_d64": lambda: _bwd_dq(64, causal=False),
-    "mha_bwd_dkdv_d64": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=64, block_kv=128, block_q=64, wave_rows=32), 64),
+    "mha_bwd_dkdv_d64": lambda: _bwd(_BWD_BUILDERS["dkdv"](64, False, False), 64),
     # grouped-query attention (K / V with H / HR heads): forward, and backward with per-query-head
     # fp32 dK / dV contributions that api.attention_backward sums per key/value head
     "mha_d128_gqa": lambda: _mha(128, 128, 64, 32, causal=False, gqa=True),
@@ -101,8 +101,7 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_bwd_dkdv_d128_causal": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=128, block_kv=128, block_q=64, wave_rows=32,
                                                                        causal=True, name="mha_bwd_dkdv_causal"), 128),
     "mha_bwd_dq_d64_causal": lambda: _bwd_dq(64, causal=True),
-    "mha_bwd_dkdv_d64_causal": lambda: _bwd(build_mha_bwd_dkdv_kernel(d=64, block_kv=128, block_q=64, wave_rows=32,
-                                                                      causal=True, name="mha_bwd_dkdv_causal"), 64),
+    "mha_bwd_dkdv_d64_causal": lambda: _bwd(_BWD_BUILDERS["dkdv"](64, True, False), 64),
 }
 
 
@@ -110,13 +109,18 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
 # 32 x 32 per wavefront, which leaves D=128 at two waves per SIMD (254 VGPRs, 32 KiB ring) and
 # D=64 at three, where 64-row key tiles needed the whole register file at D=128.
 DQ_BLOCK_KV = 32
+# The key-major dK/dV kernel steps over 32-row query tiles at D=64: its transposed score and
+# gradient tiles are then 32 x 32 per wavefront and it fits two waves per SIMD (190-206 VGPRs,
+# where 64-row steps needed the whole file).  At D=128 the dK and dV accumulators keep it at
+# one wave either way, and 64-row steps measured faster.
+DKDV_BLOCK_Q = {128: 64, 64: 32}
 
 _BWD_BUILDERS = {
     "dq": lambda d, causal, gqa: build_mha_bwd_dq_kernel(
         d=d, block_q=128, block_kv=DQ_BLOCK_KV, wave_rows=32, causal=causal, gqa=gqa,
         name="mha_bwd_dq" + ("_causal" if causal else "") + ("_gqa" if gqa else "")),
     "dkdv": lambda d, causal, gqa: build_mha_bwd_dkdv_kernel(
-        d=d, block_kv=128, block_q=64, wave_rows=32, causal=causal, gqa=gqa,
+        d=d, block_kv=128, block_q=DKDV_BLOCK_Q[d], wave_rows=32, causal=causal, gqa=gqa,
         name="mha_bwd_dkdv" + ("_causal" if causal else "") + ("_gqa" if gqa else "")),
 }
 
