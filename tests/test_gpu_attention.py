@@ -31,8 +31,8 @@ def test_reference_attention_ir(gpu, n):
     assert rel_err(o.cpu(), ref) <= TOL
 
 
-@pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp", "mha_d128_pp_swapped",
-                                     "mha_d128_lazy", "mha_d128_ovl"])
+@pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp_swapped", "mha_d128_w4",
+                                     "mha_d128_online", "mha_d128_ovl"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 1, 64)])
 def test_mha_d128(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")
@@ -78,8 +78,9 @@ def test_mha_d64_causal(gpu, variant, b, h, s):
     assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-3 * ref_lse.abs().max().item() + 1e-3
 
 
-@pytest.mark.parametrize("variant,d,causal", [("mha_d128_lazy", 128, False), ("mha_d64_causal_lazy", 64, True),
-                                                    ("mha_d128_ovl", 128, False), ("mha_d64_causal_ovl", 64, True)])
+@pytest.mark.parametrize("variant,d,causal", [("mha_d128", 128, False), ("mha_d128_w4", 128, False),
+                                              ("mha_d64_causal_lazy", 64, True), ("mha_d128_ovl", 128, False),
+                                              ("mha_d64_causal_ovl", 64, True)])
 def test_mha_lazy_rescale_with_growing_scores(gpu, variant, d, causal):
     """Keys grow along the sequence, so the running max moves by more than
     the slack on later tiles and the rescale path runs too."""
@@ -110,7 +111,7 @@ def test_mha_full_size_sampled(gpu):
 
 @pytest.mark.parametrize("variant,causal,shape", [
     (None, True, (8, 32, 8192, 64)), (None, False, (16, 16, 4096, 128)), (None, True, (16, 16, 4096, 128)),
-    ("mha_d128_pp", False, (16, 16, 4096, 128)), ("mha_d128_ovl", False, (16, 16, 4096, 128)),
+    ("mha_d128_online", False, (16, 16, 4096, 128)), ("mha_d128_ovl", False, (16, 16, 4096, 128)),
     ("mha_d64_causal_ovl", True, (8, 32, 8192, 64))])
 def test_mha_repeated_launches_bitwise_stable(gpu, variant, causal, shape):
     """Configs 5 and 4 at full size (default kernels and the ping-pong / overlapped

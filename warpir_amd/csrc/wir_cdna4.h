@@ -1138,6 +1138,109 @@ __device__ __forceinline__ void to_bf16(BTile<MS, R, C>& out, const RTile<MS, R,
       }
 }
 
+// The speculative half of lazy_softmax on its own: computes pb and updates l
+// and returns true when no score exceeds m + slack; returns false (pb written,
+// m and l untouched) when the step needs lazy_softmax's exact path.  A loop
+// that calls this and leaves for the exact path keeps every access to o in
+// its MFMAs, so o keeps one register assignment around the loop.
+template <int MS, int R, int C>
+__device__ __forceinline__ bool lazy_softmax_fast(const RTile<MS, R, C>& s, const RVec<MS, R>& m, RVec<MS, R>& l,
+                                                  BTile<MS, R, C>& pb, float c, float slack) {
+  constexpr int RB = R / MS, CB = C / MS, G = BTile<MS, R, C>::G;
+  const float guard = __builtin_amdgcn_exp2f(slack * c);
+  float part[RB][4], sum[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part[rb][j] = 0.f;
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        bf16x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s.f[cb][rb][4 * g + j], c, -m.v[rb] * c));
+          part[rb][j] += e;
+          v[j] = (bf16)e;
+        }
+        pb.f[cb][rb][g] = v;
+      }
+  bool ok = true;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    sum[rb] = (part[rb][0] + part[rb][1]) + (part[rb][2] + part[rb][3]);
+    ok = ok && (sum[rb] <= guard);  // false for inf and NaN
+  }
+  if (__builtin_amdgcn_ballot_w64(!ok) != 0) return false;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) l.v[rb] = lane_group_reduce<MS>(sum[rb], OpAdd()) + l.v[rb];
+  return true;
+}
+
+// One online-softmax step with a lazy running maximum (the IR ops
+//   cand = row_max(s, m); m' = lazy_max(m, cand, slack);
+//   p = exp2(s*c - m'*c); corr = exp2(m*c - m'*c);
+//   l' = row_sum(p, l*corr); o' = o*corr; pb = bf16(p)
+// with m, l, o updated in place), evaluated speculatively.  The step is
+// first computed with m' = m.  Every p is at most its lane's partial row
+// sum, so when no partial sum exceeds 2^(slack*c) no score exceeds
+// m + slack: lazy_max keeps m on every row, corr is exactly 1 and o, l are
+// not rescaled, and the speculation is the IR's result.  Otherwise (the
+// first tile, where m = -inf, or a tile whose scores rise above m + slack)
+// the step is recomputed row by row with the exact lazy maximum.  The fast
+// path is one fma, one exp2, one add and half a bf16 pack per score: no row
+// maximum, no rescale.
+template <int MS, int R, int C, int DO>
+__device__ __forceinline__ void lazy_softmax(const RTile<MS, R, C>& s, RVec<MS, R>& m, RVec<MS, R>& l,
+                                             RTile<MS, R, DO>& o, BTile<MS, R, C>& pb, float c, float slack) {
+  if (lazy_softmax_fast(s, m, l, pb, c, slack)) return;
+  constexpr int RB = R / MS, CB = C / MS, G = BTile<MS, R, C>::G;
+  float corr[RB], sum[RB], part[RB][4];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    float x = s.f[0][rb][0];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int i = (cb == 0 ? 1 : 0); i < MF<MS>::CREGS; ++i) x = __builtin_fmaxf(x, s.f[cb][rb][i]);
+    const float cand = __builtin_fmaxf(lane_group_reduce<MS>(x, OpMax()), m.v[rb]);
+    const float mn = cand > m.v[rb] + slack ? cand : m.v[rb];
+    corr[rb] = __builtin_amdgcn_exp2f(m.v[rb] * c - mn * c);
+    m.v[rb] = mn;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part[rb][j] = 0.f;
+  }
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        bf16x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s.f[cb][rb][4 * g + j], c, -m.v[rb] * c));
+          part[rb][j] += e;
+          v[j] = (bf16)e;
+        }
+        pb.f[cb][rb][g] = v;
+      }
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    sum[rb] = (part[rb][0] + part[rb][1]) + (part[rb][2] + part[rb][3]);
+    l.v[rb] = lane_group_reduce<MS>(sum[rb], OpAdd()) + l.v[rb] * corr[rb];
+  }
+#pragma unroll
+  for (int cb = 0; cb < o.CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < MF<MS>::CREGS; ++i) o.f[cb][rb][i] *= corr[rb];
+}
+
 // Lower-triangular mask: keep (row, col) when col_g <= row_g with
 // row_g = row_tile*BR + row0 + r and col_g = col_tile*BC + c.
 template <bool TRANSPOSED, int MS, int R, int C>

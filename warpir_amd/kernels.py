@@ -58,21 +58,27 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # Multi-head FlashAttention forward, [B, H, S, D] with LSE: SSA form (loads
     # waited every KV step) and the pipelined prefetch form of kernel_pass.
     "mha_d128_ssa": lambda: build_mha_forward_kernel(d=128, block_q=128, block_kv=64, wave_rows=32),
-    "mha_d128": lambda: _mha(128, 128, 64, 32, causal=False),
-    # 256 query rows per workgroup (8 wavefronts): each K/V tile in LDS serves twice the rows.
+    # The config-4 kernel: 256 query rows (8 wavefronts of 32) in the ping-pong form (one wave
+    # group's MFMAs beside the other's softmax), a 4-slot K/V ring loaded two tiles ahead, and
+    # the online softmax with a lazy running max (lowered speculatively: no row max, no rescale
+    # unless a tile rises above the slack).
+    "mha_d128": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
+                             rescale_slack=LAZY_SLACK),
+    # the same with the K and V load streams on the opposite wave groups from the warp assigner's answer
+    "mha_d128_pp_swapped": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
+                                        rescale_slack=LAZY_SLACK),
+    # 4 wavefronts of 32 rows (two workgroups per CU), 2-slot ring: with the lazy softmax, and
+    # with the reference IR's exact online softmax (the previous config-4 kernel)
+    "mha_d128_w4": lambda: _mha(128, 128, 64, 32, causal=False, rescale_slack=LAZY_SLACK),
+    "mha_d128_online": lambda: _mha(128, 128, 64, 32, causal=False),
+    # 256 query rows per workgroup (8 wavefronts) in the plain loop (2-slot ring, no ping-pong)
     "mha_d128_q256": lambda: _mha(128, 256, 64, 32, causal=False),
-    # The same with a 3-slot K/V ring, lowered in 8-wavefront ping-pong form.
-    "mha_d128_pp": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=96 * 1024, min_stages=3),
-    # the same with the K and V streams on the opposite wave groups from the warp assigner's answer
-    "mha_d128_pp_swapped": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=96 * 1024, min_stages=3),
     "mha_d64_causal_ssa": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
                                                            causal=True, name="mha_fwd_causal"),
     "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True),
     "mha_d128_causal": lambda: _mha(128, 128, 64, 32, causal=True),
     "mha_d64": lambda: _mha(64, 128, 64, 32, causal=False),
-    # running max moves only by more than 2**8: the O rescale is skipped on most steps
-    "mha_d128_lazy": lambda: _mha(128, 128, 64, 32, causal=False, rescale_slack=8.0),
-    "mha_d64_causal_lazy": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=8.0),
+    "mha_d64_causal_lazy": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=LAZY_SLACK),
     # software-pipelined attention loop (QK of tile i+1 and PV of tile i carry tile i's softmax)
     "mha_d128_ovl": lambda: _mha(128, 128, 64, 32, causal=False, rescale_slack=8.0),
     "mha_d64_causal_ovl": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=8.0, lds_budget=32 * 1024),
@@ -104,6 +110,11 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_bwd_dkdv_d64_causal": lambda: _bwd(_BWD_BUILDERS["dkdv"](64, True, False), 64),
 }
 
+
+# Slack (in exp2 units) of the lazy running max of the forward kernels: the softmax
+# exponentials stay below 2**LAZY_SLACK, and a tile's row maximum is computed only when
+# some exponential would exceed it.
+LAZY_SLACK = 16.0
 
 # The query-major dQ kernel steps over 32-row key tiles: its score, dP and dS tiles are then
 # 32 x 32 per wavefront, which leaves D=128 at two waves per SIMD (254 VGPRs, 32 KiB ring) and
@@ -147,7 +158,7 @@ def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_
 
 # Lowering options of variants that differ from the defaults.
 TARGETS: Dict[str, dict] = {
-    "mha_d128_ovl": {"attn_overlap": True},
+    "mha_d128_ovl": {"attn_overlap": True, "lazy_softmax": False},
     "mha_d128_pp_swapped": {"wave_groups": {"k": 1, "v": 0}},
     # (the rotated pipeline's extra fragment registers do not fit two waves per SIMD)
     # A / B load streams split between the wave sets as the warp assigner places them (A with the
@@ -156,7 +167,7 @@ TARGETS: Dict[str, dict] = {
     "gemm_256x128_ws_k32": {"warp_specialize": True, "rotate_mma": False},
     "gemm_256x128_ws_all": {"warp_specialize": True, "rotate_mma": False, "mve": False,
                             "wave_groups": {"a": 1, "b": 1}},
-    "mha_d64_causal_ovl": {"attn_overlap": True},
+    "mha_d64_causal_ovl": {"attn_overlap": True, "lazy_softmax": False},
 }
 
 

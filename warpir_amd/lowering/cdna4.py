@@ -105,6 +105,12 @@ class CDNA4Target:
     # e.g. "k", "v") in the 8-wavefront attention ping-pong.  None: take it
     # from the warp assigner's solution for the kernel (passes.warp_assigner).
     wave_groups: Optional[Dict[str, int]] = None
+    # The online-softmax step with a lazy running maximum (RowMaxOp feeding a
+    # LazyMaxOp, then the exp2 / row-sum / rescale ops of that step) becomes
+    # one speculative wir::lazy_softmax call: the step is computed with the
+    # maximum unchanged and verified from the exponentials' lane sums; only a
+    # tile that rises above the slack (and the first tile) recomputes it.
+    lazy_softmax: bool = True
     # Warp specialisation for ring-pipelined MMA loops: the workgroup gets a
     # second set of wavefronts (waves NW..2NW-1) that only issue the LDS-DMA
     # loads, while waves 0..NW-1 only read LDS and issue MFMAs.  Both sets pass
@@ -163,6 +169,10 @@ class CDNA4Lowerer:
         self._ws_producer_streams = self._ws_streams(kernel) if self._ws else set()
         if self._ws and self._ws_producer_streams is None:
             self._ws = False
+        if self.target.lazy_softmax:
+            for loop in _walk(kernel.body):
+                if isinstance(loop, ForOp):
+                    self._match_lazy_softmax(loop.body)
         body: List[str] = []
         self._emit_ops(kernel.body, body, 1)
         return self._assemble(kernel, body)
@@ -282,6 +292,8 @@ class CDNA4Lowerer:
         self._fused_ids: set = set()
         self._var_override: Dict[str, str] = {}  # resolved value name -> C++ variable
         self._ws = False                          # warp-specialised form (producer / consumer waves)
+        self._softmax_fused: Dict[int, object] = {}  # id(op) -> fused lazy-softmax plan, or "skip"
+        self._no_fusion = False                      # emit the fused groups' ops one by one
 
     def _build_aliases(self, ops) -> None:
         """iter_arg init / loop results / yielded values -> block arg (``lowering.py:87-100``)."""
@@ -573,6 +585,90 @@ class CDNA4Lowerer:
     # ------------------------------------------------------------------
     # op emission
     # ------------------------------------------------------------------
+    def _match_lazy_softmax(self, body) -> None:
+        """Find the online-softmax steps with a lazy maximum in a loop body.
+
+        The step (``tests/attention_baseline.py:42-186`` with the running max
+        replaced by ``LazyMaxOp``), matched by data flow::
+
+            m_prev = copy(m);  cand = row_max(s, m);  m' = lazy_max(m, cand, slack)
+            s_c = s * c;  m'_c = m' * c;  m_c = m_prev * c;  p = exp2(s_c - m'_c)
+            corr = exp2(m_c - m'_c);  l_c = l * corr;  l' = row_sum(p, l_c)
+            o' = o * corr;  pb = bf16(p)
+
+        Every intermediate value must stay inside the group; m', l', o' and pb
+        may be used after it.  The group is emitted as one ``wir::lazy_softmax``
+        at the position of its first op (no op between its members may read a
+        group result)."""
+        ops = list(body)
+        prod = {o.result.name: o for o in ops if isinstance(getattr(o, "result", None), Value)}
+        uses: Dict[str, List[Op]] = {}
+        for o in ops:
+            for v in _op_values(o):
+                if v is not getattr(o, "result", None):
+                    uses.setdefault(v.name, []).append(o)
+
+        def only(name, kind, **attrs):
+            cands = [u for u in uses.get(name, []) if isinstance(u, kind)
+                     and all(getattr(u, k).name == v.name if isinstance(v, Value) else getattr(u, k) == v
+                             for k, v in attrs.items())]
+            return cands[0] if len(cands) == 1 else None
+
+        for lz in (o for o in ops if isinstance(o, LazyMaxOp)):
+            rm = prod.get(lz.cand.name)
+            if not isinstance(rm, RowMaxOp) or rm.prev.name != lz.prev.name:
+                continue
+            s_v, m_v = rm.tile, lz.prev
+            ms_new = next((u for u in uses.get(lz.result.name, []) if isinstance(u, MulScalarOp)), None)
+            if ms_new is None:
+                continue
+            c = ms_new.scalar
+            ms_s = only(s_v.name, MulScalarOp, scalar=c)
+            cp = only(m_v.name, CopyOp)
+            ms_prev = cp and only(cp.result.name, MulScalarOp, scalar=c)
+            sr = ms_s and only(ms_s.result.name, SubRowOp, vec=ms_new.result)
+            e1 = sr and only(sr.result.name, Exp2Op)
+            sb = ms_prev and only(ms_prev.result.name, SubOp, b=ms_new.result)
+            e2 = sb and only(sb.result.name, Exp2Op)
+            mu = e2 and only(e2.result.name, MulOp)
+            rs = e1 and mu and only(e1.result.name, RowSumOp, prev=mu.result)
+            mr = e2 and only(e2.result.name, MulRowOp)
+            cv = e1 and only(e1.result.name, CopyOp)
+            group = [cp, rm, lz, ms_s, ms_new, ms_prev, sr, e1, sb, e2, mu, rs, mr, cv]
+            if any(g is None for g in group) or sb.a.name != ms_prev.result.name:
+                continue
+            norm = mu.a if mu.b.name == e2.result.name else mu.b
+            if not (isinstance(cv.result.type, RegTileType) and cv.result.type.data_type == GPUType.bf16):
+                continue
+            ids = {id(g) for g in group}
+            internal = [cp, rm, ms_s, ms_new, ms_prev, sr, e1, sb, e2, mu]
+            if any(id(u) not in ids for g in internal for u in uses.get(g.result.name, [])):
+                continue
+            outputs = {g.result.name for g in (lz, rs, mr, cv)}
+            inputs = {m_v.name, norm.name, mr.tile.name}
+            if any(id(u) not in ids for n in inputs for u in uses.get(n, [])):
+                continue
+            first = min(ops.index(g) for g in group)
+            last = max(ops.index(g) for g in group)
+            if any(id(o) not in ids and any(v.name in outputs for v in _op_values(o)) for o in ops[first:last + 1]):
+                continue
+            plan = dict(s=s_v, m_in=m_v, m_out=lz.result, l_in=norm, l_out=rs.result, o_in=mr.tile,
+                        o_out=mr.result, p=cv.result, c=c, slack=lz.slack)
+            for g in group:
+                self._softmax_fused[id(g)] = "skip"
+            self._softmax_fused[id(ops[first])] = plan
+
+    def _emit_lazy_softmax(self, plan, out: List[str], depth: int) -> None:
+        """m, l and O are updated in place: the group's results m', l', O' name
+        the C++ variables of m, l, O from here on (the matcher checked that
+        nothing reads m, l, O after the group), so no register tile is copied."""
+        pad = "  " * depth
+        for src, dst in (("m_in", "m_out"), ("l_in", "l_out"), ("o_in", "o_out")):
+            self._var_override[self.resolve(plan[dst].name)] = self._var(plan[src])
+        out.append(f"{pad}wir::lazy_softmax({self._var(plan['s'])}, {self._var(plan['m_in'])}, "
+                   f"{self._var(plan['l_in'])}, {self._var(plan['o_in'])}, {self._var(plan['p'])}, "
+                   f"{_flt(plan['c'])}, {_flt(plan['slack'])});")
+
     def _emit_ops(self, ops, out: List[str], depth: int) -> None:
         for op in ops:
             self._emit_op(op, out, depth)
@@ -581,6 +677,11 @@ class CDNA4Lowerer:
         pad = "  " * depth
         ms = self.geo.ms
         w = out.append
+        fused = None if self._no_fusion else self._softmax_fused.get(id(op))
+        if fused is not None:
+            if fused != "skip":
+                self._emit_lazy_softmax(fused, out, depth)
+            return
         if isinstance(op, (AllocSharedOp, YieldOp)):
             if isinstance(op, YieldOp):
                 self._emit_yield(op, out, depth)
@@ -960,16 +1061,22 @@ class CDNA4Lowerer:
             return None
         return mods.pop()
 
-    def _emit_loop(self, op: ForOp, stop: str, out: List[str], depth: int) -> None:
+    def _emit_loop(self, op: ForOp, stop: str, out: List[str], depth: int, mve: bool = True) -> None:
         """Emit the loop; ring loops are unrolled by their slot count S
         (modulo variable expansion) when the start is a constant and the step
         is 1: copy u of the body sees the constant slot (start + u + offset)
         % S, so LDS addresses fold into instruction offsets.  A remainder loop
-        with run-time slots finishes the last (trips mod S) iterations."""
+        with run-time slots finishes the last (trips mod S) iterations.
+        ``mve=False`` keeps one copy of the body (run-time slots)."""
         pad = "  " * depth
         iv = self._var(op.induction_var)
         ivn = self.resolve(op.induction_var.name)
-        m = self._ring_modulus(op) if self.target.mve else None
+        body = list(op.body)
+        fused_at = next((k for k, o in enumerate(body) if isinstance(self._softmax_fused.get(id(o)), dict)), None)
+        if fused_at is not None and not self._no_fusion:
+            self._emit_loop_lazy(op, stop, out, depth, fused_at)
+            return
+        m = self._ring_modulus(op) if self.target.mve and mve else None
         if m is None or m < 2 or m > 4 or not isinstance(op.start, int) or op.step != 1:
             out.append(f"{pad}for (int {iv} = {self._int(op.start)}; {iv} < {stop}; {iv} += {self._int(op.step)}) {{")
             self._emit_ops(op.body, out, depth + 1)
@@ -988,6 +1095,89 @@ class CDNA4Lowerer:
         out.append(f"{pad}}}")
         out.append(f"{pad}for (int {iv} = {base}; {iv} < {stop}; {iv} += 1) {{")
         self._emit_ops(op.body, out, depth + 1)
+        out.append(f"{pad}}}")
+
+    def _emit_loop_lazy(self, op: ForOp, stop: str, out: List[str], depth: int, fused_at: int) -> None:
+        """A loop whose body holds a lazy softmax step (``_match_lazy_softmax``):
+        the inner loop runs the step's speculative half and leaves for the exact
+        path, which an outer loop runs before re-entering, so inside the inner
+        loop the O accumulator is touched only by its MFMAs and keeps one
+        register assignment.  The first iteration always takes the exact path
+        (the running max starts at -inf), so it is peeled.
+
+        When the ops after the step are the PV MMA (reading this iteration's
+        ring slot) and the yield, they are rotated to the top of the next
+        iteration, ahead of its wait: the exact path is then the softmax step
+        alone, and the prefetch that overwrites that slot still comes after the
+        barrier that follows the PV."""
+        pad = "  " * depth
+        q = pad + "  "
+        iv = self._var(op.induction_var)
+        ivn = self.resolve(op.induction_var.name)
+        body = list(op.body)
+        fz = self._softmax_fused[id(body[fused_at])]
+        pre = body[:fused_at]
+        post = [o for o in body[fused_at + 1:] if self._softmax_fused.get(id(o)) != "skip"]
+        rotate = (isinstance(op.start, int) and op.step == 1 and len(post) == 2 and isinstance(post[0], MMAOp)
+                  and isinstance(post[1], YieldOp) and not post[0].transpose_b
+                  and isinstance(pre[0], (WaitBufOp, WaitOp)))
+
+        def fast_call(d: int) -> None:
+            qq = "  " * d
+            out.append(f"{qq}if (!wir::lazy_softmax_fast({self._var(fz['s'])}, {self._var(fz['m_in'])}, "
+                       f"{self._var(fz['l_in'])}, {self._var(fz['p'])}, {_flt(fz['c'])}, {_flt(fz['slack'])})) {{")
+            out.append(f"{qq}  wir_exact = true;")
+            out.append(f"{qq}  break;")
+            out.append(f"{qq}}}")
+
+        def shifted_post(d: int) -> None:
+            self._slot_shift[ivn] = self._slot_shift.get(ivn, 0) - 1
+            self._emit_ops(post, out, d)
+            self._slot_shift[ivn] += 1
+            if self._slot_shift[ivn] == 0:
+                del self._slot_shift[ivn]
+
+        out.append(f"{pad}{{")
+        if not rotate:
+            out.append(f"{q}int {iv} = {self._int(op.start)};")
+            out.append(f"{q}for (;;) {{")
+            out.append(f"{q}  bool wir_exact = false;")
+            out.append(f"{q}  for (; {iv} < {stop}; {iv} += {self._int(op.step)}) {{")
+            self._emit_ops(pre, out, depth + 3)
+            fast_call(depth + 3)
+            for src, dst in (("m_in", "m_out"), ("l_in", "l_out"), ("o_in", "o_out")):
+                self._var_override[self.resolve(fz[dst].name)] = self._var(fz[src])
+            self._emit_ops(post, out, depth + 3)
+            out.append(f"{q}  }}")
+            out.append(f"{q}  if (!wir_exact) break;")
+            self._emit_op(body[fused_at], out, depth + 2)
+            self._emit_ops(post, out, depth + 2)
+            out.append(f"{q}  {iv} += {self._int(op.step)};")
+            out.append(f"{q}}}")
+            out.append(f"{pad}}}")
+            return
+        start = op.start
+        out.append(f"{q}if (({stop}) > {start}) {{")
+        out.append(f"{q}  const int {iv} = {start};")
+        self._emit_ops(pre, out, depth + 2)
+        self._emit_op(body[fused_at], out, depth + 2)   # exact path: the running max starts at -inf
+        out.append(f"{q}}}")
+        out.append(f"{q}int {iv} = ({start}) + 1;")
+        out.append(f"{q}for (;;) {{")
+        out.append(f"{q}  bool wir_exact = false;")
+        out.append(f"{q}  for (; {iv} < {stop}; ++{iv}) {{")
+        shifted_post(depth + 3)      # PV of the previous iteration
+        self._emit_ops(pre, out, depth + 3)
+        fast_call(depth + 3)
+        out.append(f"{q}  }}")
+        out.append(f"{q}  if (!wir_exact) break;")
+        self._emit_op(body[fused_at], out, depth + 2)
+        out.append(f"{q}  ++{iv};")
+        out.append(f"{q}}}")
+        out.append(f"{q}if (({stop}) > {start}) {{")
+        out.append(f"{q}  const int {iv} = ({stop});")
+        shifted_post(depth + 2)      # PV of the last iteration
+        out.append(f"{q}}}")
         out.append(f"{pad}}}")
 
     def _attention_pingpong_plan(self, loop: ForOp):
@@ -1069,18 +1259,24 @@ class CDNA4Lowerer:
     def _emit_attention_pingpong(self, loop: ForOp, stop: str, out: List[str], depth: int) -> bool:
         """Eight-wavefront attention in ping-pong form.
 
-        Wave groups 0 (waves 0-3) and 1 (waves 4-7) share the SIMDs pairwise
-        and run one phase apart, so one group's MFMA phase overlaps the other
-        group's softmax (VALU) phase.  Iteration i of a group is
+        Wave groups A and B (waves 0-3 and 4-7, in the order the warp
+        assignment gives) share the SIMDs pairwise and run one phase apart, so
+        one group's MFMA phase overlaps the other group's softmax (VALU)
+        phase.  Iteration i of a group is
           M(i): O += P_{i-1} V_{i-1} (the PV MMA of the previous iteration,
-                rotated), the DMAs of tile i + S - 2, then S_i = Q K_i^T;
-          V(i): the online-softmax ops of iteration i (P_i, rescaled O).
-        Every phase starts at a workgroup barrier.  Group 0 loads the K
-        tiles and group 1 the V tiles (4 waves each); a ring of S >= 3
-        slots keeps V_{i-1} resident while tile i + S - 2 is written.
+                rotated), then S_i = Q K_i^T;
+          V(i): the online-softmax ops of iteration i, and this group's share
+                of the ring loads.
+        Group A runs M(i) while group B runs V(i-1).  Every phase starts with
+        ``vmcnt(L)`` and a workgroup barrier, L the loads one wave issues per
+        tile.  With a ring of S >= 4 slots, tile t is loaded S - 2 iterations
+        ahead into slot t % S: A's V(i) loads K tile i + S - 2, B's V(i) loads
+        V tile i + S - 1 (B's V phase of iteration i runs during A's M(i+1)),
+        so the slot written (tile t - S) was last read by the PV MMAs of the
+        iteration before.
         """
         plan = self._attention_pingpong_plan(loop)
-        if plan is None:
+        if plan is None or plan["S"] < 4:
             return False
         swap = self._pingpong_group_swap(plan)
         if swap is None:
@@ -1088,69 +1284,133 @@ class CDNA4Lowerer:
         pad = "  " * depth
         p1 = pad + "  "
         S, qk, pv = plan["S"], plan["qk"], plan["pv"]
+        dist = S - 2
         iv = self._var(loop.induction_var)
         ivn = self.resolve(loop.induction_var.name)
         start = loop.start
+        aff = self._var(plan["affine"].result)
 
-        def dma(ld, grp: int) -> List[str]:
+        def dma(ld, tile: str, d: int) -> Tuple[List[str], int]:
             t = ld.buf.type.tile_type
             per = t.rows * t.cols * 2 // 1024 // 4
-            ptr, key = self._buf_ptr(ld.buf, ld.slot)
+            key = self.resolve(ld.buf.name)
+            stride = _tile_bytes(self.tile_type_of(key))
             src = ld.source
             sub = src.type.sub_tile_type
-            b, d, rt, ct = (self._int(c) for c in ld.coords)
+            b, dd, _rt, ct = (self._int(c) for c in ld.coords)
             self._aligned_checks.add((self.stile(key), _cname(src.name)[2:]))
-            return [f"{p1}  if (wir_grp == {grp}) wir::Loader<{self.stile(key)}, 4>::load<WIR_AL>({ptr}, "
-                    f"globals.{_cname(src.name)[2:]}, {b}, {d}, ({rt}) * {sub.rows}, ({ct}) * {sub.cols}, wir_gw);"], per
+            pd = "  " * d
+            return [f"{pd}{{ const int {aff} = {tile};",
+                    f"{pd}  wir::Loader<{self.stile(key)}, 4>::load<WIR_AL>((smem + {self.lds_off[key]} + "
+                    f"(({aff}) % {S}) * {stride}), globals.{_cname(src.name)[2:]}, {b}, {dd}, ({aff}) * {sub.rows}, "
+                    f"({ct}) * {sub.cols}, wir_gw); }}"], per
+
+        k_ld, v_ld = plan["k_load"], plan["v_load"]
+        per = dma(k_ld, "0", 0)[1]
+        if dma(v_ld, "0", 0)[1] != per:
+            return False
 
         def emit_pv(dst: List[str], d: int) -> None:
             self._slot_shift[ivn] = -1
             self._emit_op(pv, dst, d)
             del self._slot_shift[ivn]
 
-        # Tensors that are not tile-aligned take the plain loop (per-lane
-        # bounds-checked loads need more registers than the ping-pong leaves).
+        # Both groups run the same loop: M(i), then V(i) with the group's ring
+        # load; group B has one extra V phase (its first ring load) in front,
+        # group A one extra barrier at the end, so the phases stay paired.
+        q = pad + "  "
+        # tensors that are not tile-aligned take the plain loop with bounds-checked loads;
+        # one copy of its body keeps its registers within the ping-pong's
         out.append(f"{pad}if constexpr (!WIR_AL) {{")
-        self._emit_loop(loop, stop, out, depth + 1)
+        self._no_fusion = True
+        self._emit_loop(loop, stop, out, depth + 1, mve=False)
+        self._no_fusion = False
         out.append(f"{pad}}} else {{")
-        pad, p1, depth = pad + "  ", p1 + "  ", depth + 1
-        out.append(f"{pad}const int wir_grp = (wir_wave >> 2) ^ {swap}, wir_gw = wir_wave & 3;"
-                   f"  // wave group issuing K: {swap}")
-        out.append(f"{pad}asm volatile(\"s_waitcnt vmcnt(0) lgkmcnt(0)\" ::: \"memory\");")
-        out.append(f"{pad}wir::barrier();")
-        out.append(f"{pad}if (wir_grp == 1) wir::barrier();  // group 1 runs one phase behind")
-        out.append(f"{pad}for (int {iv} = {start}; {iv} < {stop}; ++{iv}) {{")
-        # M phase
-        out.append(f"{p1}if (wir_grp == 0) asm volatile(\"s_waitcnt vmcnt(0)\" ::: \"memory\");")
-        out.append(f"{p1}wir::barrier();")
-        # PV of the previous iteration first: its P and V operands die before
-        # S = Q K^T is allocated, which keeps the phase within 256 VGPRs.
-        out.append(f"{p1}if ({iv} > {start}) {{")
+        out.append(f"{q}const int wir_grp = (wir_wave >> 2) ^ {swap}, wir_gw = wir_wave & 3;"
+                   f"  // group A (K loads) = physical wave group {swap}")
+        out.append(f"{q}for (int wir_t = {start}; wir_t < ({start}) + {dist}; ++wir_t) {{")
+        out.append(f"{q}  if (wir_grp == 0) {{")
+        out.extend(dma(k_ld, "wir_t", depth + 2)[0])
+        out.append(f"{q}  }} else {{")
+        out.extend(dma(v_ld, "wir_t", depth + 2)[0])
+        out.append(f"{q}  }}")
+        out.append(f"{q}}}")
+        out.append(f"{q}wir::wait_vm_barrier<{per}>();")
+        out.append(f"{q}if (wir_grp == 1) {{   // group B's first V phase: its first ring load only")
+        out.extend(dma(v_ld, f"({start}) + {dist}", depth + 2)[0])
+        out.append(f"{q}  wir::wait_vm_barrier<{per}>();")
+        out.append(f"{q}}}")
+        softmax = plan["softmax"]
+        fused_at = next((k for k, o in enumerate(softmax) if isinstance(self._softmax_fused.get(id(o)), dict)), None)
+
+        def v_loads(d: int) -> None:
+            qq = "  " * d
+            out.append(f"{qq}if (wir_grp == 0) {{")
+            out.extend(dma(k_ld, f"({iv}) + {dist}", d + 1)[0])
+            out.append(f"{qq}}} else {{")
+            out.extend(dma(v_ld, f"({iv}) + {dist + 1}", d + 1)[0])
+            out.append(f"{qq}}}")
+
+        def v_tail(ops, d: int) -> None:
+            self._emit_ops(ops, out, d)
+            self._emit_op(plan["yld"], out, d)
+            out.append(f"{'  ' * d}wir::wait_vm_barrier<{per}>();")
+
+        def m_phase(d: int) -> None:
+            emit_pv(out, d)
+            out.append(f"{'  ' * d}__builtin_amdgcn_sched_barrier(0);")
+            self._emit_op(qk, out, d)
+            out.append(f"{'  ' * d}wir::wait_vm_barrier<{per}>();")
+
+        # the first iteration (no PV yet) is peeled so the loop body's PV is
+        # unconditional and O keeps one register assignment around the loop
+        out.append(f"{q}if (({stop}) > {start}) {{")
+        out.append(f"{q}  const int {iv} = {start};")
+        self._emit_op(qk, out, depth + 2)
+        out.append(f"{q}  wir::wait_vm_barrier<{per}>();")
+        v_loads(depth + 2)
+        v_tail(softmax, depth + 2)
+        out.append(f"{q}}}")
+        if fused_at is None:
+            out.append(f"{q}for (int {iv} = ({start}) + 1; {iv} < {stop}; ++{iv}) {{")
+            m_phase(depth + 2)
+            v_loads(depth + 2)
+            v_tail(softmax, depth + 2)
+            out.append(f"{q}}}")
+        else:
+            # A lazy softmax leaves the inner loop for its exact path (the
+            # first tile was peeled above; later ones rarely rise above the
+            # slack), so the inner loop touches O only through its MFMAs.
+            fz = self._softmax_fused[id(softmax[fused_at])]
+            pre, post = softmax[:fused_at], softmax[fused_at + 1:]
+            out.append(f"{q}int {iv} = ({start}) + 1;")
+            out.append(f"{q}for (;;) {{")
+            out.append(f"{q}  bool wir_exact = false;")
+            out.append(f"{q}  for (; {iv} < {stop}; ++{iv}) {{")
+            m_phase(depth + 3)
+            v_loads(depth + 3)
+            self._emit_ops(pre, out, depth + 3)
+            out.append(f"{q}    if (!wir::lazy_softmax_fast({self._var(fz['s'])}, {self._var(fz['m_in'])}, "
+                       f"{self._var(fz['l_in'])}, {self._var(fz['p'])}, {_flt(fz['c'])}, {_flt(fz['slack'])})) {{")
+            out.append(f"{q}      wir_exact = true;")
+            out.append(f"{q}      break;")
+            out.append(f"{q}    }}")
+            for src, dst in (("m_in", "m_out"), ("l_in", "l_out"), ("o_in", "o_out")):
+                self._var_override[self.resolve(fz[dst].name)] = self._var(fz[src])
+            v_tail(post, depth + 3)
+            out.append(f"{q}  }}")
+            out.append(f"{q}  if (!wir_exact) break;")
+            self._emit_op(softmax[fused_at], out, depth + 2)   # the whole step, exact path included
+            v_tail(post, depth + 2)
+            out.append(f"{q}  ++{iv};")
+            out.append(f"{q}}}")
+        # the last M phase: PV of the last iteration
+        out.append(f"{q}if (({stop}) > {start}) {{")
+        out.append(f"{q}  const int {iv} = ({stop});")
         emit_pv(out, depth + 2)
-        aff = plan["affine"]
-        out.append(f"{p1}  const int {self._var(aff.result)} = ({iv}) + {S - 2};")
-        self._slot_shift[ivn] = -1
-        k_lines, k_per = dma(plan["k_load"], 0)
-        v_lines, v_per = dma(plan["v_load"], 1)
-        del self._slot_shift[ivn]
-        out.extend(k_lines + v_lines)
-        out.append(f"{p1}}}")
-        out.append(f"{p1}__builtin_amdgcn_sched_barrier(0);")
-        self._emit_op(qk, out, depth + 1)
-        # V phase
-        out.append(f"{p1}if (wir_grp == 1) asm volatile(\"s_waitcnt vmcnt({v_per})\" ::: \"memory\");")
-        out.append(f"{p1}wir::barrier();")
-        self._emit_ops(plan["softmax"], out, depth + 1)
-        self._emit_op(plan["yld"], out, depth + 1)
+        out.append(f"{q}}}")
+        out.append(f"{q}if (wir_grp == 0) wir::wait_vm_barrier<0>();   // pairs with group B's extra V phase")
         out.append(f"{pad}}}")
-        # final M phase: the last PV, then group 0 matches group 1's extra barrier
-        out.append(f"{pad}wir::barrier();")
-        out.append(f"{pad}if (({stop}) > {start}) {{")
-        out.append(f"{p1}const int {iv} = ({stop});")
-        emit_pv(out, depth + 1)
-        out.append(f"{pad}}}")
-        out.append(f"{pad}if (wir_grp == 0) wir::barrier();")
-        out.append(f"{pad[:-2]}}}")
         return True
 
     def _attention_overlap_plan(self, loop: ForOp):
@@ -1883,6 +2143,15 @@ def _walk(ops):
         yield op
         if isinstance(op, ForOp):
             yield from _walk(op.body)
+
+
+def _op_values(op):
+    """The Values an op names in its fields (not the bodies of nested loops)."""
+    import dataclasses
+    for f in dataclasses.fields(op):
+        if f.name in ("body", "iter_args", "results"):
+            continue
+        yield from _values_in(getattr(op, f.name))
 
 
 def _values_in(x):
