@@ -134,3 +134,14 @@ def test_split_k_repeated_launches_bitwise_stable(gpu):
         c.fill_(float("nan"))
         api.gemm_split_k(a, b, out=c, splits=splits, workspace=ws)
         assert torch.equal(c, first), it
+
+
+def test_skinny_benchmark_kernel_at_its_exact_shape(gpu):
+    """The kernel bench.py times for config 3' (gemm_128x32_k64) at exactly
+    M=128, N=K=8192; the oracle runs on 512 sampled output columns."""
+    a, b, c = _run("gemm_128x32_k64", 128, 8192, 8192, seed=11)
+    cols = torch.randperm(8192, generator=torch.Generator().manual_seed(5))[:512]
+    ref = gemm_ref(a, b[:, cols])
+    err = rel_err(c[:, cols], ref)
+    assert err <= TOL, err
+    assert not torch.isnan(c.float()).any()

@@ -1,0 +1,51 @@
+"""Host-side runtime behaviour that needs no GPU: the variant-handle cache is
+safe under threads, packed kernel arguments are reused per argument
+signature, and the split-K entry point rejects an ``out`` it would scramble."""
+import threading
+
+import pytest
+import torch
+
+from warpir_amd import api, kernels
+
+
+def test_handle_cache_builds_each_variant_once_across_threads():
+    name = "gemm_ref_ssa"
+    kernels._handles.pop(name, None)
+    got, barrier = [], threading.Barrier(4)
+
+    def worker():
+        barrier.wait()
+        got.append(kernels.handle(name))
+
+    threads = [threading.Thread(target=worker) for _ in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert len(got) == 4 and all(h is got[0] for h in got)
+
+
+def test_kernarg_signature_distinguishes_buffers_and_ints():
+    h = kernels.handle("gemm_ref_ssa")
+    a = torch.zeros(64, 64, dtype=torch.bfloat16)
+    b = torch.zeros(64, 64, dtype=torch.bfloat16)
+    c = torch.zeros(64, 64, dtype=torch.bfloat16)
+    s1 = h._signature(dict(A=a, B=b, N=64, C_global=c))
+    s2 = h._signature(dict(A=a, B=b, N=64, C_global=c))
+    s3 = h._signature(dict(A=a, B=c, N=64, C_global=b))
+    s4 = h._signature(dict(A=a, B=b, N=32, C_global=c))
+    assert s1 == s2 and s1 != s3 and s1 != s4
+    assert h._signature(dict(A=a, B=b, N=64)) is None           # a missing argument is not cached
+    assert h._signature(dict(A=a, B=b, N=64.0, C_global=c)) is None
+
+
+@pytest.mark.parametrize("bad", ["shape", "dtype", "strided"])
+def test_split_k_rejects_an_out_it_would_scramble(bad):
+    a = torch.zeros(64, 1024, dtype=torch.bfloat16)
+    b = torch.zeros(1024, 256, dtype=torch.bfloat16)
+    out = {"shape": torch.zeros(64, 128, dtype=torch.bfloat16),
+           "dtype": torch.zeros(64, 256, dtype=torch.float32),
+           "strided": torch.zeros(256, 64, dtype=torch.bfloat16).t()}[bad]
+    with pytest.raises(ValueError, match="out must be a contiguous bf16"):
+        api.gemm_split_k(a, b, out=out, splits=4)

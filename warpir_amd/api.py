@@ -67,7 +67,7 @@ def _splitk_reduce(partials, out, splits: int) -> None:
         _fields_ = [("partials", ctypes.c_void_p), ("out", ctypes.c_void_p), ("n", ctypes.c_longlong),
                     ("split_stride", ctypes.c_longlong), ("splits", ctypes.c_int)]
 
-    n = out.numel()
+    n = partials.shape[2] * partials.shape[3]   # M * N, the elements of one split
     args = Args(partials.data_ptr(), out.data_ptr(), n, partials.stride(1), splits)
     _reduce_kernel.launch(((n // 8 + 255) // 256, 1, 1), (256, 1, 1), args)
 
@@ -91,6 +91,12 @@ def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None):
     kc = k // splits
     if out is None:
         out = torch.empty(m, n, dtype=torch.bfloat16, device=a.device)
+    # the reduction writes M * N bf16 values flat from out's first element
+    if tuple(out.shape) != (m, n) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError(f"gemm_split_k: out must be a contiguous bf16 [{m}, {n}] tensor, got "
+                         f"{out.dtype} {tuple(out.shape)} with strides {tuple(out.stride())}")
+    if out.device != a.device:
+        raise ValueError("gemm_split_k: out must be on the operands' device")
     if workspace is None:
         workspace = torch.empty(splits * m * n, dtype=torch.float32, device=a.device)
     if workspace.numel() < splits * m * n or workspace.dtype != torch.float32:

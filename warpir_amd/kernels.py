@@ -7,6 +7,7 @@ every entry into the code-object cache, so GPU runs load prebuilt
 """
 from __future__ import annotations
 
+import threading
 from typing import Callable, Dict, Optional
 
 from warpir_amd.ir import Kernel
@@ -179,6 +180,7 @@ def lowerer(name: str):
 
 
 _handles: Dict[str, object] = {}
+_handles_lock = threading.Lock()
 
 
 def kernel(name: str) -> Kernel:
@@ -186,12 +188,17 @@ def kernel(name: str) -> Kernel:
 
 
 def handle(name: str):
-    """A compiled, launchable ``KernelHandle`` for variant *name* (memoised)."""
+    """A compiled, launchable ``KernelHandle`` for variant *name* (memoised;
+    safe to call from several threads: each variant is built once)."""
     from warpir_amd.runtime import compile_kernel
 
-    if name not in _handles:
-        _handles[name] = compile_kernel(VARIANTS[name](), lowerer(name))
-    return _handles[name]
+    h = _handles.get(name)
+    if h is not None:
+        return h
+    with _handles_lock:
+        if name not in _handles:
+            _handles[name] = compile_kernel(VARIANTS[name](), lowerer(name))
+        return _handles[name]
 
 
 def build_all(verbose: bool = False, prune: bool = True) -> Dict[str, str]:

@@ -230,6 +230,11 @@ class KernelHandle:
         self.args_type = kernarg_struct(kernel)
         self._module = None
         self._function = None
+        self._load_lock = threading.Lock()
+        # packed kernel arguments and launch configuration per argument signature
+        # (tensor pointers, shapes, strides, dtypes and int values), so repeated
+        # launches with the same buffers skip validation and packing
+        self._pack_cache: Dict[tuple, tuple] = {}
         self._loaded_stores = [v.name for v in kernel.outputs]
         self._loaded_globals = self._loaded_sources()
 
@@ -244,16 +249,19 @@ class KernelHandle:
     def load(self) -> None:
         if self._function is not None:
             return
-        lib = library()
-        with open(self.path, "rb") as f:
-            image = f.read()
-        self._image = ctypes.create_string_buffer(image, len(image))
-        mod = ctypes.c_void_p()
-        check(lib.wir_module_load(self._image, len(image), ctypes.byref(mod)), "wir_module_load")
-        fn = ctypes.c_void_p()
-        check(lib.wir_module_get_function(mod, self.kernel.name.encode(), ctypes.byref(fn)),
-              f"wir_module_get_function({self.kernel.name})")
-        self._module, self._function = mod, fn
+        with self._load_lock:   # one module per handle, also when threads race here
+            if self._function is not None:
+                return
+            lib = library()
+            with open(self.path, "rb") as f:
+                image = f.read()
+            self._image = ctypes.create_string_buffer(image, len(image))
+            mod = ctypes.c_void_p()
+            check(lib.wir_module_load(self._image, len(image), ctypes.byref(mod)), "wir_module_load")
+            fn = ctypes.c_void_p()
+            check(lib.wir_module_get_function(mod, self.kernel.name.encode(), ctypes.byref(fn)),
+                  f"wir_module_get_function({self.kernel.name})")
+            self._module, self._function = mod, fn
 
     def pack(self, args: Dict[str, object]):
         """Validate tensors / ints and build the kernel-argument struct and grid."""
@@ -302,10 +310,33 @@ class KernelHandle:
         cfg = self.lowerer.launch_config(self.kernel, {k: s for k, s in shapes.items()})
         return packed, cfg, device
 
+    def _signature(self, args: Dict[str, object]):
+        """Hashable summary of the arguments that fixes the packed struct, or None."""
+        import torch
+
+        sig = []
+        for v in list(self.kernel.inputs) + list(self.kernel.outputs):
+            x = args.get(v.name)
+            if isinstance(x, torch.Tensor):
+                sig.append((x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.dtype, x.device))
+            elif isinstance(x, int):
+                sig.append(x)
+            else:
+                return None
+        return tuple(sig) if len(args) == len(sig) else None
+
     def __call__(self, stream=None, **args) -> None:
         import torch
 
-        packed, cfg, device = self.pack(args)
+        key = self._signature(args)
+        hit = self._pack_cache.get(key) if key is not None else None
+        if hit is None:
+            hit = self.pack(args)
+            if key is not None:
+                if len(self._pack_cache) >= 64:
+                    self._pack_cache.clear()
+                self._pack_cache[key] = hit
+        packed, cfg, device = hit
         self.load()
         if stream is None:
             stream = torch.cuda.current_stream(device).cuda_stream
@@ -330,6 +361,9 @@ def compile_kernel(kernel: Kernel, lowerer=None) -> KernelHandle:
     return KernelHandle(kernel, lowerer)
 
 
+_raw_lock = threading.Lock()
+
+
 class RawKernel:
     """A hand-written kernel from a prebuilt code object in the package
     (``__graft_entry__.build()`` compiles them), launched through the C ABI
@@ -344,6 +378,11 @@ class RawKernel:
     def _load(self) -> None:
         if self._function is not None:
             return
+        with _raw_lock:
+            if self._function is None:
+                self._load_locked()
+
+    def _load_locked(self) -> None:
         if not os.path.exists(self.path):
             raise CompileError(f"{self.path} is not built (run __graft_entry__.build())")
         lib = library()
