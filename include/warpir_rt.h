@@ -35,7 +35,7 @@ typedef void* wir_function_t; /* a kernel inside a module (hipFunction_t) */
 typedef void* wir_event_t;    /* a timing event (hipEvent_t)              */
 
 /* ABI version of this header; bumped on any signature change. */
-#define WIR_RT_ABI_VERSION 1
+#define WIR_RT_ABI_VERSION 2
 int wir_abi_version(void);
 
 /* Make `device` current for the calling thread. */
@@ -80,8 +80,34 @@ int wir_event_destroy(wir_event_t event);
 int wir_event_record(wir_event_t event, void* stream);
 int wir_event_elapsed_ms(wir_event_t start, wir_event_t end, float* ms);
 
-/* Human-readable message for a code returned by any function above. */
+/* Human-readable message for a code returned by any function in this header
+ * (hipError_t codes and the WIR_ERROR_* codes below). */
 const char* wir_error_string(int code);
+
+/* Returned when an input needs more device scratch than the library holds. */
+#define WIR_ERROR_SCRATCH_LIMIT 20001
+
+/* Floats of device scratch held by wir_gemm_splitk_noalloc: 8 Mi fp32 values
+ * (32 MiB) on every device the library runs on, until the process ends. */
+#define WIR_NOALLOC_SCRATCH_FLOATS (8 * 1024 * 1024)
+
+/* out[M][N] (bf16) = a[M][K] @ b[K][N] (bf16, row-major, contiguous) as
+ * `splits` K slices plus an fp32 reduction, with no device allocation: the
+ * fp32 partials live in the library's own device scratch instead of a
+ * workspace.  No counterpart in the reference; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).
+ *   gemm   -- gemm_128_splitk, loaded from its code object;
+ *   reduce -- wir_splitk_reduce, loaded from splitk_reduce.hsaco.
+ * Requires 1 <= splits <= 16, K % (64 * splits) == 0, N % 8 == 0 and 16-byte
+ * aligned a, b, out; returns WIR_ERROR_SCRATCH_LIMIT when
+ * splits * M * N > WIR_NOALLOC_SCRATCH_FLOATS.  Runs on the current device,
+ * which must own `stream`.  Every call on one device shares that device's
+ * scratch: calls that overlap on one device race, so order them on one
+ * stream. */
+int wir_gemm_splitk_noalloc(wir_function_t gemm, wir_function_t reduce, const void* a,
+                            const void* b, void* out, int m, int n, int k, int splits,
+                            void* stream);
 
 #ifdef __cplusplus
 }

@@ -49,3 +49,27 @@ def test_split_k_rejects_an_out_it_would_scramble(bad):
            "strided": torch.zeros(256, 64, dtype=torch.bfloat16).t()}[bad]
     with pytest.raises(ValueError, match="out must be a contiguous bf16"):
         api.gemm_split_k(a, b, out=out, splits=4)
+
+
+def test_noalloc_entry_point_rejects_oversize_inputs_before_touching_a_device():
+    import ctypes
+
+    from warpir_amd.runtime import LIB_PATH, library
+    import os
+    if not os.path.exists(LIB_PATH):
+        pytest.skip("libwarpir_rt.so not built")
+    lib = library()
+    fake = ctypes.c_void_p(256)   # never dereferenced: validation fails first
+    code = lib.wir_gemm_splitk_noalloc(fake, fake, fake, fake, fake, 1024, 8192, 8192, 4, None)
+    assert code == 20001
+    assert b"device scratch" in lib.wir_error_string(code)
+    assert lib.wir_gemm_splitk_noalloc(fake, fake, fake, fake, fake, 64, 8192, 8000, 4, None) != 0  # K % 256
+
+
+def test_noalloc_split_k_validates_operands_on_the_host():
+    a = torch.zeros(64, 1024, dtype=torch.bfloat16)
+    b = torch.zeros(1024, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="gemm_split_k_noalloc: out"):
+        api.gemm_split_k_noalloc(a, b, torch.zeros(64, 128, dtype=torch.bfloat16), splits=4)
+    with pytest.raises(ValueError, match="must be on one GPU"):
+        api.gemm_split_k_noalloc(a, b, torch.zeros(64, 256, dtype=torch.bfloat16), splits=4)

@@ -109,6 +109,51 @@ def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None):
     return out
 
 
+NOALLOC_SCRATCH_FLOATS = 8 * 1024 * 1024   # WIR_NOALLOC_SCRATCH_FLOATS of include/warpir_rt.h
+
+
+def gemm_split_k_noalloc(a, b, out, splits: Optional[int] = None, stream=None):
+    """``out = a @ b`` by the same two kernels as ``gemm_split_k``, with the
+    fp32 partials in the native library's own device scratch: no device
+    memory is allocated (``wir_gemm_splitk_noalloc``).  ``out`` is required.
+    Raises ``HipError`` when ``splits * M * N`` exceeds the scratch
+    (``NOALLOC_SCRATCH_FLOATS``).  Calls that overlap on one device share the
+    scratch and race; order them on one stream."""
+    import ctypes
+
+    import torch
+
+    from warpir_amd.runtime import RawKernel, check, library
+
+    global _reduce_kernel
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
+        raise ValueError(f"gemm: shapes {tuple(a.shape)} @ {tuple(b.shape)} do not chain")
+    m, k = a.shape
+    n = b.shape[1]
+    splits = splits or splitk_count(m, n, k)
+    for name, t, shape in (("a", a, (m, k)), ("b", b, (k, n)), ("out", out, (m, n))):
+        if (not isinstance(t, torch.Tensor) or tuple(t.shape) != shape or t.dtype != torch.bfloat16
+                or not t.is_contiguous()):
+            raise ValueError(f"gemm_split_k_noalloc: {name} must be a contiguous bf16 {list(shape)} tensor")
+    if not a.is_cuda or b.device != a.device or out.device != a.device:
+        raise ValueError("gemm_split_k_noalloc: a, b and out must be on one GPU")
+    gemm_h = kernels.handle(SPLITK_GEMM_VARIANT)
+    gemm_h.load()
+    if _reduce_kernel is None:
+        _reduce_kernel = RawKernel("splitk_reduce.hsaco", "wir_splitk_reduce")
+    _reduce_kernel._load()
+    if stream is None:
+        stream = torch.cuda.current_stream(a.device).cuda_stream
+    elif hasattr(stream, "cuda_stream"):
+        stream = stream.cuda_stream
+    with torch.cuda.device(a.device):
+        check(library().wir_gemm_splitk_noalloc(gemm_h._function, _reduce_kernel._function, a.data_ptr(),
+                                                b.data_ptr(), out.data_ptr(), m, n, k, splits,
+                                                ctypes.c_void_p(stream)),
+              "wir_gemm_splitk_noalloc")
+    return out
+
+
 def gemm(a, b, out=None, variant: Optional[str] = None):
     """``out[M, N] = a[M, K] @ b[K, N]`` in bf16 with fp32 accumulation.
 

@@ -111,6 +111,10 @@ int wir_event_elapsed_ms(wir_event_t start, wir_event_t end, float* ms) {
   return (int)hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end);
 }
 
-const char* wir_error_string(int code) { return hipGetErrorString((hipError_t)code); }
+const char* wir_error_string(int code) {
+  if (code == WIR_ERROR_SCRATCH_LIMIT)
+    return "input exceeds the library's device scratch (splits * M * N > WIR_NOALLOC_SCRATCH_FLOATS)";
+  return hipGetErrorString((hipError_t)code);
+}
 
 }  // extern "C"

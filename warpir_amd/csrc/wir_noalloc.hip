@@ -1,0 +1,132 @@
+// wir_noalloc.hip -- split-K GEMM through the C ABI with no device allocation.
+//
+// The allocating split-K path (warpir_amd.api.gemm_split_k) takes an fp32
+// workspace of splits * M * N partial sums from the caller or allocates one.
+// wir_gemm_splitk_noalloc runs the same two kernels -- the generated
+// gemm_128_splitk GEMM and wir_splitk_reduce -- with that workspace in
+// `scratch`, a file-scope device array of WIR_NOALLOC_SCRATCH_FLOATS floats
+// that every device holds from the library's first use until the process
+// ends.  Host code never passes `scratch` itself to a kernel: the name is a
+// host-side stand-in.  The device address comes from hipGetSymbolAddress,
+// looked up once per device with that device current and kept in
+// g_scratch[device].
+//
+// Every call on one device shares that device's array.  The GEMM writes every
+// partial element [split][row < M][col < N] before the reduction reads it, so
+// nothing needs clearing between calls; two calls that overlap on one device
+// (different streams or threads without ordering between them) race on it.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+
+#include "warpir_rt.h"
+
+static __device__ __align__(256) float scratch[WIR_NOALLOC_SCRATCH_FLOATS];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device).
+int scratch_on_current_device(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+  float* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (!addr) return (int)hipErrorInvalidSymbol;
+      p = (float*)addr;
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return 0;
+}
+
+// Host mirror of the generated kernel's wir::gl<T>: data pointer, four dims
+// (b, d, r, c) and three element strides (sb, sd, sr).
+struct GlobalView {
+  const void* data;
+  int b, d, r, c;
+  long long sb, sd, sr;
+};
+
+// Kernel arguments of gemm_128_splitk, laid out as its emitted globals
+// struct (inputs then outputs in IR order: A, B, N, C_global).
+struct SplitKGemmArgs {
+  GlobalView A;   // [1][splits][M][K/splits], K-slice s starts at column s*K/splits
+  GlobalView B;   // [1][splits][K/splits][N]
+  int N;          // K/splits: the loop bound of one slice
+  GlobalView C;   // fp32 partials [1][splits][M][N]
+};
+static_assert(sizeof(GlobalView) == 48, "wir::gl layout");
+static_assert(offsetof(SplitKGemmArgs, B) == 48 && offsetof(SplitKGemmArgs, N) == 96 &&
+                  offsetof(SplitKGemmArgs, C) == 104 && sizeof(SplitKGemmArgs) == 152,
+              "gemm_128_splitk globals layout");
+
+// Kernel arguments of wir_splitk_reduce (splitk_reduce.hip).
+struct SplitKReduceArgs {
+  const float* partials;
+  void* out;
+  long long n;
+  long long split_stride;
+  int splits;
+};
+
+constexpr int kTile = 128;       // gemm_128_splitk output tile (rows and columns)
+constexpr int kThreads = 256;    // gemm_128_splitk workgroup size
+constexpr int kKStep = 64;       // K per pipeline step
+constexpr int kMaxSplits = 16;
+
+int launch(hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned bx, void* stream,
+           void* args, size_t size) {
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
+                    HIP_LAUNCH_PARAM_END};
+  return (int)hipModuleLaunchKernel(f, gx, gy, gz, bx, 1, 1, 0, (hipStream_t)stream, nullptr, config);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" int wir_gemm_splitk_noalloc(wir_function_t gemm, wir_function_t reduce, const void* a,
+                                       const void* b, void* out, int m, int n, int k, int splits,
+                                       void* stream) {
+  if (!gemm || !reduce || !a || !b || !out) return (int)hipErrorInvalidValue;
+  if (m <= 0 || n <= 0 || k <= 0 || splits <= 0 || splits > kMaxSplits) return (int)hipErrorInvalidValue;
+  if (k % (kKStep * splits) || n % 8 || !aligned16(a) || !aligned16(b) || !aligned16(out))
+    return (int)hipErrorInvalidValue;
+  const long long split_elems = (long long)m * n;
+  if ((long long)splits * split_elems > (long long)WIR_NOALLOC_SCRATCH_FLOATS) return WIR_ERROR_SCRATCH_LIMIT;
+
+  float* ws = nullptr;
+  int e = scratch_on_current_device(&ws);
+  if (e) return e;
+
+  const int kc = k / splits;
+  SplitKGemmArgs g;
+  g.A = {a, 1, splits, m, kc, 0, kc, k};
+  g.B = {b, 1, splits, kc, n, (long long)k * n, (long long)kc * n, n};
+  g.N = kc;
+  g.C = {ws, 1, splits, m, n, (long long)splits * split_elems, split_elems, n};
+  e = launch((hipFunction_t)gemm, (unsigned)((n + kTile - 1) / kTile), (unsigned)((m + kTile - 1) / kTile),
+             (unsigned)splits, kThreads, stream, &g, sizeof(g));
+  if (e) return e;
+
+  SplitKReduceArgs r = {ws, out, split_elems, split_elems, splits};
+  return launch((hipFunction_t)reduce, (unsigned)((split_elems / 8 + 255) / 256), 1, 1, 256, stream, &r,
+                sizeof(r));
+}
