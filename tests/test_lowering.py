@@ -140,6 +140,26 @@ def test_attention_pingpong_groups_follow_the_warp_assignment():
     assert group_line(CDNA4Target(wave_groups={"k": 0, "v": 0})) == []
 
 
+def test_attention_pingpong_one_barrier_per_iteration():
+    """Group A passes its barrier after each V phase, group B after each M
+    phase: one barrier per iteration per wave (the peeled first iteration,
+    the inner loop and the lazy softmax's exact path included), and the same
+    count in front of the loop, so the groups' barrier sequences pair up."""
+    from warpir_amd.lowering.cdna4 import CDNA4Target
+    k = kernels.kernel("mha_d128")
+    src = CDNA4Lowerer(CDNA4Target()).lower(k)
+    pp = src[src.index("const int wir_grp ="):src.index("ring buffers dead")]
+    lines = [l.strip() for l in pp.split("\n")]
+    assert lines.count("wir::wait_vm_barrier<4>();") == 1                      # after the prologue loads
+    assert lines.count("if (wir_grp == 1) wir::wait_vm_barrier<4>();") == 2    # after M: peeled, loop
+    assert lines.count("if (wir_grp == 0) wir::wait_vm_barrier<4>();") == 3    # after V: peeled, loop, exact
+    assert "pairs with group B" not in pp
+    two = CDNA4Lowerer(CDNA4Target(pingpong_one_barrier=False)).lower(k)
+    pp2 = two[two.index("const int wir_grp ="):two.index("ring buffers dead")]
+    assert "if (wir_grp == 0) wir::wait_vm_barrier<0>();   // pairs with group B's extra V phase" in pp2
+    assert "if (wir_grp == 1) wir::wait_vm_barrier" not in pp2
+
+
 def test_warp_specialized_gemm_form():
     k = kernels.kernel("gemm_256x128_ws")
     low = kernels.lowerer("gemm_256x128_ws")

@@ -1190,13 +1190,13 @@ __device__ __forceinline__ bool lazy_softmax_fast(const RTile<MS, R, C>& s, cons
 // m + slack: lazy_max keeps m on every row, corr is exactly 1 and o, l are
 // not rescaled, and the speculation is the IR's result.  Otherwise (the
 // first tile, where m = -inf, or a tile whose scores rise above m + slack)
-// the step is recomputed row by row with the exact lazy maximum.  The fast
-// path is one fma, one exp2, one add and half a bf16 pack per score: no row
-// maximum, no rescale.
+// the step is recomputed row by row with the exact lazy maximum
+// (lazy_softmax_exact, which a loop that already ran lazy_softmax_fast on
+// the tile calls directly).  The fast path is one fma, one exp2, one add and
+// half a bf16 pack per score: no row maximum, no rescale.
 template <int MS, int R, int C, int DO>
-__device__ __forceinline__ void lazy_softmax(const RTile<MS, R, C>& s, RVec<MS, R>& m, RVec<MS, R>& l,
-                                             RTile<MS, R, DO>& o, BTile<MS, R, C>& pb, float c, float slack) {
-  if (lazy_softmax_fast(s, m, l, pb, c, slack)) return;
+__device__ __forceinline__ void lazy_softmax_exact(const RTile<MS, R, C>& s, RVec<MS, R>& m, RVec<MS, R>& l,
+                                                   RTile<MS, R, DO>& o, BTile<MS, R, C>& pb, float c, float slack) {
   constexpr int RB = R / MS, CB = C / MS, G = BTile<MS, R, C>::G;
   float corr[RB], sum[RB], part[RB][4];
 #pragma unroll
@@ -1239,6 +1239,13 @@ __device__ __forceinline__ void lazy_softmax(const RTile<MS, R, C>& s, RVec<MS, 
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int i = 0; i < MF<MS>::CREGS; ++i) o.f[cb][rb][i] *= corr[rb];
+}
+
+template <int MS, int R, int C, int DO>
+__device__ __forceinline__ void lazy_softmax(const RTile<MS, R, C>& s, RVec<MS, R>& m, RVec<MS, R>& l,
+                                             RTile<MS, R, DO>& o, BTile<MS, R, C>& pb, float c, float slack) {
+  if (lazy_softmax_fast(s, m, l, pb, c, slack)) return;
+  lazy_softmax_exact(s, m, l, o, pb, c, slack);
 }
 
 // Lower-triangular mask: keep (row, col) when col_g <= row_g with

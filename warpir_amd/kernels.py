@@ -60,11 +60,17 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # waited every KV step) and the pipelined prefetch form of kernel_pass.
     "mha_d128_ssa": lambda: build_mha_forward_kernel(d=128, block_q=128, block_kv=64, wave_rows=32),
     # The config-4 kernel: 256 query rows (8 wavefronts of 32) in the ping-pong form (one wave
-    # group's MFMAs beside the other's softmax), a 4-slot K/V ring loaded two tiles ahead, and
-    # the online softmax with a lazy running max (lowered speculatively: no row max, no rescale
-    # unless a tile rises above the slack).
+    # group's MFMAs beside the other's softmax, one barrier per iteration), a 4-slot K/V ring
+    # loaded two tiles ahead, and the online softmax with a lazy running max (lowered
+    # speculatively: no row max, no rescale unless a tile rises above the slack).
     "mha_d128": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
                              rescale_slack=LAZY_SLACK),
+    # the same with a barrier at the end of every phase (the groups in lock-step)
+    "mha_d128_pp2b": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
+                                  rescale_slack=LAZY_SLACK),
+    # the same with a 5-slot ring (the whole 160 KB of LDS), loaded three tiles ahead
+    "mha_d128_s5": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=160 * 1024, min_stages=5,
+                                rescale_slack=LAZY_SLACK),
     # the same with the K and V load streams on the opposite wave groups from the warp assigner's answer
     "mha_d128_pp_swapped": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
                                         rescale_slack=LAZY_SLACK),
@@ -76,10 +82,15 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_d128_q256": lambda: _mha(128, 256, 64, 32, causal=False),
     "mha_d64_causal_ssa": lambda: build_mha_forward_kernel(d=64, block_q=128, block_kv=64, wave_rows=32,
                                                            causal=True, name="mha_fwd_causal"),
-    "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True),
+    # The config-5 kernel: 128 query rows (4 wavefronts of 32, three workgroups per CU), a 3-slot
+    # ring, the lazy-max softmax; and the same with the reference IR's exact online softmax.
+    "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=LAZY_SLACK),
+    "mha_d64_causal_online": lambda: _mha(64, 128, 64, 32, causal=True),
     "mha_d128_causal": lambda: _mha(128, 128, 64, 32, causal=True),
     "mha_d64": lambda: _mha(64, 128, 64, 32, causal=False),
-    "mha_d64_causal_lazy": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=LAZY_SLACK),
+    # Eight wavefronts in ping-pong (256 query rows, 4-slot K/V rings) with the lazy-max softmax.
+    "mha_d64_causal_pp": lambda: _mha(64, 256, 64, 32, causal=True, lds_budget=128 * 1024, min_stages=4,
+                                      rescale_slack=LAZY_SLACK),
     # software-pipelined attention loop (QK of tile i+1 and PV of tile i carry tile i's softmax)
     "mha_d128_ovl": lambda: _mha(128, 128, 64, 32, causal=False, rescale_slack=8.0),
     "mha_d64_causal_ovl": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=8.0, lds_budget=32 * 1024),
@@ -161,6 +172,7 @@ def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_
 TARGETS: Dict[str, dict] = {
     "mha_d128_ovl": {"attn_overlap": True, "lazy_softmax": False},
     "mha_d128_pp_swapped": {"wave_groups": {"k": 1, "v": 0}},
+    "mha_d128_pp2b": {"pingpong_one_barrier": False},
     # (the rotated pipeline's extra fragment registers do not fit two waves per SIMD)
     # A / B load streams split between the wave sets as the warp assigner places them (A with the
     # MFMA waves, B on the DMA waves); _all puts both on the DMA waves

@@ -111,6 +111,10 @@ class CDNA4Target:
     # maximum unchanged and verified from the exponentials' lane sums; only a
     # tile that rises above the slack (and the first tile) recomputes it.
     lazy_softmax: bool = True
+    # Attention ping-pong with one workgroup barrier per iteration instead of
+    # one per phase: group A passes it after its V phase, group B after its
+    # M phase, so the two groups' phases interleave without lock-step.
+    pingpong_one_barrier: bool = True
     # Warp specialisation for ring-pipelined MMA loops: the workgroup gets a
     # second set of wavefronts (waves NW..2NW-1) that only issue the LDS-DMA
     # loads, while waves 0..NW-1 only read LDS and issue MFMAs.  Both sets pass
@@ -294,6 +298,7 @@ class CDNA4Lowerer:
         self._ws = False                          # warp-specialised form (producer / consumer waves)
         self._softmax_fused: Dict[int, object] = {}  # id(op) -> fused lazy-softmax plan, or "skip"
         self._no_fusion = False                      # emit the fused groups' ops one by one
+        self._lazy_exact_only = False                # fused groups emit only the exact half
 
     def _build_aliases(self, ops) -> None:
         """iter_arg init / loop results / yielded values -> block arg (``lowering.py:87-100``)."""
@@ -665,9 +670,18 @@ class CDNA4Lowerer:
         pad = "  " * depth
         for src, dst in (("m_in", "m_out"), ("l_in", "l_out"), ("o_in", "o_out")):
             self._var_override[self.resolve(plan[dst].name)] = self._var(plan[src])
-        out.append(f"{pad}wir::lazy_softmax({self._var(plan['s'])}, {self._var(plan['m_in'])}, "
+        # where the speculative half is known to fail (the first tile, whose running max is
+        # -inf) or has just failed (a loop's exit to its exact path), only the exact half runs
+        fn = "lazy_softmax_exact" if self._lazy_exact_only else "lazy_softmax"
+        out.append(f"{pad}wir::{fn}({self._var(plan['s'])}, {self._var(plan['m_in'])}, "
                    f"{self._var(plan['l_in'])}, {self._var(plan['o_in'])}, {self._var(plan['p'])}, "
                    f"{_flt(plan['c'])}, {_flt(plan['slack'])});")
+
+    def _emit_exact(self, op: Op, out: List[str], depth: int) -> None:
+        """A fused lazy-softmax group with only its exact half."""
+        self._lazy_exact_only = True
+        self._emit_op(op, out, depth)
+        self._lazy_exact_only = False
 
     def _emit_ops(self, ops, out: List[str], depth: int) -> None:
         for op in ops:
@@ -1150,7 +1164,7 @@ class CDNA4Lowerer:
             self._emit_ops(post, out, depth + 3)
             out.append(f"{q}  }}")
             out.append(f"{q}  if (!wir_exact) break;")
-            self._emit_op(body[fused_at], out, depth + 2)
+            self._emit_exact(body[fused_at], out, depth + 2)
             self._emit_ops(post, out, depth + 2)
             out.append(f"{q}  {iv} += {self._int(op.step)};")
             out.append(f"{q}}}")
@@ -1160,7 +1174,7 @@ class CDNA4Lowerer:
         out.append(f"{q}if (({stop}) > {start}) {{")
         out.append(f"{q}  const int {iv} = {start};")
         self._emit_ops(pre, out, depth + 2)
-        self._emit_op(body[fused_at], out, depth + 2)   # exact path: the running max starts at -inf
+        self._emit_exact(body[fused_at], out, depth + 2)   # the running max starts at -inf
         out.append(f"{q}}}")
         out.append(f"{q}int {iv} = ({start}) + 1;")
         out.append(f"{q}for (;;) {{")
@@ -1171,7 +1185,7 @@ class CDNA4Lowerer:
         fast_call(depth + 3)
         out.append(f"{q}  }}")
         out.append(f"{q}  if (!wir_exact) break;")
-        self._emit_op(body[fused_at], out, depth + 2)
+        self._emit_exact(body[fused_at], out, depth + 2)
         out.append(f"{q}  ++{iv};")
         out.append(f"{q}}}")
         out.append(f"{q}if (({stop}) > {start}) {{")
@@ -1267,13 +1281,21 @@ class CDNA4Lowerer:
                 rotated), then S_i = Q K_i^T;
           V(i): the online-softmax ops of iteration i, and this group's share
                 of the ring loads.
-        Group A runs M(i) while group B runs V(i-1).  Every phase starts with
+        Group A runs M(i) while group B runs V(i-1).  A barrier is
         ``vmcnt(L)`` and a workgroup barrier, L the loads one wave issues per
-        tile.  With a ring of S >= 4 slots, tile t is loaded S - 2 iterations
-        ahead into slot t % S: A's V(i) loads K tile i + S - 2, B's V(i) loads
-        V tile i + S - 1 (B's V phase of iteration i runs during A's M(i+1)),
-        so the slot written (tile t - S) was last read by the PV MMAs of the
-        iteration before.
+        tile.  With ``pingpong_one_barrier`` each wave passes one barrier per
+        iteration -- group A after its V phase, group B after its M phase --
+        so between two barriers A runs M(i), V(i) and B runs V(i-1), M(i),
+        and neither group waits for the other inside the interval;
+        otherwise every phase ends with one (lock-step).  With a ring of
+        S >= 4 slots, tile t is loaded S - 2 iterations ahead into slot
+        t % S: A's V(i) loads K tile i + S - 2, B's V(i) loads V tile
+        i + S - 1 (B's V phase of iteration i runs during A's M(i+1)).  In
+        the one-barrier form K tile t is issued in interval t - 2, complete
+        at its loader's barrier closing interval t - 1 (the next batch is
+        then the only one outstanding) and read in interval t; V tile t is
+        issued in interval t - 2 and read in interval t + 1; the slot a load
+        writes was last read two intervals (K) or one interval (V) before.
         """
         plan = self._attention_pingpong_plan(loop)
         if plan is None or plan["S"] < 4:
@@ -1336,10 +1358,22 @@ class CDNA4Lowerer:
         out.append(f"{q}  }}")
         out.append(f"{q}}}")
         out.append(f"{q}wir::wait_vm_barrier<{per}>();")
+        one = self.target.pingpong_one_barrier
         out.append(f"{q}if (wir_grp == 1) {{   // group B's first V phase: its first ring load only")
         out.extend(dma(v_ld, f"({start}) + {dist}", depth + 2)[0])
-        out.append(f"{q}  wir::wait_vm_barrier<{per}>();")
+        if not one:
+            out.append(f"{q}  wir::wait_vm_barrier<{per}>();")
         out.append(f"{q}}}")
+
+        def m_barrier(d: int) -> None:   # end of an M phase
+            pd = "  " * d
+            out.append(f"{pd}if (wir_grp == 1) wir::wait_vm_barrier<{per}>();" if one
+                       else f"{pd}wir::wait_vm_barrier<{per}>();")
+
+        def v_barrier(d: int) -> None:   # end of a V phase
+            pd = "  " * d
+            out.append(f"{pd}if (wir_grp == 0) wir::wait_vm_barrier<{per}>();" if one
+                       else f"{pd}wir::wait_vm_barrier<{per}>();")
         softmax = plan["softmax"]
         fused_at = next((k for k, o in enumerate(softmax) if isinstance(self._softmax_fused.get(id(o)), dict)), None)
 
@@ -1354,22 +1388,24 @@ class CDNA4Lowerer:
         def v_tail(ops, d: int) -> None:
             self._emit_ops(ops, out, d)
             self._emit_op(plan["yld"], out, d)
-            out.append(f"{'  ' * d}wir::wait_vm_barrier<{per}>();")
+            v_barrier(d)
 
         def m_phase(d: int) -> None:
             emit_pv(out, d)
             out.append(f"{'  ' * d}__builtin_amdgcn_sched_barrier(0);")
             self._emit_op(qk, out, d)
-            out.append(f"{'  ' * d}wir::wait_vm_barrier<{per}>();")
+            m_barrier(d)
 
         # the first iteration (no PV yet) is peeled so the loop body's PV is
         # unconditional and O keeps one register assignment around the loop
         out.append(f"{q}if (({stop}) > {start}) {{")
         out.append(f"{q}  const int {iv} = {start};")
         self._emit_op(qk, out, depth + 2)
-        out.append(f"{q}  wir::wait_vm_barrier<{per}>();")
+        m_barrier(depth + 2)
         v_loads(depth + 2)
+        self._lazy_exact_only = True    # the first tile's running max is -inf
         v_tail(softmax, depth + 2)
+        self._lazy_exact_only = False
         out.append(f"{q}}}")
         if fused_at is None:
             out.append(f"{q}for (int {iv} = ({start}) + 1; {iv} < {stop}; ++{iv}) {{")
@@ -1400,7 +1436,7 @@ class CDNA4Lowerer:
             v_tail(post, depth + 3)
             out.append(f"{q}  }}")
             out.append(f"{q}  if (!wir_exact) break;")
-            self._emit_op(softmax[fused_at], out, depth + 2)   # the whole step, exact path included
+            self._emit_exact(softmax[fused_at], out, depth + 2)   # the step's exact half
             v_tail(post, depth + 2)
             out.append(f"{q}  ++{iv};")
             out.append(f"{q}}}")
@@ -1409,7 +1445,8 @@ class CDNA4Lowerer:
         out.append(f"{q}  const int {iv} = ({stop});")
         emit_pv(out, depth + 2)
         out.append(f"{q}}}")
-        out.append(f"{q}if (wir_grp == 0) wir::wait_vm_barrier<0>();   // pairs with group B's extra V phase")
+        if not one:
+            out.append(f"{q}if (wir_grp == 0) wir::wait_vm_barrier<0>();   // pairs with group B's extra V phase")
         out.append(f"{pad}}}")
         return True
 
