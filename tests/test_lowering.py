@@ -35,7 +35,8 @@ def test_every_variant_lowers_to_self_contained_hip(name):
 
 
 def _waits(src):
-    return [int(x) for x in re.findall(r"wait_vm_barrier<(\d+)>", src)]
+    body = src[src.rindex('extern "C" __global__'):]   # the kernel, not the tile library
+    return [int(x) for x in re.findall(r"wait_vm_barrier<(\d+)>", body)]
 
 
 def test_pipelined_gemm_waits_keep_one_stage_in_flight():
@@ -150,14 +151,18 @@ def test_attention_pingpong_one_barrier_per_iteration():
     src = CDNA4Lowerer(CDNA4Target()).lower(k)
     pp = src[src.index("const int wir_grp ="):src.index("ring buffers dead")]
     lines = [l.strip() for l in pp.split("\n")]
+    stop = "((globals.N) + 63) / 64"
+    after = f"wir::wait_vm_barrier_after<4>((v_i) + 2 < {stop});"   # drains fully once past the end
     assert lines.count("wir::wait_vm_barrier<4>();") == 1                      # after the prologue loads
-    assert lines.count("if (wir_grp == 1) wir::wait_vm_barrier<4>();") == 2    # after M: peeled, loop
-    assert lines.count("if (wir_grp == 0) wir::wait_vm_barrier<4>();") == 3    # after V: peeled, loop, exact
+    assert lines.count(f"if (wir_grp == 1) {after}") == 2    # after M: peeled, loop
+    assert lines.count(f"if (wir_grp == 0) {after}") == 3    # after V: peeled, loop, exact
     assert "pairs with group B" not in pp
+    # ring loads of tiles past the end are skipped
+    assert lines.count(f"if ((v_i) + 2 < {stop})") == 2 and lines.count(f"if ((v_i) + 3 < {stop})") == 2
     two = CDNA4Lowerer(CDNA4Target(pingpong_one_barrier=False)).lower(k)
     pp2 = two[two.index("const int wir_grp ="):two.index("ring buffers dead")]
     assert "if (wir_grp == 0) wir::wait_vm_barrier<0>();   // pairs with group B's extra V phase" in pp2
-    assert "if (wir_grp == 1) wir::wait_vm_barrier" not in pp2
+    assert "if (wir_grp == 1) wir::wait_vm_barrier" not in pp2 and "wir_grp == 0 ? 1 : 0" in pp2
 
 
 def test_warp_specialized_gemm_form():

@@ -299,6 +299,18 @@ __device__ __forceinline__ void wait_vm_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// wait_vm_barrier<N> after a wave's latest batch of N loads was issued;
+// when that batch was skipped (a tile past the loop's end) the batch before
+// it is the newest and must land too: wait_vm_barrier<0>.  One barrier on
+// either branch (the condition is wave-uniform).
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier_after(bool issued) {
+  if (issued)
+    wait_vm_barrier<N>();
+  else
+    wait_vm_barrier<0>();
+}
+
 __device__ __forceinline__ void barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();

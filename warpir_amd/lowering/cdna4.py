@@ -1365,24 +1365,34 @@ class CDNA4Lowerer:
             out.append(f"{q}  wir::wait_vm_barrier<{per}>();")
         out.append(f"{q}}}")
 
+        # Ring loads of tiles past the loop's end are skipped; a barrier whose
+        # wave's latest batch was skipped drains all its loads instead (the
+        # batch before is then the newest).  A's batch of V(i) is K tile
+        # i + dist, B's batch of V(i) is V tile i + dist + 1.
         def m_barrier(d: int) -> None:   # end of an M phase
             pd = "  " * d
-            out.append(f"{pd}if (wir_grp == 1) wir::wait_vm_barrier<{per}>();" if one
-                       else f"{pd}wir::wait_vm_barrier<{per}>();")
+            if one:   # B's latest batch: from its V(i-1)
+                out.append(f"{pd}if (wir_grp == 1) wir::wait_vm_barrier_after<{per}>(({iv}) + {dist} < {stop});")
+            else:
+                out.append(f"{pd}wir::wait_vm_barrier_after<{per}>(({iv}) + {dist} - (wir_grp == 0 ? 1 : 0) < {stop});")
 
         def v_barrier(d: int) -> None:   # end of a V phase
             pd = "  " * d
-            out.append(f"{pd}if (wir_grp == 0) wir::wait_vm_barrier<{per}>();" if one
-                       else f"{pd}wir::wait_vm_barrier<{per}>();")
+            if one:   # A's latest batch: from this V(i)
+                out.append(f"{pd}if (wir_grp == 0) wir::wait_vm_barrier_after<{per}>(({iv}) + {dist} < {stop});")
+            else:
+                out.append(f"{pd}wir::wait_vm_barrier_after<{per}>(({iv}) + {dist} + (wir_grp == 1 ? 1 : 0) < {stop});")
         softmax = plan["softmax"]
         fused_at = next((k for k, o in enumerate(softmax) if isinstance(self._softmax_fused.get(id(o)), dict)), None)
 
         def v_loads(d: int) -> None:
             qq = "  " * d
             out.append(f"{qq}if (wir_grp == 0) {{")
-            out.extend(dma(k_ld, f"({iv}) + {dist}", d + 1)[0])
+            out.append(f"{qq}  if (({iv}) + {dist} < {stop})")
+            out.extend(dma(k_ld, f"({iv}) + {dist}", d + 2)[0])
             out.append(f"{qq}}} else {{")
-            out.extend(dma(v_ld, f"({iv}) + {dist + 1}", d + 1)[0])
+            out.append(f"{qq}  if (({iv}) + {dist + 1} < {stop})")
+            out.extend(dma(v_ld, f"({iv}) + {dist + 1}", d + 2)[0])
             out.append(f"{qq}}}")
 
         def v_tail(ops, d: int) -> None:
