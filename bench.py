@@ -25,6 +25,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -36,7 +37,12 @@ PEAK_HBM_GBS = 8000.0
 METRIC = "bf16 TFLOP/s + % MFMA peak: GEMM 8192³ and FA-fwd B16 H16 S4096 D128"
 
 
-def _time_launches(launch, steps: int, warmup: int, stream):
+def _time_launches(launch, steps: int, warmup: int, stream, per_launch: bool = False):
+    """Mean ms per launch over ``steps`` back-to-back launches (one event pair
+    around all of them) and the wall-clock mean; with ``per_launch``, also the
+    median of ``steps`` launches each bracketed by its own event pair (the
+    reference's method, tests/test_modal_gpu.py:126-152).  Returns
+    ``(mean_ms, wall_ms, median_ms or None)``."""
     import torch
 
     from warpir_amd.runtime import Event
@@ -52,7 +58,17 @@ def _time_launches(launch, steps: int, warmup: int, stream):
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return e0.elapsed_ms(e1) / steps, wall * 1e3 / steps
+    mean = e0.elapsed_ms(e1) / steps
+    median = None
+    if per_launch:
+        pairs = [(Event(), Event()) for _ in range(steps)]
+        for a, b in pairs:
+            a.record(stream)
+            launch()
+            b.record(stream)
+        torch.cuda.synchronize()
+        median = statistics.median(a.elapsed_ms(b) for a, b in pairs)
+    return mean, wall * 1e3 / steps, median
 
 
 def _traffic_from_profiles(kernel: str):
@@ -67,7 +83,7 @@ def _traffic_from_profiles(kernel: str):
     return None
 
 
-def bench_gemm(steps, warmup, cpu: bool):
+def bench_gemm(steps, warmup, cpu: bool, median: bool = False):
     import torch
 
     from oracle.torch_ref import gemm_ref, seeded_normal
@@ -83,11 +99,13 @@ def bench_gemm(steps, warmup, cpu: bool):
     def launch():
         h(A=a, B=b, N=k, C_global=c)
 
-    ms, wall_ms = _time_launches(launch, steps, warmup, stream)
+    mean, wall_ms, med = _time_launches(launch, steps, warmup, stream, per_launch=True)
+    ms = med if median else mean
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
     res = {
-        "value": tflops, "ms_per_step": ms, "wall_ms_per_step": wall_ms,
+        "value": tflops, "ms_per_step": ms, "wall_ms_per_step": wall_ms, "ms_median_per_launch": med,
+        "ms_back_to_back": mean,
         "config": {"workload": "gemm_bf16_8192x8192x8192", "M": m, "N": n, "K": k,
                    "kernel": "gemm_256_k64", "block_tile": [256, 256, 64], "lds_stages": 2,
                    "wavefronts": 4},
@@ -119,7 +137,7 @@ def _cpu_gemm(a, b, gemm_ref):
             "sample": f"torch.matmul fp32 on {rows} of 8192 rows of A (x 8192x8192 B), median of 3"}
 
 
-def bench_fa(steps, warmup, cpu: bool):
+def bench_fa(steps, warmup, cpu: bool, median: bool = False):
     import torch
 
     from oracle.torch_ref import attention_ref, seeded_normal
@@ -135,12 +153,14 @@ def bench_fa(steps, warmup, cpu: bool):
     def launch():
         h(Q=q, K=k, V=v, N=seq, O=o, L=lse)
 
-    ms, wall_ms = _time_launches(launch, steps, warmup, stream)
+    mean, wall_ms, med = _time_launches(launch, steps, warmup, stream, per_launch=True)
+    ms = med if median else mean
     flops = api.attention_flops(bsz, heads, seq, d)
     tflops = flops / (ms * 1e-3) / 1e12
     ref_flops = flops + 4.0 * bsz * heads * seq * seq   # the reference's formula adds softmax
     res = {
         "value": tflops, "unit": "TFLOP/s", "ms_per_step": ms, "wall_ms_per_step": wall_ms,
+        "ms_median_per_launch": med, "ms_back_to_back": mean,
         "tflops_with_softmax_term": ref_flops / (ms * 1e-3) / 1e12,
         "config": {"workload": "fa_fwd_bf16_B16_H16_S4096_D128_noncausal", "B": bsz, "H": heads, "S": seq,
                    "D": d, "kernel": "mha_d128", "outputs": "O bf16 + LSE fp32"},
@@ -165,73 +185,158 @@ def bench_fa(steps, warmup, cpu: bool):
     return res
 
 
-def bench_extra(steps: int, warmup: int):
-    """The other BASELINE configurations, one timed line each (no CPU leg).
+def _extra_gemm(m: int, n: int, k: int, steps: int, warmup: int, rotate: int = 1):
+    """One GEMM configuration through the kernel ``api.gemm_variant`` picks.
+    ``rotate`` distinct B operands are cycled launch by launch, so that with
+    ``rotate * K * N * 2`` bytes above the 256 MB MALL every launch streams
+    its B from HBM."""
+    import itertools
 
-    GEMM 4096^3 (config 2), skinny GEMM M=128 N=K=8192 (config 3', judged
-    on the HBM roofline: 2(MK+KN+MN) bytes), causal FA B8 H32 S8192 D64
-    (config 5, matmul flops halved for the mask), and FlashAttention
-    backward at the config-4 shape (prep + dQ + dK/dV kernels).
-    """
     import torch
 
     from oracle.torch_ref import seeded_normal
     from warpir_amd import api, kernels
 
     stream = torch.cuda.current_stream().cuda_stream
-    out = {}
-    for name, (m, n, k) in {"gemm_4096": (4096, 4096, 4096), "gemm_skinny_m128": (128, 8192, 8192)}.items():
-        a = seeded_normal((m, k), 5, 0.1).cuda()
-        b = seeded_normal((k, n), 6, 0.1).cuda()
-        c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-        variant = api.gemm_variant(m, n, k)
-        h = kernels.handle(variant)
-        ms, _ = _time_launches(lambda: h(A=a, B=b, N=k, C_global=c), steps, warmup, stream)
-        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        rec = {"M": m, "N": n, "K": k, "ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
-               "kernel": variant}
-        if name == "gemm_skinny_m128":
-            gbs = 2.0 * (m * k + k * n + m * n) / (ms * 1e-3) / 1e9
-            rec.update({"hbm_gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "bound": "hbm"})
-        out[name] = rec
-        del a, b, c
+    a = seeded_normal((m, k), 5, 0.1).cuda()
+    bs = [seeded_normal((k, n), 6 + i, 0.1).cuda() for i in range(rotate)]
+    c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    variant = api.gemm_variant(m, n, k)
+    h = kernels.handle(variant)
+    nxt = itertools.cycle(bs).__next__
+    mean, _, med = _time_launches(lambda: h(A=a, B=nxt(), N=k, C_global=c), steps, warmup, stream,
+                                  per_launch=True)
+    tf = 2.0 * m * n * k / (mean * 1e-3) / 1e12
+    rec = {"M": m, "N": n, "K": k, "ms": mean, "timing": "mean of back-to-back launches between one event pair",
+           "ms_median_per_launch": med, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS, "kernel": variant}
+    if rotate > 1:
+        rec["b_buffers_rotated"] = rotate
+        rec["b_bytes_rotated"] = rotate * k * n * 2
+    return rec
+
+
+def _extra_skinny(steps: int, warmup: int):
+    """Config 3': M=128, N=K=8192, judged on the HBM roofline.  Four 128 MiB
+    B operands rotate (512 MiB, twice the MALL).  ``frac_hbm`` divides the
+    counter-measured HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, scaled
+    by a plain copy's reading) by the launch time; the algorithmic
+    2(MK + KN + MN) bytes give ``frac_hbm_algorithmic``."""
+    m, n, k = 128, 8192, 8192
+    rec = _extra_gemm(m, n, k, steps, warmup, rotate=4)
+    algo = 2.0 * (m * k + k * n + m * n)
+    sec = rec["ms"] * 1e-3
+    rec.update({"bound": "hbm", "algorithmic_bytes": algo, "hbm_gbs_algorithmic": algo / sec / 1e9,
+                "frac_hbm_algorithmic": algo / sec / 1e9 / PEAK_HBM_GBS})
+    traffic = _traffic_from_profiles(rec["kernel"])
+    if traffic is not None:
+        rec.update({"traffic": traffic, "hbm_gbs": traffic / sec / 1e9, "frac_hbm": traffic / sec / 1e9 / PEAK_HBM_GBS,
+                    "frac_hbm_source": f"profiles/{rec['kernel']}_traffic.txt"})
+    else:
+        rec.update({"hbm_gbs": algo / sec / 1e9, "frac_hbm": algo / sec / 1e9 / PEAK_HBM_GBS,
+                    "frac_hbm_source": "algorithmic bytes (no counter profile)"})
+    return rec
+
+
+def _extra_fa_causal_d64(steps: int, warmup: int):
+    """Config 5: causal FA forward B8 H32 S8192 D64 (matmul flops halved for the mask)."""
+    import torch
+
+    from oracle.torch_ref import seeded_normal
+    from warpir_amd import api, kernels
+
+    stream = torch.cuda.current_stream().cuda_stream
     bsz, heads, seq, d = 8, 32, 8192, 64
     q, k, v = (seeded_normal((bsz, heads, seq, d), s).cuda() for s in (3, 4, 5))
     o = torch.empty_like(q)
     lse = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
     h = kernels.handle("mha_d64_causal")
-    ms, _ = _time_launches(lambda: h(Q=q, K=k, V=v, N=seq, O=o, L=lse), steps, warmup, stream)
+    ms, _, med = _time_launches(lambda: h(Q=q, K=k, V=v, N=seq, O=o, L=lse), steps, warmup, stream,
+                                per_launch=True)
     tf = api.attention_flops(bsz, heads, seq, d, causal=True) / (ms * 1e-3) / 1e12
-    out["fa_fwd_causal_b8_h32_s8192_d64"] = {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
-                                             "kernel": "mha_d64_causal"}
-    del q, k, v, o, lse
-    # FlashAttention backward at the config-4 shape (next step after the forward)
+    return {"ms": ms, "ms_median_per_launch": med, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
+            "kernel": "mha_d64_causal"}
+
+
+def _bwd_inputs():
+    import torch
+
+    from oracle.torch_ref import seeded_normal
+
     bsz, heads, seq, d = 16, 16, 4096, 128
     q, k, v, do = (seeded_normal((bsz, heads, seq, d), s).cuda() for s in (10, 11, 12, 13))
-    o, lse = api.attention_forward(q, k, v)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
-    ms, _ = _time_launches(lambda: api.attention_backward(q, k, v, o, lse, do, dq, dk, dv, dvec),
-                           max(3, steps // 2), max(1, warmup // 2), stream)
+    return (bsz, heads, seq, d), (q, k, v, do, dq, dk, dv, dvec)
+
+
+def _extra_fa_bwd(steps: int, warmup: int):
+    """FlashAttention backward at the config-4 shape (prep + dQ + dK/dV kernels)."""
+    import torch
+
+    from warpir_amd import api
+
+    stream = torch.cuda.current_stream().cuda_stream
+    (bsz, heads, seq, d), (q, k, v, do, dq, dk, dv, dvec) = _bwd_inputs()
+    o, lse = api.attention_forward(q, k, v)
+    ms, _, _ = _time_launches(lambda: api.attention_backward(q, k, v, o, lse, do, dq, dk, dv, dvec),
+                              max(3, steps // 2), max(1, warmup // 2), stream)
     tf = api.attention_backward_flops(bsz, heads, seq, d) / (ms * 1e-3) / 1e12
-    out["fa_bwd_b16_h16_s4096_d128"] = {
+    return {"fa_bwd_b16_h16_s4096_d128": {
         "ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
         "kernels": ["mha_bwd_prep_d128", "mha_bwd_dq_d128", "mha_bwd_dkdv_d128"],
-        "flops": "10*B*H*S^2*D (the five S x S x D products); the kernels run seven (dQ recomputes S and dP)"}
-    # causal forward and backward at the same shape
+        "flops": "10*B*H*S^2*D (the five S x S x D products); the kernels run seven (dQ recomputes S and dP)"}}
+
+
+def _extra_fa_causal_d128(steps: int, warmup: int):
+    """Causal forward and backward at the config-4 shape."""
+    import torch
+
+    from warpir_amd import api
+
+    stream = torch.cuda.current_stream().cuda_stream
+    (bsz, heads, seq, d), (q, k, v, do, dq, dk, dv, dvec) = _bwd_inputs()
     o, lse = api.attention_forward(q, k, v, causal=True)
-    ms, _ = _time_launches(lambda: api.attention_forward(q, k, v, causal=True, out=o, lse=lse), steps, warmup,
-                           stream)
+    ms, _, _ = _time_launches(lambda: api.attention_forward(q, k, v, causal=True, out=o, lse=lse), steps, warmup,
+                              stream)
     tf = api.attention_flops(bsz, heads, seq, d, causal=True) / (ms * 1e-3) / 1e12
-    out["fa_fwd_causal_b16_h16_s4096_d128"] = {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
-                                               "kernel": "mha_d128_causal"}
-    ms, _ = _time_launches(lambda: api.attention_backward(q, k, v, o, lse, do, dq, dk, dv, dvec, causal=True),
-                           max(3, steps // 2), max(1, warmup // 2), stream)
+    out = {"fa_fwd_causal_b16_h16_s4096_d128": {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
+                                                "kernel": "mha_d128_causal"}}
+    ms, _, _ = _time_launches(lambda: api.attention_backward(q, k, v, o, lse, do, dq, dk, dv, dvec, causal=True),
+                              max(3, steps // 2), max(1, warmup // 2), stream)
     tf = api.attention_backward_flops(bsz, heads, seq, d, causal=True) / (ms * 1e-3) / 1e12
     out["fa_bwd_causal_b16_h16_s4096_d128"] = {
         "ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
         "kernels": ["mha_bwd_prep_d128", "mha_bwd_dq_d128_causal", "mha_bwd_dkdv_d128_causal"],
         "flops": "5*B*H*S^2*D (the five products, halved by the causal mask)"}
+    return out
+
+
+# The other BASELINE configurations (no CPU leg), by --only name -> (result key or None for a
+# dict of several results, function).
+EXTRA = {
+    "gemm4096": ("gemm_4096", lambda s, w: _extra_gemm(4096, 4096, 4096, s, w)),
+    "skinny": ("gemm_skinny_m128", _extra_skinny),
+    "fa_causal_d64": ("fa_fwd_causal_b8_h32_s8192_d64", _extra_fa_causal_d64),
+    "fa_bwd": (None, _extra_fa_bwd),
+    "fa_causal_d128": (None, _extra_fa_causal_d128),
+}
+
+
+def bench_extra(steps: int, warmup: int, names=None):
+    """The configurations of ``EXTRA`` named in *names* (all when None), in order."""
+    import torch
+
+    out = {}
+    for name, (key, fn) in EXTRA.items():
+        if names is not None and name not in names:
+            continue
+        print(f"[bench] {name}", file=sys.stderr, flush=True)
+        res = fn(steps, warmup)
+        if key is None:
+            out.update(res)
+        else:
+            out[key] = res
+        torch.cuda.empty_cache()
     return out
 
 
@@ -350,13 +455,20 @@ def bench_compare(steps: int, warmup: int):
     return out
 
 
+ONLY = ["gemm", "fa", "ceiling"] + list(EXTRA)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["gemm", "fa"], default=None)
+    ap.add_argument("--only", default=None, metavar="NAMES",
+                    help="comma-separated subset of " + ",".join(ONLY) + " (profiling runs)")
+    ap.add_argument("--median", action="store_true",
+                    help="headline value from the median of per-launch event pairs (the reference's method) "
+                         "instead of the mean over back-to-back launches")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
     ap.add_argument("--compare", action="store_true",
                     help="also time the schedule alternatives (COMPARE_GEMM / COMPARE_FA) at the headline shapes")
@@ -369,6 +481,13 @@ def main() -> int:
               "GEMM shards by output rows and attention by (batch, head), with no communication",
               file=sys.stderr)
         return 2
+    only = None
+    if args.only:
+        only = [x.strip() for x in args.only.split(",") if x.strip()]
+        bad = [x for x in only if x not in ONLY]
+        if bad:
+            print(f"bench.py: unknown --only names {bad}; choose from {ONLY}", file=sys.stderr)
+            return 2
 
     import torch
 
@@ -379,20 +498,20 @@ def main() -> int:
         return 1
     info = device_info(0)
     gemm = fa = None
-    if args.only in (None, "gemm"):
+    if only is None or "gemm" in only:
         print("[bench] gemm 8192^3", file=sys.stderr, flush=True)
-        gemm = bench_gemm(args.steps, args.warmup, not args.no_cpu)
-    if args.only in (None, "fa"):
+        gemm = bench_gemm(args.steps, args.warmup, not args.no_cpu, args.median)
+    if only is None or "fa" in only:
         print("[bench] fa-fwd B16 H16 S4096 D128", file=sys.stderr, flush=True)
-        fa = bench_fa(args.steps, args.warmup, not args.no_cpu)
+        fa = bench_fa(args.steps, args.warmup, not args.no_cpu, args.median)
     ceiling = None
-    if args.only is None:
+    if only is None or "ceiling" in only:
         print("[bench] mfma ceiling probe", file=sys.stderr, flush=True)
         ceiling = mfma_ceiling()
     extra = None
-    if args.only is None and not args.no_extra:
-        print("[bench] other configurations", file=sys.stderr, flush=True)
-        extra = bench_extra(max(5, args.steps // 2), max(2, args.warmup // 2))
+    names = [x for x in only if x in EXTRA] if only is not None else None
+    if not args.no_extra and (names is None or names):
+        extra = bench_extra(max(5, args.steps // 2), max(2, args.warmup // 2), names)
     compare = None
     if args.compare:
         print("[bench] schedule comparison", file=sys.stderr, flush=True)
@@ -407,14 +526,27 @@ def main() -> int:
         print(f"[bench] calibration copy: {args.calibrate_copy} MiB read + written, 3 launches",
               file=sys.stderr, flush=True)
     head = gemm or fa
+    if head is None:   # a profiling run of other configurations only
+        print(json.dumps({"metric": METRIC, "value": None, "partial_run": only, "other_configs": extra,
+                          "mfma_ceiling": ceiling, "device": info}))
+        return 0
     line = {
         "metric": METRIC, "value": head["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1), GEMM x0.1)",
         "config": head["config"], "roofline": head["roofline"],
+        "timing": ("median of per-launch HIP event pairs" if args.median else
+                   "mean of back-to-back launches between one HIP event pair"),
+        "peak_note": ("frac = achieved / 2500 TFLOP/s, AMD's published dense bf16 MFMA peak for MI355X "
+                      "(2516.6 = 256 CUs x 4 SIMDs x 1024 flop/clk x 2.4 GHz is 0.7% higher)"),
     }
     if "cpu_baseline" in head:
         line["cpu_baseline"] = head["cpu_baseline"]
+    if ceiling is not None and ceiling.get("random_operands"):
+        roof = ceiling["random_operands"]["tflops"]
+        line["value_vs_mfma_ceiling"] = head["value"] / roof
+        if gemm is not None and fa is not None:
+            fa["value_vs_mfma_ceiling"] = fa["value"] / roof
     if gemm is not None and fa is not None:
         line["fa_fwd"] = fa
     if extra is not None:
