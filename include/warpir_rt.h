@@ -35,7 +35,7 @@ typedef void* wir_function_t; /* a kernel inside a module (hipFunction_t) */
 typedef void* wir_event_t;    /* a timing event (hipEvent_t)              */
 
 /* ABI version of this header; bumped on any signature change. */
-#define WIR_RT_ABI_VERSION 2
+#define WIR_RT_ABI_VERSION 3
 int wir_abi_version(void);
 
 /* Make `device` current for the calling thread. */
@@ -92,12 +92,24 @@ const char* wir_error_string(int code);
 #define WIR_NOALLOC_SCRATCH_FLOATS (8 * 1024 * 1024)
 
 /* out[M][N] (bf16) = a[M][K] @ b[K][N] (bf16, row-major, contiguous) as
+ * `splits` K slices plus an fp32 reduction, the partials in `workspace`
+ * (fp32, at least splits * M * N of its `workspace_floats`, 16-byte
+ * aligned): both launches of one product in one call, on `stream`.  The
+ * reference has no split-K path; this is the host side of
+ * warpir_amd.api.gemm_split_k, whose short-M products would otherwise be
+ * bound by per-launch host work.  gemm and reduce as below. */
+int wir_gemm_splitk(wir_function_t gemm, wir_function_t reduce, const void* a, const void* b,
+                    void* out, void* workspace, size_t workspace_floats, int m, int n, int k,
+                    int splits, void* stream);
+
+/* out[M][N] (bf16) = a[M][K] @ b[K][N] (bf16, row-major, contiguous) as
  * `splits` K slices plus an fp32 reduction, with no device allocation: the
  * fp32 partials live in the library's own device scratch instead of a
  * workspace.  No counterpart in the reference; it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).
- *   gemm   -- gemm_128_splitk, loaded from its code object;
+ *   gemm   -- a split-K GEMM variant (128x128 tiles, 4 wavefronts:
+ *             gemm_128_splitk*), loaded from its code object;
  *   reduce -- wir_splitk_reduce, loaded from splitk_reduce.hsaco.
  * Requires 1 <= splits <= 16, K % (64 * splits) == 0, N % 8 == 0 and 16-byte
  * aligned a, b, out; returns WIR_ERROR_SCRATCH_LIMIT when

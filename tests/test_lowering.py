@@ -237,11 +237,11 @@ def test_c_abi_library_exports_every_declared_symbol():
         pytest.skip("libwarpir_rt.so not built (run __graft_entry__.build())")
     lib = ctypes.CDLL(LIB_PATH)
     syms = _declared_symbols()
-    assert len(syms) == 16
+    assert len(syms) == 17
     for s in syms:
         assert hasattr(lib, s), s
     lib.wir_abi_version.restype = ctypes.c_int
-    assert lib.wir_abi_version() == 2
+    assert lib.wir_abi_version() == 3
     lib.wir_error_string.restype = ctypes.c_char_p
     assert lib.wir_error_string(0)
 
@@ -264,9 +264,10 @@ def test_gemm_variant_selection():
     assert api.gemm_variant(8192, 8192) == "gemm_256_k64"
     assert api.gemm_variant(4096, 4096) == "gemm_256_k64"      # 256 tiles: one per CU
     assert api.gemm_variant(2048, 2048) == "gemm_128_k64"      # 64 tiles of 256x256
-    assert api.gemm_variant(128, 8192) == "gemm_128x32_k64"
+    assert api.gemm_variant(128, 8192) == "gemm_128x32_k64"          # K unknown: no split
     assert api.gemm_variant(256, 8192) == "gemm_128x64_k64"
-    assert api.gemm_variant(64, 8192, 8192) == "gemm_128_splitk"
+    assert api.gemm_variant(64, 8192, 8192) == api.SPLITK_GEMM_VARIANT == "gemm_128_splitk_k128"
+    assert api.gemm_variant(128, 8192, 8192) == api.SPLITK_GEMM_VARIANT
     assert api.gemm_variant(64, 8192, 100) == "gemm_128x32_k64"   # K too short to split
     for v in ("gemm_256_k64", "gemm_128_k64", "gemm_128x32_k64"):
         assert v in kernels.VARIANTS

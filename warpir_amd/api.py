@@ -23,9 +23,11 @@ MID_GEMM_VARIANT = "gemm_128_k64"         # fewer 256x256 tiles than CUs: 128x12
 def gemm_variant(m: int, n: int, k: Optional[int] = None) -> str:
     """Kernel variant for an M x N (x K) GEMM on the 256 CUs of one MI355X.
 
-    Measured at N = K = 8192 (TFLOP/s): M=64 split-K x4 214 vs 128x32 125;
-    M=128 128x32 443 vs split-K x4 438; M=256 128x64 718 vs 128x32 469."""
-    if m <= 64 and k is not None and splitk_count(m, n, k) >= 4:
+    Measured at N = K = 8192 with four B operands cycled (512 MiB, so B
+    streams from HBM), microseconds per product: M=64 split-K x4 42.4 vs
+    128x32 67.1; M=128 split-K x4 38.8 vs 128x32 60.4; M=256 128x64 68.5
+    vs split-K x2 69.6."""
+    if m <= 128 and k is not None and splitk_count(m, n, k) >= 4:
         return SPLITK_GEMM_VARIANT
     if m <= 128:
         return SKINNY_GEMM_VARIANT
@@ -36,7 +38,9 @@ def gemm_variant(m: int, n: int, k: Optional[int] = None) -> str:
     return GEMM_VARIANT
 
 
-SPLITK_GEMM_VARIANT = "gemm_128_splitk"
+# 128x128 tiles, 128-deep K steps double-buffered in 128 KiB of LDS: each
+# slice's B panel streams with 64 KiB in flight per CU.
+SPLITK_GEMM_VARIANT = "gemm_128_splitk_k128"
 _reduce_kernel = None
 
 
@@ -54,31 +58,44 @@ def splitk_count(m: int, n: int, k: int, num_cus: int = 256) -> int:
     return best
 
 
-def _splitk_reduce(partials, out, splits: int) -> None:
-    import ctypes
+_splitk_checked: set = set()
 
+
+def _splitk_functions(variant: str):
+    """(GEMM, reduction) kernel functions of a split-K variant, loaded.  The
+    first use of a variant checks that its launch geometry is the one the C
+    ABI's split-K entry points build (128x128 tiles, 256 threads, slices on
+    blockIdx.z)."""
     from warpir_amd.runtime import RawKernel
 
     global _reduce_kernel
+    h = kernels.handle(variant)
+    if variant not in _splitk_checked:
+        cfg = h.lowerer.launch_config(h.kernel, {"A": (1, 2, 256, 512), "B": (1, 2, 512, 384),
+                                                 "C_global": (1, 2, 256, 384)})
+        if cfg.grid != (3, 2, 2) or tuple(cfg.block) != (256, 1, 1):
+            raise ValueError(f"{variant}: launch geometry {cfg} is not the split-K entry points' "
+                             "(128x128 tiles, 256 threads)")
+        _splitk_checked.add(variant)
+    h.load()
     if _reduce_kernel is None:
         _reduce_kernel = RawKernel("splitk_reduce.hsaco", "wir_splitk_reduce")
-
-    class Args(ctypes.Structure):
-        _fields_ = [("partials", ctypes.c_void_p), ("out", ctypes.c_void_p), ("n", ctypes.c_longlong),
-                    ("split_stride", ctypes.c_longlong), ("splits", ctypes.c_int)]
-
-    n = partials.shape[2] * partials.shape[3]   # M * N, the elements of one split
-    args = Args(partials.data_ptr(), out.data_ptr(), n, partials.stride(1), splits)
-    _reduce_kernel.launch(((n // 8 + 255) // 256, 1, 1), (256, 1, 1), args)
+    _reduce_kernel._load()
+    return h._function, _reduce_kernel._function
 
 
-def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None):
+def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None, variant: Optional[str] = None):
     """``out = a @ b`` as ``splits`` K slices run side by side (``blockIdx.z``)
     plus an fp32 reduction: the form for short M and long K, where the
     output alone has too few tiles to fill the chip.  ``workspace`` is an
     fp32 tensor of at least ``splits * M * N`` elements (allocated if
-    omitted)."""
+    omitted); ``variant`` names a split-K kernel variant (default
+    ``SPLITK_GEMM_VARIANT``)."""
+    import ctypes
+
     import torch
+
+    from warpir_amd.runtime import check, library
 
     if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
         raise ValueError(f"gemm: shapes {tuple(a.shape)} @ {tuple(b.shape)} do not chain")
@@ -88,7 +105,8 @@ def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None):
     if k % (64 * splits) or n % 8 or not a.is_contiguous() or not b.is_contiguous():
         raise ValueError(f"gemm_split_k: K={k} must split into {splits} multiples of 64, N % 8 == 0, "
                          "contiguous operands")
-    kc = k // splits
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise TypeError("gemm_split_k: a and b must be bf16")
     if out is None:
         out = torch.empty(m, n, dtype=torch.bfloat16, device=a.device)
     # the reduction writes M * N bf16 values flat from out's first element
@@ -101,11 +119,17 @@ def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None):
         workspace = torch.empty(splits * m * n, dtype=torch.float32, device=a.device)
     if workspace.numel() < splits * m * n or workspace.dtype != torch.float32:
         raise ValueError("gemm_split_k: workspace must be fp32 with splits * M * N elements")
-    av = a.as_strided((1, splits, m, kc), (0, kc, k, 1))
-    bv = b.view(1, splits, kc, n)
-    part = workspace[: splits * m * n].view(1, splits, m, n)
-    kernels.handle(SPLITK_GEMM_VARIANT)(A=av, B=bv, N=kc, C_global=part)
-    _splitk_reduce(part, out, splits)
+    if workspace.device != a.device or not workspace.is_contiguous():
+        raise ValueError("gemm_split_k: workspace must be a contiguous tensor on the operands' device")
+    if not a.is_cuda or b.device != a.device:
+        raise ValueError("gemm_split_k: a, b, out and workspace must be on one GPU")
+    if any(t.data_ptr() % 16 for t in (a, b, out, workspace)):
+        raise ValueError("gemm_split_k: a, b, out and workspace must be 16-byte aligned")
+    gemm_fn, reduce_fn = _splitk_functions(variant or SPLITK_GEMM_VARIANT)
+    stream = torch.cuda.current_stream(a.device).cuda_stream
+    check(library().wir_gemm_splitk(gemm_fn, reduce_fn, a.data_ptr(), b.data_ptr(), out.data_ptr(),
+                                    workspace.data_ptr(), workspace.numel(), m, n, k, splits,
+                                    ctypes.c_void_p(stream)), "wir_gemm_splitk")
     return out
 
 
@@ -123,9 +147,8 @@ def gemm_split_k_noalloc(a, b, out, splits: Optional[int] = None, stream=None):
 
     import torch
 
-    from warpir_amd.runtime import RawKernel, check, library
+    from warpir_amd.runtime import check, library
 
-    global _reduce_kernel
     if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
         raise ValueError(f"gemm: shapes {tuple(a.shape)} @ {tuple(b.shape)} do not chain")
     m, k = a.shape
@@ -137,28 +160,25 @@ def gemm_split_k_noalloc(a, b, out, splits: Optional[int] = None, stream=None):
             raise ValueError(f"gemm_split_k_noalloc: {name} must be a contiguous bf16 {list(shape)} tensor")
     if not a.is_cuda or b.device != a.device or out.device != a.device:
         raise ValueError("gemm_split_k_noalloc: a, b and out must be on one GPU")
-    gemm_h = kernels.handle(SPLITK_GEMM_VARIANT)
-    gemm_h.load()
-    if _reduce_kernel is None:
-        _reduce_kernel = RawKernel("splitk_reduce.hsaco", "wir_splitk_reduce")
-    _reduce_kernel._load()
+    gemm_fn, reduce_fn = _splitk_functions(SPLITK_GEMM_VARIANT)
     if stream is None:
         stream = torch.cuda.current_stream(a.device).cuda_stream
     elif hasattr(stream, "cuda_stream"):
         stream = stream.cuda_stream
     with torch.cuda.device(a.device):
-        check(library().wir_gemm_splitk_noalloc(gemm_h._function, _reduce_kernel._function, a.data_ptr(),
+        check(library().wir_gemm_splitk_noalloc(gemm_fn, reduce_fn, a.data_ptr(),
                                                 b.data_ptr(), out.data_ptr(), m, n, k, splits,
                                                 ctypes.c_void_p(stream)),
               "wir_gemm_splitk_noalloc")
     return out
 
 
-def gemm(a, b, out=None, variant: Optional[str] = None):
+def gemm(a, b, out=None, variant: Optional[str] = None, workspace=None):
     """``out[M, N] = a[M, K] @ b[K, N]`` in bf16 with fp32 accumulation.
 
     The variant follows ``gemm_variant``: 256x256 tiles by default, smaller
-    tiles for outputs with fewer tiles than CUs, split-K for M <= 64.
+    tiles for outputs with fewer tiles than CUs, split-K for M <= 128 and
+    long K (``workspace`` as in ``gemm_split_k``).
     """
     import torch
 
@@ -173,7 +193,7 @@ def gemm(a, b, out=None, variant: Optional[str] = None):
     if variant is None:
         variant = gemm_variant(m, n, k)
     if variant == SPLITK_GEMM_VARIANT:
-        return gemm_split_k(a, b, out=out)
+        return gemm_split_k(a, b, out=out, workspace=workspace)
     kernels.handle(variant)(A=a, B=b, N=k, C_global=out)
     return out
 

@@ -1,9 +1,10 @@
-// wir_noalloc.hip -- split-K GEMM through the C ABI with no device allocation.
+// wir_splitk.hip -- split-K GEMM through the C ABI: the host side of one
+// product (kernel arguments and the two launches) in one call.
 //
-// The allocating split-K path (warpir_amd.api.gemm_split_k) takes an fp32
-// workspace of splits * M * N partial sums from the caller or allocates one.
-// wir_gemm_splitk_noalloc runs the same two kernels -- the generated
-// gemm_128_splitk GEMM and wir_splitk_reduce -- with that workspace in
+// wir_gemm_splitk takes the fp32 workspace of splits * M * N partial sums
+// from the caller (warpir_amd.api.gemm_split_k allocates it when the caller
+// does not).  wir_gemm_splitk_noalloc runs the same two kernels -- the
+// generated split-K GEMM and wir_splitk_reduce -- with that workspace in
 // `scratch`, a file-scope device array of WIR_NOALLOC_SCRATCH_FLOATS floats
 // that every device holds from the library's first use until the process
 // ends.  Host code never passes `scratch` itself to a kernel: the name is a
@@ -64,8 +65,9 @@ struct GlobalView {
   long long sb, sd, sr;
 };
 
-// Kernel arguments of gemm_128_splitk, laid out as its emitted globals
-// struct (inputs then outputs in IR order: A, B, N, C_global).
+// Kernel arguments of the split-K GEMM variants (128x128 output tiles, four
+// wavefronts: gemm_128_splitk*), laid out as their emitted globals struct
+// (inputs then outputs in IR order: A, B, N, C_global).
 struct SplitKGemmArgs {
   GlobalView A;   // [1][splits][M][K/splits], K-slice s starts at column s*K/splits
   GlobalView B;   // [1][splits][K/splits][N]
@@ -75,7 +77,7 @@ struct SplitKGemmArgs {
 static_assert(sizeof(GlobalView) == 48, "wir::gl layout");
 static_assert(offsetof(SplitKGemmArgs, B) == 48 && offsetof(SplitKGemmArgs, N) == 96 &&
                   offsetof(SplitKGemmArgs, C) == 104 && sizeof(SplitKGemmArgs) == 152,
-              "gemm_128_splitk globals layout");
+              "split-K GEMM globals layout");
 
 // Kernel arguments of wir_splitk_reduce (splitk_reduce.hip).
 struct SplitKReduceArgs {
@@ -86,8 +88,8 @@ struct SplitKReduceArgs {
   int splits;
 };
 
-constexpr int kTile = 128;       // gemm_128_splitk output tile (rows and columns)
-constexpr int kThreads = 256;    // gemm_128_splitk workgroup size
+constexpr int kTile = 128;       // split-K GEMM output tile (rows and columns)
+constexpr int kThreads = 256;    // split-K GEMM workgroup size
 constexpr int kKStep = 64;       // K per pipeline step
 constexpr int kMaxSplits = 16;
 
@@ -100,33 +102,54 @@ int launch(hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned bx, 
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-}  // namespace
-
-extern "C" int wir_gemm_splitk_noalloc(wir_function_t gemm, wir_function_t reduce, const void* a,
-                                       const void* b, void* out, int m, int n, int k, int splits,
-                                       void* stream) {
-  if (!gemm || !reduce || !a || !b || !out) return (int)hipErrorInvalidValue;
-  if (m <= 0 || n <= 0 || k <= 0 || splits <= 0 || splits > kMaxSplits) return (int)hipErrorInvalidValue;
-  if (k % (kKStep * splits) || n % 8 || !aligned16(a) || !aligned16(b) || !aligned16(out))
-    return (int)hipErrorInvalidValue;
+// The two launches of a split-K product with its fp32 partials in `ws`
+// (splits * m * n floats); arguments already validated.
+int splitk_launch(hipFunction_t gemm, hipFunction_t reduce, const void* a, const void* b, void* out, float* ws,
+                  int m, int n, int k, int splits, void* stream) {
   const long long split_elems = (long long)m * n;
-  if ((long long)splits * split_elems > (long long)WIR_NOALLOC_SCRATCH_FLOATS) return WIR_ERROR_SCRATCH_LIMIT;
-
-  float* ws = nullptr;
-  int e = scratch_on_current_device(&ws);
-  if (e) return e;
-
   const int kc = k / splits;
   SplitKGemmArgs g;
   g.A = {a, 1, splits, m, kc, 0, kc, k};
   g.B = {b, 1, splits, kc, n, (long long)k * n, (long long)kc * n, n};
   g.N = kc;
   g.C = {ws, 1, splits, m, n, (long long)splits * split_elems, split_elems, n};
-  e = launch((hipFunction_t)gemm, (unsigned)((n + kTile - 1) / kTile), (unsigned)((m + kTile - 1) / kTile),
-             (unsigned)splits, kThreads, stream, &g, sizeof(g));
+  int e = launch(gemm, (unsigned)((n + kTile - 1) / kTile), (unsigned)((m + kTile - 1) / kTile), (unsigned)splits,
+                 kThreads, stream, &g, sizeof(g));
   if (e) return e;
-
   SplitKReduceArgs r = {ws, out, split_elems, split_elems, splits};
-  return launch((hipFunction_t)reduce, (unsigned)((split_elems / 8 + 255) / 256), 1, 1, 256, stream, &r,
-                sizeof(r));
+  return launch(reduce, (unsigned)((split_elems / 8 + 255) / 256), 1, 1, 256, stream, &r, sizeof(r));
+}
+
+int splitk_check(wir_function_t gemm, wir_function_t reduce, const void* a, const void* b, void* out, int m, int n,
+                 int k, int splits) {
+  if (!gemm || !reduce || !a || !b || !out) return (int)hipErrorInvalidValue;
+  if (m <= 0 || n <= 0 || k <= 0 || splits <= 0 || splits > kMaxSplits) return (int)hipErrorInvalidValue;
+  if (k % (kKStep * splits) || n % 8 || !aligned16(a) || !aligned16(b) || !aligned16(out))
+    return (int)hipErrorInvalidValue;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int wir_gemm_splitk(wir_function_t gemm, wir_function_t reduce, const void* a, const void* b, void* out,
+                               void* workspace, size_t workspace_floats, int m, int n, int k, int splits,
+                               void* stream) {
+  int e = splitk_check(gemm, reduce, a, b, out, m, n, k, splits);
+  if (e) return e;
+  if (!workspace || !aligned16(workspace) || (unsigned long long)splits * m * n > workspace_floats)
+    return (int)hipErrorInvalidValue;
+  return splitk_launch((hipFunction_t)gemm, (hipFunction_t)reduce, a, b, out, (float*)workspace, m, n, k, splits,
+                       stream);
+}
+
+extern "C" int wir_gemm_splitk_noalloc(wir_function_t gemm, wir_function_t reduce, const void* a,
+                                       const void* b, void* out, int m, int n, int k, int splits,
+                                       void* stream) {
+  int e = splitk_check(gemm, reduce, a, b, out, m, n, k, splits);
+  if (e) return e;
+  if ((long long)splits * m * n > (long long)WIR_NOALLOC_SCRATCH_FLOATS) return WIR_ERROR_SCRATCH_LIMIT;
+  float* ws = nullptr;
+  e = scratch_on_current_device(&ws);
+  if (e) return e;
+  return splitk_launch((hipFunction_t)gemm, (hipFunction_t)reduce, a, b, out, ws, m, n, k, splits, stream);
 }

@@ -43,10 +43,22 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
                                             lds_budget=80 * 1024),
     "gemm_128x32_k64": lambda: _gemm_mi355x(64, block_m=128, block_n=32, wave_m=32, wave_n=32,
                                             lds_budget=80 * 1024),
+    "gemm_128x32_k64_s8": lambda: _gemm_mi355x(64, block_m=128, block_n=32, wave_m=32, wave_n=32,
+                                               lds_budget=160 * 1024),
+    "gemm_128x32_k128": lambda: _gemm_mi355x(128, block_m=128, block_n=32, wave_m=32, wave_n=32,
+                                             lds_budget=160 * 1024),
     # Split-K form of the 128x128 tile: K slices along blockIdx.z, fp32 partials
     # summed by the split-K reduction (short M, long K).
     "gemm_128_splitk": lambda: _gemm_mi355x(64, block_m=128, block_n=128, wave_m=64, wave_n=64,
                                             lds_budget=80 * 1024, split_k=True),
+    "gemm_128_splitk_k128": lambda: _gemm_mi355x(128, block_m=128, block_n=128, wave_m=64, wave_n=64,
+                                                 lds_budget=160 * 1024, split_k=True),
+    "gemm_128x64_splitk": lambda: _gemm_mi355x(64, block_m=128, block_n=64, wave_m=64, wave_n=32,
+                                               lds_budget=80 * 1024, split_k=True),
+    "gemm_128_splitk_s5": lambda: _gemm_mi355x(64, block_m=128, block_n=128, wave_m=64, wave_n=64,
+                                               lds_budget=160 * 1024, split_k=True),
+    "gemm_128_splitk_k32": lambda: _gemm_mi355x(32, block_m=128, block_n=128, wave_m=64, wave_n=64,
+                                                lds_budget=160 * 1024, split_k=True, load_units=12),
     # 8 wavefronts (2 per SIMD) of 128x64 in the ping-pong form, K=32 with a 4-slot ring.
     "gemm_256_pp": lambda: _gemm_mi355x(32, wave_m=128, wave_n=64, load_units=12),
     # warp-specialised: 4 MFMA wavefronts of 128x64 plus 4 DMA-only wavefronts (2 per SIMD)

@@ -90,6 +90,7 @@ def library() -> ctypes.CDLL:
             "wir_event_record": ([vp, vp], ci),
             "wir_event_elapsed_ms": ([vp, vp, ctypes.POINTER(ctypes.c_float)], ci),
             "wir_error_string": ([ci], ctypes.c_char_p),
+            "wir_gemm_splitk": ([vp, vp, vp, vp, vp, vp, sz, ci, ci, ci, ci, vp], ci),
             "wir_gemm_splitk_noalloc": ([vp, vp, vp, vp, vp, ci, ci, ci, ci, vp], ci),
         }
         for name, (args, res) in sig.items():
