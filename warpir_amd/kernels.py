@@ -32,6 +32,10 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "gemm_ref_piped": lambda: kernel_pass(build_gemm_kernel()),
     # MI355X GEMM: 256x256 block tile, 4 wavefronts of 128x128, 3-stage LDS ring.
     "gemm_256_k32": lambda: _gemm_mi355x(32),
+    "gemm_256_k64_g4": lambda: _gemm_mi355x(64),
+    "gemm_256_k64_g16": lambda: _gemm_mi355x(64),
+    "gemm_256_k64_g32": lambda: _gemm_mi355x(64),
+    "gemm_256_k64_noxcd": lambda: _gemm_mi355x(64),
     # Same tile with a 64-deep K step: MMA twice as long per stage, 2-slot ring.
     "gemm_256_k64": lambda: _gemm_mi355x(64),
     # 128x128 block tile (4 wavefronts of 64x64): more workgroups for short M (skinny GEMM).
@@ -185,6 +189,11 @@ TARGETS: Dict[str, dict] = {
     "mha_d128_ovl": {"attn_overlap": True, "lazy_softmax": False},
     "mha_d128_pp_swapped": {"wave_groups": {"k": 1, "v": 0}},
     "mha_d128_pp2b": {"pingpong_one_barrier": False},
+    # tile orders of the 8192^3 GEMM: GROUP_M rows of tiles per group, and without the XCD remap
+    "gemm_256_k64_g4": {"group_m": 4},
+    "gemm_256_k64_g16": {"group_m": 16},
+    "gemm_256_k64_g32": {"group_m": 32},
+    "gemm_256_k64_noxcd": {"xcd_remap": False},
     # (the rotated pipeline's extra fragment registers do not fit two waves per SIMD)
     # A / B load streams split between the wave sets as the warp assigner places them (A with the
     # MFMA waves, B on the DMA waves); _all puts both on the DMA waves
