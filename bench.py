@@ -407,40 +407,55 @@ def mfma_ceiling(iters: int = 20000):
 # options): the evidence behind the default choices.
 COMPARE_GEMM = ["gemm_256_k64", "gemm_256_k32", "gemm_256_pp", "gemm_256x128", "gemm_256x128_ws_all",
                 "gemm_256x128_ws", "gemm_128_k64"]
-COMPARE_FA = ["mha_d128", "mha_d128_w4", "mha_d128_online", "mha_d128_q256", "mha_d128_ovl"]
+COMPARE_FA = ["mha_d128", "mha_d128_pp2b", "mha_d128_s5", "mha_d128_w4", "mha_d128_online", "mha_d128_q256",
+              "mha_d128_ovl"]
 COMPARE_BWD_DQ = ["mha_bwd_dq_d128", "mha_bwd_dq_d128_kv64"]
 
 
-def bench_compare(steps: int, warmup: int):
-    """Time each schedule variant at the headline shapes, one after the other (in the order of
-    COMPARE_GEMM, COMPARE_FA, then COMPARE_BWD_DQ, so a kernel trace of the run can be matched
-    to it).  The mha_fwd launches of the last FA variant leave O and LSE for the dQ kernels."""
+def bench_compare(steps: int, warmup: int, names=None):
+    """Time each schedule variant at the headline shapes, one after the other (GEMM variants,
+    then FA forward, then dQ, each group in the order given, so a kernel trace of the run can be
+    matched to it).  ``names`` picks variants (default: COMPARE_GEMM, COMPARE_FA and
+    COMPARE_BWD_DQ).  The mha_fwd launches of the last FA variant leave O and LSE for the dQ
+    kernels."""
     import torch
 
     from oracle.torch_ref import seeded_normal
     from warpir_amd import kernels
 
+    if names is None:
+        names = COMPARE_GEMM + COMPARE_FA + COMPARE_BWD_DQ
+    for name in names:
+        if name not in kernels.VARIANTS:
+            raise ValueError(f"--compare: unknown variant {name!r}")
+    gemms = [x for x in names if x.startswith("gemm_")]
+    dqs = [x for x in names if x.startswith("mha_bwd_dq_")]
+    fas = [x for x in names if x.startswith("mha_d128") and x not in dqs]
     stream = torch.cuda.current_stream().cuda_stream
     out = {}
     n = 8192
-    a = seeded_normal((n, n), 0, 0.1).cuda()
-    b = seeded_normal((n, n), 1, 0.1).cuda()
-    c = torch.empty(n, n, dtype=torch.bfloat16, device="cuda")
-    for name in COMPARE_GEMM:
+    a = seeded_normal((n, n), 0, 0.1).cuda() if gemms else None
+    b = seeded_normal((n, n), 1, 0.1).cuda() if gemms else None
+    c = torch.empty(n, n, dtype=torch.bfloat16, device="cuda") if gemms else None
+    for name in gemms:
         h = kernels.handle(name)
-        ms, _ = _time_launches(lambda: h(A=a, B=b, N=n, C_global=c), steps, warmup, stream)
+        ms, _, _ = _time_launches(lambda: h(A=a, B=b, N=n, C_global=c), steps, warmup, stream)
         lc = h.lowerer.launch_config(h.kernel, {"A": tuple(a.shape), "B": tuple(b.shape), "C_global": tuple(c.shape)})
         out[name] = {"ms": ms, "tflops": 2.0 * n ** 3 / (ms * 1e-3) / 1e12, "options": kernels.TARGETS.get(name, {}),
                      "grid": list(lc.grid), "block": lc.block[0]}
     del a, b, c
+    if not fas:
+        return out
     bsz, heads, seq, d = 16, 16, 4096, 128
     q, k, v = (seeded_normal((bsz, heads, seq, d), sd).cuda() for sd in (0, 1, 2))
     o = torch.empty_like(q)
     lse = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
     flops = 4.0 * bsz * heads * seq * seq * d
-    for name in COMPARE_FA:
+    if dqs and not fas:
+        fas = ["mha_d128"]   # the dQ kernels read the forward's O and LSE
+    for name in fas:
         h = kernels.handle(name)
-        ms, _ = _time_launches(lambda: h(Q=q, K=k, V=v, N=seq, O=o, L=lse), steps, warmup, stream)
+        ms, _, _ = _time_launches(lambda: h(Q=q, K=k, V=v, N=seq, O=o, L=lse), steps, warmup, stream)
         lc = h.lowerer.launch_config(h.kernel, {"Q": tuple(q.shape), "K": tuple(k.shape), "V": tuple(v.shape),
                                                 "O": tuple(o.shape), "L": tuple(lse.shape)})
         out[name] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "options": kernels.TARGETS.get(name, {}),
@@ -450,9 +465,10 @@ def bench_compare(steps: int, warmup: int):
     dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
     kernels.handle("mha_bwd_prep_d128")(O=o, dO=do, Dv=dvec)
     dq = torch.empty_like(q)
-    for name in COMPARE_BWD_DQ:
+    for name in dqs:
         h = kernels.handle(name)
-        ms, _ = _time_launches(lambda: h(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq), steps, warmup, stream)
+        ms, _, _ = _time_launches(lambda: h(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq), steps, warmup,
+                                  stream)
         lc = h.lowerer.launch_config(h.kernel, {"Q": tuple(q.shape), "K": tuple(k.shape), "V": tuple(v.shape),
                                                 "dO": tuple(do.shape), "L": tuple(lse.shape),
                                                 "Dv": tuple(dvec.shape), "dQ": tuple(dq.shape)})
@@ -461,7 +477,7 @@ def bench_compare(steps: int, warmup: int):
     return out
 
 
-ONLY = ["gemm", "fa", "ceiling"] + list(EXTRA)
+ONLY = ["gemm", "fa", "ceiling"] + list(EXTRA) + ["none"]   # none: only --compare / --calibrate-copy
 
 
 def main() -> int:
@@ -476,8 +492,9 @@ def main() -> int:
                     help="headline value from the median of per-launch event pairs (the reference's method) "
                          "instead of the mean over back-to-back launches")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
-    ap.add_argument("--compare", action="store_true",
-                    help="also time the schedule alternatives (COMPARE_GEMM / COMPARE_FA) at the headline shapes")
+    ap.add_argument("--compare", nargs="?", const="default", default=None, metavar="VARIANTS",
+                    help="also time schedule alternatives at the headline shapes: COMPARE_GEMM, COMPARE_FA and "
+                         "COMPARE_BWD_DQ, or the comma-separated kernels.VARIANTS names given")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (read MIB, write MIB) three times, "
                          "the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -521,7 +538,8 @@ def main() -> int:
     compare = None
     if args.compare:
         print("[bench] schedule comparison", file=sys.stderr, flush=True)
-        compare = bench_compare(max(5, args.steps // 2), max(2, args.warmup // 2))
+        picked = None if args.compare == "default" else [x.strip() for x in args.compare.split(",") if x.strip()]
+        compare = bench_compare(max(5, args.steps // 2), max(2, args.warmup // 2), picked)
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
@@ -534,7 +552,7 @@ def main() -> int:
     head = gemm or fa
     if head is None:   # a profiling run of other configurations only
         print(json.dumps({"metric": METRIC, "value": None, "partial_run": only, "other_configs": extra,
-                          "mfma_ceiling": ceiling, "device": info}))
+                          "mfma_ceiling": ceiling, "schedule_comparison": compare, "device": info}))
         return 0
     line = {
         "metric": METRIC, "value": head["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
