@@ -228,6 +228,33 @@ def test_mha_backward_repeated_launches_bitwise_stable(gpu, causal):
             assert torch.equal(t, f), (it, name)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_mha_backward_config5_shape(gpu, causal):
+    """Config 5's shape (B8 H32 S8192 D64), where the D=64 dQ kernel steps over 32-row key tiles
+    and the dK/dV kernel over 32-row query tiles: 2 of the 256 (b, h) heads against autograd, then
+    3 more launches into the same buffers that must reproduce the first bit for bit."""
+    from oracle.torch_ref import attention_bwd_ref
+    shape = (8, 32, 8192, 64)
+    announce(f"mha backward config-5 shape causal={causal} {shape}")
+    q, k, v, do = (seeded_normal(shape, sd) for sd in (70, 71, 72, 73))
+    qd, kd, vd, dod = q.cuda(), k.cuda(), v.cuda(), do.cuda()
+    o, lse = api.attention_forward(qd, kd, vd, causal=causal)
+    dq, dk, dv = api.attention_backward(qd, kd, vd, o, lse, dod, causal=causal)
+    torch.cuda.synchronize()
+    first = [t.clone() for t in (dq, dk, dv)]
+    for it in range(3):
+        for t in (dq, dk, dv):
+            t.fill_(float("nan"))
+        api.attention_backward(qd, kd, vd, o, lse, dod, dq, dk, dv, causal=causal)
+        for name, t, f in zip(("dQ", "dK", "dV"), (dq, dk, dv), first):
+            assert torch.equal(t, f), (it, name)
+    for (bi, hi) in [(0, 0), (7, 21)]:
+        rq, rk, rv = attention_bwd_ref(q[bi, hi], k[bi, hi], v[bi, hi], do[bi, hi], causal=causal)
+        for name, got, ref in (("dQ", first[0], rq), ("dK", first[1], rk), ("dV", first[2], rv)):
+            err = rel_err(got[bi, hi].cpu().float(), ref)
+            assert err <= TOL, (name, bi, hi, err)
+
+
 def test_dq_schedule_alternative_agrees(gpu):
     """The previous dQ schedule (64-row key tiles), kept for the schedule comparison, against the
     default (32-row key tiles) on the same forward outputs."""

@@ -273,6 +273,20 @@ def test_gemm_variant_selection():
         assert v in kernels.VARIANTS
 
 
+def test_dkdv_cost_model_follows_its_query_tile():
+    """The dK/dV kernel's kernel_pass prices its real loop tile (DKDV_BLOCK_Q[d] query rows
+    against the resident 128-row key tile): at D=64, two 32-row Q / dO slots plus the LSE and Dv
+    vectors, 17 KiB of LDS."""
+    from warpir_amd.kernels import DKDV_BLOCK_Q
+    assert DKDV_BLOCK_Q == {128: 64, 64: 32}
+    low = kernels.lowerer("mha_bwd_dkdv_d64")
+    low.lower(kernels.kernel("mha_bwd_dkdv_d64"))
+    off = low.lds_off
+    assert [low.tile_type_of(k).rows for k in ("q_bufs", "do_bufs", "l_bufs", "dv_bufs")] == [32] * 4
+    assert off["do_bufs"] - off["q_bufs"] == off["l_bufs"] - off["do_bufs"] == 2 * 32 * 64 * 2   # two slots
+    assert low.lds_total == 17408   # + two 256-byte-aligned slots of each fp32 vector
+
+
 def test_split_k_count_and_ir():
     from warpir_amd import api
     assert api.splitk_count(128, 8192, 8192) == 4        # 64 tiles x 4 slices = 256 workgroups

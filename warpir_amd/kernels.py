@@ -169,7 +169,8 @@ def _bwd(kernel: Kernel, d: int) -> Kernel:
         # two-slot ring of 32-row K and V tiles (32 KiB at D=128)
         return kernel_pass(kernel, cost_model=gfx950_attention_cost_model(128, DQ_BLOCK_KV, d,
                                                                           lds_budget=32 * 1024))
-    return kernel_pass(kernel, cost_model=gfx950_attention_cost_model(128, 64, d))
+    # dK / dV: the 128-row key tile stays resident, query tiles of DKDV_BLOCK_Q[d] rows stream
+    return kernel_pass(kernel, cost_model=gfx950_attention_cost_model(128, DKDV_BLOCK_Q[d], d))
 
 
 def _bwd_dq(d: int, causal: bool) -> Kernel:
