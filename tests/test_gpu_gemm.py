@@ -73,7 +73,9 @@ def test_identity_returns_a(gpu):
 
 
 @pytest.mark.parametrize("m,n,k,splits", [(128, 8192, 8192, None), (128, 1024, 2048, 4), (64, 512, 1024, 2),
-                                          (300, 520, 2048, 4), (128, 256, 4096, 8)])
+                                          (300, 520, 2048, 4), (128, 256, 4096, 8),
+                                          # K slices that are not a whole number of the kernel's 128-deep steps
+                                          (96, 384, 384, 2), (128, 256, 8256, 3)])
 def test_split_k_gemm(gpu, m, n, k, splits):
     """Split-K form (K slices on blockIdx.z, fp32 partials, HIP reduction) vs the fp32 oracle."""
     from warpir_amd import api
@@ -145,3 +147,19 @@ def test_skinny_benchmark_kernel_at_its_exact_shape(gpu):
     err = rel_err(c[:, cols], ref)
     assert err <= TOL, err
     assert not torch.isnan(c.float()).any()
+
+
+def test_split_k_kernel_variants_agree(gpu):
+    """The 64-deep-step split-K kernel against the default 128-deep one on the same slices: both
+    accumulate every output's k in order, 16 per MFMA, so the results are bitwise equal."""
+    from warpir_amd import api
+
+    m, n, k, splits = 128, 1024, 4096, 4
+    announce(f"split-K variants {m}x{n}x{k} splits={splits}")
+    a = seeded_normal((m, k), 90, 0.1).cuda()
+    b = seeded_normal((k, n), 91, 0.1).cuda()
+    c64 = api.gemm_split_k(a, b, splits=splits, variant="gemm_128_splitk")
+    c128 = api.gemm_split_k(a, b, splits=splits, variant="gemm_128_splitk_k128")
+    torch.cuda.synchronize()
+    assert torch.equal(c64, c128)
+    assert rel_err(c128.cpu(), gemm_ref(a.cpu(), b.cpu())) <= TOL
