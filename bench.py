@@ -22,6 +22,7 @@ Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--compa
 from __future__ import annotations
 
 import argparse
+import collections
 import json
 import math
 import os
@@ -412,12 +413,14 @@ COMPARE_FA = ["mha_d128", "mha_d128_pp2b", "mha_d128_s5", "mha_d128_w4", "mha_d1
 COMPARE_BWD_DQ = ["mha_bwd_dq_d128", "mha_bwd_dq_d128_kv64"]
 
 
-def bench_compare(steps: int, warmup: int, names=None):
+def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
     """Time each schedule variant at the headline shapes, one after the other (GEMM variants,
     then FA forward, then dQ, each group in the order given, so a kernel trace of the run can be
     matched to it).  ``names`` picks variants (default: COMPARE_GEMM, COMPARE_FA and
-    COMPARE_BWD_DQ).  The mha_fwd launches of the last FA variant leave O and LSE for the dQ
-    kernels."""
+    COMPARE_BWD_DQ).  With ``reps`` > 1 each group is timed ``reps`` times in rotation and
+    ``ms`` is the median (the clock drifts over a sequential run, so rotation compares
+    variants under the same conditions); ``ms_reps`` holds every repetition.  The mha_fwd
+    launches of the last FA variant leave O and LSE for the dQ kernels."""
     import torch
 
     from oracle.torch_ref import seeded_normal
@@ -437,12 +440,17 @@ def bench_compare(steps: int, warmup: int, names=None):
     a = seeded_normal((n, n), 0, 0.1).cuda() if gemms else None
     b = seeded_normal((n, n), 1, 0.1).cuda() if gemms else None
     c = torch.empty(n, n, dtype=torch.bfloat16, device="cuda") if gemms else None
+    timed = collections.defaultdict(list)
+    for _ in range(reps):
+        for name in gemms:
+            h = kernels.handle(name)
+            timed[name].append(_time_launches(lambda: h(A=a, B=b, N=n, C_global=c), steps, warmup, stream)[0])
     for name in gemms:
         h = kernels.handle(name)
-        ms, _, _ = _time_launches(lambda: h(A=a, B=b, N=n, C_global=c), steps, warmup, stream)
+        ms = statistics.median(timed[name])
         lc = h.lowerer.launch_config(h.kernel, {"A": tuple(a.shape), "B": tuple(b.shape), "C_global": tuple(c.shape)})
-        out[name] = {"ms": ms, "tflops": 2.0 * n ** 3 / (ms * 1e-3) / 1e12, "options": kernels.TARGETS.get(name, {}),
-                     "grid": list(lc.grid), "block": lc.block[0]}
+        out[name] = {"ms": ms, "ms_reps": timed[name], "tflops": 2.0 * n ** 3 / (ms * 1e-3) / 1e12,
+                     "options": kernels.TARGETS.get(name, {}), "grid": list(lc.grid), "block": lc.block[0]}
     del a, b, c
     if not fas:
         return out
@@ -453,27 +461,35 @@ def bench_compare(steps: int, warmup: int, names=None):
     flops = 4.0 * bsz * heads * seq * seq * d
     if dqs and not fas:
         fas = ["mha_d128"]   # the dQ kernels read the forward's O and LSE
+    for _ in range(reps):
+        for name in fas:
+            h = kernels.handle(name)
+            timed[name].append(_time_launches(lambda: h(Q=q, K=k, V=v, N=seq, O=o, L=lse), steps, warmup, stream)[0])
     for name in fas:
         h = kernels.handle(name)
-        ms, _, _ = _time_launches(lambda: h(Q=q, K=k, V=v, N=seq, O=o, L=lse), steps, warmup, stream)
+        ms = statistics.median(timed[name])
         lc = h.lowerer.launch_config(h.kernel, {"Q": tuple(q.shape), "K": tuple(k.shape), "V": tuple(v.shape),
                                                 "O": tuple(o.shape), "L": tuple(lse.shape)})
-        out[name] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "options": kernels.TARGETS.get(name, {}),
-                     "grid": list(lc.grid), "block": lc.block[0]}
+        out[name] = {"ms": ms, "ms_reps": timed[name], "tflops": flops / (ms * 1e-3) / 1e12,
+                     "options": kernels.TARGETS.get(name, {}), "grid": list(lc.grid), "block": lc.block[0]}
     # backward dQ kernel: 3 of the S x S x D products, over the forward's O and LSE
     do = seeded_normal((bsz, heads, seq, d), 3).cuda()
     dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
     kernels.handle("mha_bwd_prep_d128")(O=o, dO=do, Dv=dvec)
     dq = torch.empty_like(q)
+    for _ in range(reps):
+        for name in dqs:
+            h = kernels.handle(name)
+            timed[name].append(_time_launches(lambda: h(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq), steps,
+                                              warmup, stream)[0])
     for name in dqs:
         h = kernels.handle(name)
-        ms, _, _ = _time_launches(lambda: h(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq), steps, warmup,
-                                  stream)
+        ms = statistics.median(timed[name])
         lc = h.lowerer.launch_config(h.kernel, {"Q": tuple(q.shape), "K": tuple(k.shape), "V": tuple(v.shape),
                                                 "dO": tuple(do.shape), "L": tuple(lse.shape),
                                                 "Dv": tuple(dvec.shape), "dQ": tuple(dq.shape)})
-        out[name] = {"ms": ms, "tflops": 1.5 * flops / (ms * 1e-3) / 1e12, "options": kernels.TARGETS.get(name, {}),
-                     "grid": list(lc.grid), "block": lc.block[0]}
+        out[name] = {"ms": ms, "ms_reps": timed[name], "tflops": 1.5 * flops / (ms * 1e-3) / 1e12,
+                     "options": kernels.TARGETS.get(name, {}), "grid": list(lc.grid), "block": lc.block[0]}
     return out
 
 
@@ -495,6 +511,8 @@ def main() -> int:
     ap.add_argument("--compare", nargs="?", const="default", default=None, metavar="VARIANTS",
                     help="also time schedule alternatives at the headline shapes: COMPARE_GEMM, COMPARE_FA and "
                          "COMPARE_BWD_DQ, or the comma-separated kernels.VARIANTS names given")
+    ap.add_argument("--reps", type=int, default=1,
+                    help="--compare: time each group this many times in rotation and report the median")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (read MIB, write MIB) three times, "
                          "the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -539,7 +557,7 @@ def main() -> int:
     if args.compare:
         print("[bench] schedule comparison", file=sys.stderr, flush=True)
         picked = None if args.compare == "default" else [x.strip() for x in args.compare.split(",") if x.strip()]
-        compare = bench_compare(max(5, args.steps // 2), max(2, args.warmup // 2), picked)
+        compare = bench_compare(max(5, args.steps // 2), max(2, args.warmup // 2), picked, max(1, args.reps))
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
