@@ -1,4 +1,5 @@
-"""TEST INFRASTRUCTURE -- numerical oracles (fp32 on CPU), never used by the product.
+"""TEST INFRASTRUCTURE -- numerical oracles (fp32; on the CPU, or on the GPU where a test
+evaluates them at full size there with torch's own fp32 matmuls), never used by the product.
 
 Follows the reference's checks:
 * GEMM: ``torch.mm(A.float(), B.float())`` (``tests/test_modal_gpu.py:115``).
@@ -33,7 +34,7 @@ def gemm_ref(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 def attention_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
                   causal: bool = False, heads: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Naive fp32 attention over ``[..., S, D]``; returns ``(O, LSE)``.
+    """Naive fp32 attention over ``[..., S, D]`` on the inputs' device; returns ``(O, LSE)``.
 
     ``LSE[..., s] = logsumexp_j(q_s . k_j * scale)`` (natural log).  With
     ``heads`` set, only the first ``heads`` of the flattened (batch, head)
@@ -51,7 +52,7 @@ def attention_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Opti
         s = (qf[h].float() @ kf[h].float().t()) * scale
         if causal:
             sq, sk = s.shape
-            mask = torch.ones(sq, sk, dtype=torch.bool).tril_(diagonal=sk - sq)
+            mask = torch.ones(sq, sk, dtype=torch.bool, device=s.device).tril_(diagonal=sk - sq)
             s = s.masked_fill(~mask, float("-inf"))
         lses.append(torch.logsumexp(s, dim=-1))
         outs.append(torch.softmax(s, dim=-1) @ vf[h].float())
@@ -65,8 +66,8 @@ def attention_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Opti
 
 def attention_bwd_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, do: torch.Tensor,
                       scale: Optional[float] = None, causal: bool = False):
-    """``(dQ, dK, dV)`` of ``sum(softmax(q k^T * scale) v * do)`` in fp32 on CPU,
-    by autograd over ``[..., S, D]`` inputs (per leading index, to bound memory)."""
+    """``(dQ, dK, dV)`` of ``sum(softmax(q k^T * scale) v * do)`` in fp32 on the inputs'
+    device, by autograd over ``[..., S, D]`` inputs (per leading index, to bound memory)."""
     scale = scale if scale is not None else 1.0 / math.sqrt(q.shape[-1])
     lead = q.shape[:-2]
     qf, kf, vf, dof = (t.float().reshape(-1, *t.shape[-2:]) for t in (q, k, v, do))
@@ -76,7 +77,7 @@ def attention_bwd_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, do: tor
         s = (qn @ kn.t()) * scale
         if causal:
             rows, cols = s.shape
-            s = s.masked_fill(torch.ones(rows, cols, dtype=torch.bool).triu(1), float("-inf"))
+            s = s.masked_fill(torch.ones(rows, cols, dtype=torch.bool, device=s.device).triu(1), float("-inf"))
         o = torch.softmax(s, dim=-1) @ vn
         o.backward(dof[n])
         for acc, t in zip(outs, (qn, kn, vn)):
