@@ -431,9 +431,15 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
     for name in names:
         if name not in kernels.VARIANTS:
             raise ValueError(f"--compare: unknown variant {name!r}")
-    gemms = [x for x in names if x.startswith("gemm_")]
-    dqs = [x for x in names if x.startswith("mha_bwd_dq_")]
-    fas = [x for x in names if x.startswith("mha_d128") and x not in dqs]
+    # the shapes timed here: GEMM 8192^3 (not the split-K kernels, whose C is fp32 partials),
+    # FA forward and dQ at D=128 without masking or grouped heads
+    gemms = [x for x in names if x.startswith("gemm_") and "splitk" not in x]
+    dqs = [x for x in names if x.startswith("mha_bwd_dq_d128") and not x.endswith(("_causal", "_gqa"))]
+    fas = [x for x in names if x.startswith("mha_d128") and "causal" not in x and "gqa" not in x]
+    untimed = [x for x in names if x not in gemms + dqs + fas]
+    if untimed:
+        raise ValueError(f"--compare times GEMM 8192^3, FA forward and dQ at the config-4 shape; "
+                         f"not {', '.join(untimed)}")
     stream = torch.cuda.current_stream().cuda_stream
     out = {}
     n = 8192
@@ -452,6 +458,8 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
         out[name] = {"ms": ms, "ms_reps": timed[name], "tflops": 2.0 * n ** 3 / (ms * 1e-3) / 1e12,
                      "options": kernels.TARGETS.get(name, {}), "grid": list(lc.grid), "block": lc.block[0]}
     del a, b, c
+    if dqs and not fas:
+        fas = ["mha_d128"]   # the dQ kernels read the forward's O and LSE
     if not fas:
         return out
     bsz, heads, seq, d = 16, 16, 4096, 128
@@ -459,8 +467,6 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
     o = torch.empty_like(q)
     lse = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
     flops = 4.0 * bsz * heads * seq * seq * d
-    if dqs and not fas:
-        fas = ["mha_d128"]   # the dQ kernels read the forward's O and LSE
     for _ in range(reps):
         for name in fas:
             h = kernels.handle(name)
