@@ -32,7 +32,8 @@ def test_reference_attention_ir(gpu, n):
 
 
 @pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp_swapped", "mha_d128_w4",
-                                     "mha_d128_online", "mha_d128_ovl", "mha_d128_s5", "mha_d128_pp2b"])
+                                     "mha_d128_online", "mha_d128_ovl", "mha_d128_s5", "mha_d128_pp2b",
+                                     "mha_d128_fold"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 1, 64)])
 def test_mha_d128(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")
@@ -67,7 +68,7 @@ def test_mha_d128_causal(gpu, b, h, s):
 
 
 @pytest.mark.parametrize("variant", ["mha_d64_causal", "mha_d64_causal_ssa", "mha_d64_causal_online", "mha_d64_causal_ovl",
-                                     "mha_d64_causal_pp"])
+                                     "mha_d64_causal_pp", "mha_d64_causal_fold"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 2, 512), (1, 2, 1024), (1, 1, 192)])
 def test_mha_d64_causal(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")

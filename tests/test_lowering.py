@@ -165,6 +165,39 @@ def test_attention_pingpong_one_barrier_per_iteration():
     assert "if (wir_grp == 1) wir::wait_vm_barrier" not in pp2 and "wir_grp == 0 ? 1 : 0" in pp2
 
 
+def test_lazy_softmax_folds_scale_into_q_and_max_into_the_score_mfmas():
+    """``fold_softmax_scale`` (opt-in): with the lazy softmax on hoisted Q, the fused loop scales
+    the fragments once, declares the score bias, starts each QK MMA with the bias MFMA and calls
+    the _b softmax halves (no fma per score).  The ping-pong kernel's plain loop for unaligned
+    tensors keeps the unfolded math; the defaults and the exact online softmax are not folded."""
+    from warpir_amd.lowering.cdna4 import CDNA4Target
+
+    def body(src):
+        return src[src.rindex('extern "C" __global__'):]
+
+    fold = CDNA4Target(fold_softmax_scale=True)
+    for name in ("mha_d128", "mha_d64_causal", "mha_d128_w4", "mha_d64_causal_pp"):
+        b = body(CDNA4Lowerer(fold).lower(kernels.kernel(name)))
+        assert b.count("wir::scale_frags(hf_q_shared, ") == 1, name
+        assert b.count("wir_sb.init();") == 1, name
+        assert "wir::lazy_softmax_fast(" not in b and "wir::lazy_softmax_exact(" not in b, name
+        assert b.count("wir::lazy_softmax_fast_b(") == 1 and b.count("wir::lazy_softmax_exact_b(") == 2, name
+        assert b.count("wir::mma_ABt_frags_bias<") == 2, name   # the peeled first tile and the loop
+        # the scale is applied before any folded MMA reads the fragments
+        assert b.index("wir::scale_frags(") < b.index("wir::mma_ABt_frags_bias<"), name
+    pp = body(CDNA4Lowerer(fold).lower(kernels.kernel("mha_d128")))
+    plain, aligned = pp.split("} else {", 1)
+    assert "wir::mma_ABt_frags<" in plain and "scale_frags" not in plain and "wir_sb" not in plain
+    assert "wir::mma_ABt_frags<" not in aligned.split("ring buffers dead")[0]
+    for name in ("mha_d128_fold", "mha_d64_causal_fold"):
+        assert kernels.TARGETS[name] == {"fold_softmax_scale": True}
+        assert "wir::mma_ABt_frags_bias<" in body(kernels.lowerer(name).lower(kernels.kernel(name)))
+    default = body(kernels.lowerer("mha_d128").lower(kernels.kernel("mha_d128")))
+    assert "scale_frags" not in default and "wir::lazy_softmax_fast(" in default and "_b(" not in default
+    online = body(CDNA4Lowerer(fold).lower(kernels.kernel("mha_d128_online")))
+    assert "scale_frags" not in online and "mma_ABt_frags_bias" not in online
+
+
 def test_warp_specialized_gemm_form():
     k = kernels.kernel("gemm_256x128_ws")
     low = kernels.lowerer("gemm_256x128_ws")

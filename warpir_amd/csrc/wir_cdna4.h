@@ -1260,6 +1260,201 @@ __device__ __forceinline__ void lazy_softmax(const RTile<MS, R, C>& s, RVec<MS, 
   lazy_softmax_exact(s, m, l, o, pb, c, slack);
 }
 
+// ---------------------------------------------------------------------------
+// Lazy softmax with the scale folded into Q and the running max into the
+// score MFMAs.  The hoisted Q fragments are scaled by c once (bf16 of c*q),
+// and every column block of S = Q K^T starts with one extra MFMA whose
+// operands are (1, 1, 0...) on the key side and (-b_hi, -b_lo, 0...) on the
+// query side, b = the running max in scaled units split into two bf16 words
+// (b_hi = bf16(b), b_lo = bf16(b - b_hi), exact to ~2^-16 relative).  The
+// MFMAs then deliver s = c*S - b directly, and the speculative half is one
+// exp2, one add and half a bf16 pack per score, without the fma.  Only
+// lanes 0-31 carry operand values: k = 8*(lane/32) + j, so the bias sits in
+// k = 0, 1.
+template <int RB>
+struct ScoreBias {
+  float b[RB];       // the bias in the MFMAs, c * running max (0 while the max is -inf)
+  bf16x8 q[RB];      // query-side operand per row block
+  bf16x8 k;          // key-side operand (the same for every block)
+  __device__ __forceinline__ static bf16x8 query_operand(float b) {
+    bf16x8 v = {};
+    const bf16 hi = (bf16)b;
+    const bf16 lo = (bf16)(b - (float)hi);
+    if (lane_id() < 32) {
+      v[0] = -hi;
+      v[1] = -lo;
+    }
+    return v;
+  }
+  __device__ __forceinline__ void init() {
+    k = bf16x8{};
+    if (lane_id() < 32) k[0] = k[1] = (bf16)1.0f;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      b[rb] = 0.f;
+      q[rb] = query_operand(0.f);
+    }
+  }
+};
+
+// q *= c in place, bf16 -> fp32 -> bf16 (the scale folded into Q).
+template <int MS, int RB, int KS>
+__device__ __forceinline__ void scale_frags(RowFrags<MS, RB, KS>& fr, float c) {
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) fr.f[rb][ks][j] = (bf16)((float)fr.f[rb][ks][j] * c);
+}
+
+// mma_ABt_frags with every accumulator started by the bias MFMA: acc = a b^T - bias.
+template <int MS, int R, int C, class TB, int KS>
+__device__ __forceinline__ void mma_ABt_frags_bias(RTile<MS, R, C>& acc, const RowFrags<MS, R / MS, KS>& a,
+                                                   const ScoreBias<R / MS>& sb, char* b_base, int b_row0) {
+  static_assert(MS == 32, "the bias operands follow the 32x32x16 lane layout");
+  constexpr int CB = RTile<MS, R, C>::CB, RB = RTile<MS, R, C>::RB;
+  constexpr int LOOK = KS < 2 ? KS : 2;
+  bf16x8 ring[LOOK + 1][CB];
+  __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+  for (int p = 0; p < LOOK; ++p)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) ring[p][cb] = row_operand<TB, MS>(b_base, b_row0 + cb * MS, p);
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc.f[cb][rb] = MF<MS>::mma(sb.k, sb.q[rb], typename MF<MS>::cvec{});
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (ks + LOOK < KS) {
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+        ring[(ks + LOOK) % (LOOK + 1)][cb] = row_operand<TB, MS>(b_base, b_row0 + cb * MS, ks + LOOK);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        acc.f[cb][rb] = MF<MS>::mma(ring[ks % (LOOK + 1)][cb], a.f[rb][ks], acc.f[cb][rb]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __builtin_amdgcn_s_setprio(0);
+}
+
+// lazy_softmax_fast on biased scores s = c*S - b: valid while b is the scaled
+// running max, i.e. after the step that first set it (lazy_softmax_exact_b).
+// `guard` = 2^(slack*c).
+template <int MS, int R, int C>
+__device__ __forceinline__ bool lazy_softmax_fast_b(const RTile<MS, R, C>& s, RVec<MS, R>& l,
+                                                    BTile<MS, R, C>& pb, float guard) {
+  constexpr int RB = R / MS, CB = C / MS, G = BTile<MS, R, C>::G;
+  float part[RB][4], sum[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part[rb][j] = 0.f;
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        bf16x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = __builtin_amdgcn_exp2f(s.f[cb][rb][4 * g + j]);
+          part[rb][j] += e;
+          v[j] = (bf16)e;
+        }
+        pb.f[cb][rb][g] = v;
+      }
+  bool ok = true;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    sum[rb] = (part[rb][0] + part[rb][1]) + (part[rb][2] + part[rb][3]);
+    ok = ok && (sum[rb] <= guard);  // false for inf and NaN
+  }
+  if (__builtin_amdgcn_ballot_w64(!ok) != 0) return false;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) l.v[rb] = lane_group_reduce<MS>(sum[rb], OpAdd()) + l.v[rb];
+  return true;
+}
+
+// lazy_softmax_exact on biased scores s = c*S - b.  m stays in unscaled units
+// (the IR's running max); the scaled max is sb.b once m is finite.  With
+// cand = max(s) + b: the max moves to cand when cand > c*m + c*slack, then
+// p = exp2(s - (m'c - b)), corr = exp2(c*m - m'c), l' = rowsum(p) + l*corr,
+// o' = o*corr, and the bias becomes m'c.
+template <int MS, int R, int C, int DO>
+__device__ __forceinline__ void lazy_softmax_exact_b(const RTile<MS, R, C>& s, RVec<MS, R>& m, RVec<MS, R>& l,
+                                                     RTile<MS, R, DO>& o, BTile<MS, R, C>& pb, float c,
+                                                     float slack, ScoreBias<R / MS>& sb) {
+  constexpr int RB = R / MS, CB = C / MS, G = BTile<MS, R, C>::G;
+  float corr[RB], delta[RB], sum[RB], part[RB][4];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    float x = s.f[0][rb][0];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int i = (cb == 0 ? 1 : 0); i < MF<MS>::CREGS; ++i) x = __builtin_fmaxf(x, s.f[cb][rb][i]);
+    const float cand = lane_group_reduce<MS>(x, OpMax()) + sb.b[rb];
+    const float old = m.v[rb] == -__builtin_inff() ? -__builtin_inff() : sb.b[rb];
+    const bool take = cand > old + slack * c;
+    const float mn = take ? cand : old;
+    corr[rb] = __builtin_amdgcn_exp2f(old - mn);
+    delta[rb] = mn - sb.b[rb];
+    if (take) {
+      m.v[rb] = cand / c;
+      sb.b[rb] = cand;
+      sb.q[rb] = ScoreBias<RB>::query_operand(cand);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part[rb][j] = 0.f;
+  }
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        bf16x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = __builtin_amdgcn_exp2f(s.f[cb][rb][4 * g + j] - delta[rb]);
+          part[rb][j] += e;
+          v[j] = (bf16)e;
+        }
+        pb.f[cb][rb][g] = v;
+      }
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    sum[rb] = (part[rb][0] + part[rb][1]) + (part[rb][2] + part[rb][3]);
+    l.v[rb] = lane_group_reduce<MS>(sum[rb], OpAdd()) + l.v[rb] * corr[rb];
+  }
+#pragma unroll
+  for (int cb = 0; cb < o.CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < MF<MS>::CREGS; ++i) o.f[cb][rb][i] *= corr[rb];
+}
+
+template <int MS, int R, int C, int DO>
+__device__ __forceinline__ void lazy_softmax_b(const RTile<MS, R, C>& s, RVec<MS, R>& m, RVec<MS, R>& l,
+                                               RTile<MS, R, DO>& o, BTile<MS, R, C>& pb, float c, float slack,
+                                               ScoreBias<R / MS>& sb) {
+  // rows whose max is still -inf have no bias yet: the exact half sets it
+  bool fresh = false;
+#pragma unroll
+  for (int rb = 0; rb < R / MS; ++rb) fresh = fresh || m.v[rb] == -__builtin_inff();
+  if (__builtin_amdgcn_ballot_w64(fresh) == 0 && lazy_softmax_fast_b(s, l, pb, __builtin_amdgcn_exp2f(slack * c)))
+    return;
+  lazy_softmax_exact_b(s, m, l, o, pb, c, slack, sb);
+}
+
 // Lower-triangular mask: keep (row, col) when col_g <= row_g with
 // row_g = row_tile*BR + row0 + r and col_g = col_tile*BC + c.
 template <bool TRANSPOSED, int MS, int R, int C>

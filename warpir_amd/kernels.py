@@ -81,6 +81,10 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # speculatively: no row max, no rescale unless a tile rises above the slack).
     "mha_d128": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
                              rescale_slack=LAZY_SLACK),
+    # the same with the softmax scale folded into Q and the running max into the score MFMAs
+    # (CDNA4Target.fold_softmax_scale: no fma per score, a second bf16 rounding of Q)
+    "mha_d128_fold": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
+                                    rescale_slack=LAZY_SLACK),
     # the same with a barrier at the end of every phase (the groups in lock-step)
     "mha_d128_pp2b": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
                                   rescale_slack=LAZY_SLACK),
@@ -102,6 +106,8 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # ring, the lazy-max softmax; and the same with the reference IR's exact online softmax.
     "mha_d64_causal": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=LAZY_SLACK),
     "mha_d64_causal_online": lambda: _mha(64, 128, 64, 32, causal=True),
+    # the config-5 kernel with the folded softmax scale and running max
+    "mha_d64_causal_fold": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=LAZY_SLACK),
     "mha_d128_causal": lambda: _mha(128, 128, 64, 32, causal=True),
     "mha_d64": lambda: _mha(64, 128, 64, 32, causal=False),
     # Eight wavefronts in ping-pong (256 query rows, 4-slot K/V rings) with the lazy-max softmax.
@@ -190,6 +196,8 @@ TARGETS: Dict[str, dict] = {
     "mha_d128_ovl": {"attn_overlap": True, "lazy_softmax": False},
     "mha_d128_pp_swapped": {"wave_groups": {"k": 1, "v": 0}},
     "mha_d128_pp2b": {"pingpong_one_barrier": False},
+    "mha_d128_fold": {"fold_softmax_scale": True},
+    "mha_d64_causal_fold": {"fold_softmax_scale": True},
     # tile orders of the 8192^3 GEMM: GROUP_M rows of tiles per group, and without the XCD remap
     "gemm_256_k64_g4": {"group_m": 4},
     "gemm_256_k64_g16": {"group_m": 16},

@@ -115,6 +115,14 @@ class CDNA4Target:
     # one per phase: group A passes it after its V phase, group B after its
     # M phase, so the two groups' phases interleave without lock-step.
     pingpong_one_barrier: bool = True
+    # With the lazy softmax on scores from hoisted Q fragments: the scale c is
+    # folded into those fragments (bf16 of c*q, once per program) and the
+    # running max into the score MFMAs (one extra MFMA per column block
+    # subtracts it), so the step needs no fma per score (wir::ScoreBias,
+    # wir::lazy_softmax_fast_b / lazy_softmax_exact_b).  Off by default: the
+    # second bf16 rounding of Q makes the score error grow with the logits'
+    # magnitude (O error 1.3e-2 at LSE ~47, against 3.6e-3 unfolded).
+    fold_softmax_scale: bool = False
     # Warp specialisation for ring-pipelined MMA loops: the workgroup gets a
     # second set of wavefronts (waves NW..2NW-1) that only issue the LDS-DMA
     # loads, while waves 0..NW-1 only read LDS and issue MFMAs.  Both sets pass
@@ -177,6 +185,8 @@ class CDNA4Lowerer:
             for loop in _walk(kernel.body):
                 if isinstance(loop, ForOp):
                     self._match_lazy_softmax(loop.body)
+            if self.target.fold_softmax_scale:
+                self._plan_score_folds(kernel)
         body: List[str] = []
         self._emit_ops(kernel.body, body, 1)
         return self._assemble(kernel, body)
@@ -299,6 +309,8 @@ class CDNA4Lowerer:
         self._softmax_fused: Dict[int, object] = {}  # id(op) -> fused lazy-softmax plan, or "skip"
         self._no_fusion = False                      # emit the fused groups' ops one by one
         self._lazy_exact_only = False                # fused groups emit only the exact half
+        self._score_folds: Dict[int, dict] = {}      # id(QK MMA) -> fold of its lazy-softmax group
+        self._fold_live = False                      # inside a fused loop whose ScoreBias is declared
 
     def _build_aliases(self, ops) -> None:
         """iter_arg init / loop results / yielded values -> block arg (``lowering.py:87-100``)."""
@@ -658,10 +670,73 @@ class CDNA4Lowerer:
             if any(id(o) not in ids and any(v.name in outputs for v in _op_values(o)) for o in ops[first:last + 1]):
                 continue
             plan = dict(s=s_v, m_in=m_v, m_out=lz.result, l_in=norm, l_out=rs.result, o_in=mr.tile,
-                        o_out=mr.result, p=cv.result, c=c, slack=lz.slack)
+                        o_out=mr.result, p=cv.result, c=c, slack=lz.slack, ids=ids)
             for g in group:
                 self._softmax_fused[id(g)] = "skip"
             self._softmax_fused[id(ops[first])] = plan
+
+    def _plan_score_folds(self, kernel: Kernel) -> None:
+        """Lazy-softmax groups whose scores can come out of the MFMAs already
+        scaled and shifted (``CDNA4Target.fold_softmax_scale``): the group's
+        score tile is S = Q K^T (or its causal mask) from a QK MMA whose Q is
+        a hoisted register fragment read by that MMA alone, and the raw and
+        masked scores are read by nothing outside the group.  Folding
+        changes what those values hold (c*S - c*m instead of S), so every
+        reader must be one of these ops."""
+        if self.geo.ms != 32:
+            return
+        ops = list(_walk(kernel.body))
+        prod = {self.resolve(o.result.name): o for o in ops if isinstance(getattr(o, "result", None), Value)}
+        uses: Dict[str, List[Op]] = {}
+        for o in ops:
+            for v in _op_values(o):
+                if v is not getattr(o, "result", None):
+                    uses.setdefault(self.resolve(v.name), []).append(o)
+        for plan in [p for p in self._softmax_fused.values() if isinstance(p, dict)]:
+            src = prod.get(self.resolve(plan["s"].name))
+            mask = None
+            if isinstance(src, CausalMaskOp):
+                mask, src = src, prod.get(self.resolve(src.tile.name))
+            if not isinstance(src, MMAOp) or not src.transpose_b:
+                continue
+            q = self.resolve(src.a.name)
+            if q not in self._register_tiles and q not in self._pending_hoist:
+                continue
+            if [id(u) for u in uses.get(q, []) if not isinstance(u, (WaitOp, WaitBufOp))] != [id(src)]:
+                continue
+            raw_readers = {id(mask)} if mask is not None else plan["ids"]
+            if any(id(u) not in raw_readers for u in uses.get(self.resolve(src.result.name), [])):
+                continue
+            if mask is not None and any(id(u) not in plan["ids"]
+                                        for u in uses.get(self.resolve(mask.result.name), [])):
+                continue
+            plan["fold"] = True
+            self._score_folds[id(src)] = dict(q=q, c=plan["c"], rb=src.result.type.rows // self.geo.ms)
+
+    def _fold_preamble(self, ops, out: List[str], depth: int) -> bool:
+        """At the top of a fused lazy-softmax loop: scale the hoisted Q
+        fragments of its folded QK MMA by c and declare the score bias.
+        Returns whether the loop runs folded (at most one fold per loop)."""
+        folds = [self._score_folds[id(o)] for o in _walk(ops) if id(o) in self._score_folds]
+        if len(folds) != 1 or folds[0]["q"] not in self._hoisted:
+            return False
+        f = folds[0]
+        pad = "  " * depth
+        out.append(f"{pad}wir::scale_frags({self._hoisted[f['q']][0]}, {_flt(f['c'])});"
+                   f"  // softmax scale folded into Q")
+        out.append(f"{pad}wir::ScoreBias<{f['rb']}> wir_sb;   // running max folded into the score MFMAs")
+        out.append(f"{pad}wir_sb.init();")
+        self._fold_live = True
+        return True
+
+    def _fast_call(self, fz) -> str:
+        """The speculative half of a fused group, as a C++ condition."""
+        if self._fold_live and fz.get("fold"):
+            guard = 2.0 ** (float(fz["slack"]) * float(fz["c"]))
+            return (f"wir::lazy_softmax_fast_b({self._var(fz['s'])}, {self._var(fz['l_in'])}, "
+                    f"{self._var(fz['p'])}, {_flt(guard)})")
+        return (f"wir::lazy_softmax_fast({self._var(fz['s'])}, {self._var(fz['m_in'])}, "
+                f"{self._var(fz['l_in'])}, {self._var(fz['p'])}, {_flt(fz['c'])}, {_flt(fz['slack'])})")
 
     def _emit_lazy_softmax(self, plan, out: List[str], depth: int) -> None:
         """m, l and O are updated in place: the group's results m', l', O' name
@@ -673,9 +748,10 @@ class CDNA4Lowerer:
         # where the speculative half is known to fail (the first tile, whose running max is
         # -inf) or has just failed (a loop's exit to its exact path), only the exact half runs
         fn = "lazy_softmax_exact" if self._lazy_exact_only else "lazy_softmax"
-        out.append(f"{pad}wir::{fn}({self._var(plan['s'])}, {self._var(plan['m_in'])}, "
+        folded = self._fold_live and plan.get("fold")
+        out.append(f"{pad}wir::{fn}{'_b' if folded else ''}({self._var(plan['s'])}, {self._var(plan['m_in'])}, "
                    f"{self._var(plan['l_in'])}, {self._var(plan['o_in'])}, {self._var(plan['p'])}, "
-                   f"{_flt(plan['c'])}, {_flt(plan['slack'])});")
+                   f"{_flt(plan['c'])}, {_flt(plan['slack'])}{', wir_sb' if folded else ''});")
 
     def _emit_exact(self, op: Op, out: List[str], depth: int) -> None:
         """A fused lazy-softmax group with only its exact half."""
@@ -975,6 +1051,10 @@ class CDNA4Lowerer:
         if op.transpose_b:
             hoisted = self._hoisted.get(self.resolve(op.a.name))
             if hoisted is not None:
+                if self._fold_live and id(op) in self._score_folds:
+                    out.append(f"{pad}wir::mma_ABt_frags_bias<{ms}, {res_t.rows}, {res_t.cols}, "
+                               f"{self.stile(b_key)}, {hoisted[1]}>({res}, {hoisted[0]}, wir_sb, {b_ptr}, wave_col0);")
+                    return
                 out.append(f"{pad}wir::mma_ABt_frags<{ms}, {res_t.rows}, {res_t.cols}, {self.stile(b_key)}, "
                            f"{hoisted[1]}>({res}, {hoisted[0]}, {b_ptr}, wave_col0);")
                 return
@@ -1138,11 +1218,25 @@ class CDNA4Lowerer:
 
         def fast_call(d: int) -> None:
             qq = "  " * d
-            out.append(f"{qq}if (!wir::lazy_softmax_fast({self._var(fz['s'])}, {self._var(fz['m_in'])}, "
-                       f"{self._var(fz['l_in'])}, {self._var(fz['p'])}, {_flt(fz['c'])}, {_flt(fz['slack'])})) {{")
+            out.append(f"{qq}if (!{self._fast_call(fz)}) {{")
             out.append(f"{qq}  wir_exact = true;")
             out.append(f"{qq}  break;")
             out.append(f"{qq}}}")
+
+        out.append(f"{pad}{{")
+        was_live = self._fold_live
+        self._fold_preamble(op.body, out, depth + 1)
+        try:
+            self._emit_loop_lazy_body(op, stop, out, depth, fused_at, fz, pre, post, rotate, fast_call)
+        finally:
+            self._fold_live = was_live
+
+    def _emit_loop_lazy_body(self, op, stop, out, depth, fused_at, fz, pre, post, rotate, fast_call) -> None:
+        pad = "  " * depth
+        q = pad + "  "
+        iv = self._var(op.induction_var)
+        ivn = self.resolve(op.induction_var.name)
+        body = list(op.body)
 
         def shifted_post(d: int) -> None:
             self._slot_shift[ivn] = self._slot_shift.get(ivn, 0) - 1
@@ -1151,7 +1245,6 @@ class CDNA4Lowerer:
             if self._slot_shift[ivn] == 0:
                 del self._slot_shift[ivn]
 
-        out.append(f"{pad}{{")
         if not rotate:
             out.append(f"{q}int {iv} = {self._int(op.start)};")
             out.append(f"{q}for (;;) {{")
@@ -1350,6 +1443,9 @@ class CDNA4Lowerer:
         out.append(f"{pad}}} else {{")
         out.append(f"{q}const int wir_grp = (wir_wave >> 2) ^ {swap}, wir_gw = wir_wave & 3;"
                    f"  // group A (K loads) = physical wave group {swap}")
+        was_live = self._fold_live
+        if any(isinstance(self._softmax_fused.get(id(o)), dict) for o in plan["softmax"]):
+            self._fold_preamble([qk], out, depth + 1)
         out.append(f"{q}for (int wir_t = {start}; wir_t < ({start}) + {dist}; ++wir_t) {{")
         out.append(f"{q}  if (wir_grp == 0) {{")
         out.extend(dma(k_ld, "wir_t", depth + 2)[0])
@@ -1436,8 +1532,7 @@ class CDNA4Lowerer:
             m_phase(depth + 3)
             v_loads(depth + 3)
             self._emit_ops(pre, out, depth + 3)
-            out.append(f"{q}    if (!wir::lazy_softmax_fast({self._var(fz['s'])}, {self._var(fz['m_in'])}, "
-                       f"{self._var(fz['l_in'])}, {self._var(fz['p'])}, {_flt(fz['c'])}, {_flt(fz['slack'])})) {{")
+            out.append(f"{q}    if (!{self._fast_call(fz)}) {{")
             out.append(f"{q}      wir_exact = true;")
             out.append(f"{q}      break;")
             out.append(f"{q}    }}")
@@ -1458,6 +1553,7 @@ class CDNA4Lowerer:
         if not one:
             out.append(f"{q}if (wir_grp == 0) wir::wait_vm_barrier<0>();   // pairs with group B's extra V phase")
         out.append(f"{pad}}}")
+        self._fold_live = was_live
         return True
 
     def _attention_overlap_plan(self, loop: ForOp):
