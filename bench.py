@@ -481,7 +481,7 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
     # backward dQ kernel: 3 of the S x S x D products, over the forward's O and LSE
     do = seeded_normal((bsz, heads, seq, d), 3).cuda()
     dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
-    kernels.handle("mha_bwd_prep_d128")(O=o, dO=do, Dv=dvec)
+    kernels.handle("mha_bwd_prep_d128")(O=o, dO=do, L=lse, Dv=dvec, L2=torch.empty_like(lse))
     dq = torch.empty_like(q)
     for _ in range(reps):
         for name in dqs:

@@ -35,12 +35,13 @@ def _bwd_via_ir(q, k, v, do, o, lse, pipelined: bool, d: int, causal: bool = Fal
     if pipelined:
         dq_k = kernel_pass(dq_k, cost_model=gfx950_attention_cost_model(128, 64, d))
         dkdv_k = kernel_pass(dkdv_k, cost_model=gfx950_attention_cost_model(128, 64, d))
-    dv_vec = torch.zeros(b, h, s)
-    run_kernel(prep, {"O": o, "dO": do, "Dv": dv_vec}, {})
+    dv_vec, lse2 = torch.zeros(b, h, s), torch.zeros(b, h, s)
+    run_kernel(prep, {"O": o, "dO": do, "L": lse, "Dv": dv_vec, "L2": lse2}, {})
+    assert torch.equal(lse2, lse * math.log2(math.e))   # the same fp32 product as the dq kernel's
     dq = torch.zeros(b, h, s, d, dtype=torch.bfloat16)
     dk, dv = torch.zeros_like(dq), torch.zeros_like(dq)
     run_kernel(dq_k, {"Q": q, "K": k, "V": v, "dO": do, "L": lse, "Dv": dv_vec, "dQ": dq}, {"N": s})
-    run_kernel(dkdv_k, {"Q": q, "K": k, "V": v, "dO": do, "L": lse, "Dv": dv_vec, "dK": dk, "dV": dv}, {"N": s})
+    run_kernel(dkdv_k, {"Q": q, "K": k, "V": v, "dO": do, "L2": lse2, "Dv": dv_vec, "dK": dk, "dV": dv}, {"N": s})
     return dv_vec, dq, dk, dv
 
 
@@ -98,14 +99,14 @@ def test_grouped_query_attention_ir_matches_autograd(causal):
     run_kernel(fwd, {"Q": q, "K": k, "V": v, "O": o, "L": lse}, {"N": s, "HR": hr})
     ref_o, ref_lse = attention_ref(q, k.repeat_interleave(hr, 1), v.repeat_interleave(hr, 1), causal=causal)
     assert rel_err(o, ref_o) <= TOL and (lse - ref_lse).abs().max().item() <= 1e-3
-    dv_vec = torch.zeros(b, hq, s)
-    run_kernel(build_mha_bwd_prep_kernel(d=d), {"O": o, "dO": do, "Dv": dv_vec}, {})
+    dv_vec, lse2 = torch.zeros(b, hq, s), torch.zeros(b, hq, s)
+    run_kernel(build_mha_bwd_prep_kernel(d=d), {"O": o, "dO": do, "L": lse, "Dv": dv_vec, "L2": lse2}, {})
     dq = torch.zeros(b, hq, s, d, dtype=torch.bfloat16)
     dq_k = kernel_pass(build_mha_bwd_dq_kernel(d=d, causal=causal, gqa=True), cost_model=cost)
     run_kernel(dq_k, {"Q": q, "K": k, "V": v, "dO": do, "L": lse, "Dv": dv_vec, "dQ": dq}, {"N": s, "HR": hr})
     dk_part, dv_part = torch.zeros(b, hq, s, d), torch.zeros(b, hq, s, d)
     dkdv_k = kernel_pass(build_mha_bwd_dkdv_kernel(d=d, causal=causal, gqa=True), cost_model=cost)
-    run_kernel(dkdv_k, {"Q": q, "K": k, "V": v, "dO": do, "L": lse, "Dv": dv_vec, "dK_part": dk_part,
+    run_kernel(dkdv_k, {"Q": q, "K": k, "V": v, "dO": do, "L2": lse2, "Dv": dv_vec, "dK_part": dk_part,
                         "dV_part": dv_part}, {"N": s, "HR": hr})
     dk, dv = dk_part.view(b, hkv, hr, s, d).sum(2), dv_part.view(b, hkv, hr, s, d).sum(2)
     qf, kf, vf = (t.float().requires_grad_(True) for t in (q, k, v))

@@ -264,7 +264,7 @@ def test_dq_schedule_alternative_agrees(gpu):
     q, k, v, do = (seeded_normal((b, h, s, d), sd).cuda() for sd in (60, 61, 62, 63))
     o, lse = api.attention_forward(q, k, v)
     dvec = torch.empty(b, h, s, dtype=torch.float32, device="cuda")
-    kernels.handle("mha_bwd_prep_d128")(O=o, dO=do, Dv=dvec)
+    kernels.handle("mha_bwd_prep_d128")(O=o, dO=do, L=lse, Dv=dvec, L2=torch.empty_like(lse))
     out = {}
     for name in ("mha_bwd_dq_d128", "mha_bwd_dq_d128_kv64"):
         dq = torch.full_like(q, float("nan"))

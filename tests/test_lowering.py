@@ -315,8 +315,8 @@ def test_dkdv_cost_model_follows_its_query_tile():
     low = kernels.lowerer("mha_bwd_dkdv_d64")
     low.lower(kernels.kernel("mha_bwd_dkdv_d64"))
     off = low.lds_off
-    assert [low.tile_type_of(k).rows for k in ("q_bufs", "do_bufs", "l_bufs", "dv_bufs")] == [32] * 4
-    assert off["do_bufs"] - off["q_bufs"] == off["l_bufs"] - off["do_bufs"] == 2 * 32 * 64 * 2   # two slots
+    assert [low.tile_type_of(k).rows for k in ("q_bufs", "do_bufs", "l2_bufs", "dv_bufs")] == [32] * 4
+    assert off["do_bufs"] - off["q_bufs"] == off["l2_bufs"] - off["do_bufs"] == 2 * 32 * 64 * 2   # two slots
     assert low.lds_total == 17408   # + two 256-byte-aligned slots of each fp32 vector
 
 

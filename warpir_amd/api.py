@@ -253,8 +253,8 @@ def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None
     reduction sums the ``H / H_kv`` contributions of every key/value head
     into bf16 ``dK`` / ``dV``.  Three WarpIR kernels run
     on the current stream: ``Dv = rowsum(dO * O)`` (into ``dvec``, fp32
-    ``[B, H, S]``, allocated if omitted), the query-major dQ kernel and the
-    key-major dK/dV kernel (the reference's TK backward,
+    ``[B, H, S]``, allocated if omitted) together with the LSE in log2 units,
+    the query-major dQ kernel and the key-major dK/dV kernel (the reference's TK backward,
     ``kernel_examples/attention/mha_h100.cu:253-303,482-642``, computes the
     same gradients with dQ by atomic adds)."""
     import torch
@@ -271,11 +271,12 @@ def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None
     dk = torch.empty_like(k) if dk is None else dk
     dv = torch.empty_like(v) if dv is None else dv
     dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device=q.device) if dvec is None else dvec
-    kernels.handle(f"mha_bwd_prep_d{d}")(O=o, dO=do, Dv=dvec)
+    lse2 = torch.empty_like(lse)   # the LSE in log2 units, for the dK/dV kernel
+    kernels.handle(f"mha_bwd_prep_d{d}")(O=o, dO=do, L=lse, Dv=dvec, L2=lse2)
     sfx = "_causal" if causal else ""
     if hr == 1:
         kernels.handle(f"mha_bwd_dq_d{d}{sfx}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dQ=dq)
-        kernels.handle(f"mha_bwd_dkdv_d{d}{sfx}")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, dK=dk, dV=dv)
+        kernels.handle(f"mha_bwd_dkdv_d{d}{sfx}")(Q=q, K=k, V=v, dO=do, L2=lse2, Dv=dvec, N=seq, dK=dk, dV=dv)
         return dq, dk, dv
     numel = q.numel()
     if workspace is None:
@@ -285,7 +286,7 @@ def attention_backward(q, k, v, o, lse, do, dq=None, dk=None, dv=None, dvec=None
     dk_part = workspace[:numel].view(q.shape)
     dv_part = workspace[numel:2 * numel].view(q.shape)
     kernels.handle(f"mha_bwd_dq_d{d}{sfx}_gqa")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, HR=hr, dQ=dq)
-    kernels.handle(f"mha_bwd_dkdv_d{d}{sfx}_gqa")(Q=q, K=k, V=v, dO=do, L=lse, Dv=dvec, N=seq, HR=hr,
+    kernels.handle(f"mha_bwd_dkdv_d{d}{sfx}_gqa")(Q=q, K=k, V=v, dO=do, L2=lse2, Dv=dvec, N=seq, HR=hr,
                                                   dK_part=dk_part, dV_part=dv_part)
     _group_reduce(dk_part, dk, hr)
     _group_reduce(dv_part, dv, hr)

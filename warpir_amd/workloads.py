@@ -310,10 +310,16 @@ def _bwd_globals(d: int, rows: int):
 
 
 def build_mha_bwd_prep_kernel(d: int = 128, block_q: int = 128, wave_rows: int = 32,
-                              name: str = "mha_bwd_prep") -> Kernel:
-    """``Dv[b, h, q] = sum_d dO * O`` over ``[B, H, S, D]`` (bwd prep, ``mha_h100.cu:253-303``)."""
+                              name: str = "mha_bwd_prep", lse_log2: bool = True) -> Kernel:
+    """``Dv[b, h, q] = sum_d dO * O`` over ``[B, H, S, D]`` (bwd prep, ``mha_h100.cu:253-303``).
+
+    With ``lse_log2`` it also writes ``L2 = L * log2(e)`` from the forward's
+    natural-log ``L``: the key-major dK/dV kernel reads the LSE of every
+    query column at every step, and taking it in log2 units there saves one
+    multiply per column per step (the same fp32 product, computed once)."""
     g_bf, g_vec, tile = _bwd_globals(d, block_q)
     O, dO, Dv = Value("O", g_bf), Value("dO", g_bf), Value("Dv", g_vec)
+    L, L2 = Value("L", g_vec), Value("L2", g_vec)
     q_idx, head, batch = (Value(n, IntType()) for n in ("blockIdx.x", "blockIdx.y", "blockIdx.z"))
     reg = RegTileType(GPUType.fp32, wave_rows, d)
     cvec = ColVecType(GPUType.fp32, wave_rows, d)
@@ -331,7 +337,15 @@ def build_mha_bwd_prep_kernel(d: int = 128, block_q: int = 128, wave_rows: int =
         RowSumOp(result=dvec, tile=prod, prev=zero),
         TMAStoreOp(source=dvec, dest=Dv, coords=(batch, head, q_idx, 0)),
     )
-    return Kernel(name=name, inputs=(O, dO), outputs=(Dv,), body=body)
+    if not lse_log2:
+        return Kernel(name=name, inputs=(O, dO), outputs=(Dv,), body=body)
+    lse, lse2 = Value("lse", cvec), Value("lse_log2", cvec)
+    body += (
+        LoadVecOp(result=lse, source=L, coords=(batch, head, q_idx, 0)),
+        MulScalarOp(result=lse2, input=lse, scalar=LOG2E),
+        TMAStoreOp(source=lse2, dest=L2, coords=(batch, head, q_idx, 0)),
+    )
+    return Kernel(name=name, inputs=(O, dO, L), outputs=(Dv, L2), body=body)
 
 
 def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64, wave_rows: int = 32,
@@ -416,7 +430,8 @@ def build_mha_bwd_dq_kernel(d: int = 128, block_q: int = 128, block_kv: int = 64
 
 
 def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 64, wave_rows: int = 32,
-                              name: str = "mha_bwd_dkdv", causal: bool = False, gqa: bool = False) -> Kernel:
+                              name: str = "mha_bwd_dkdv", causal: bool = False, gqa: bool = False,
+                              lse_log2: bool = True) -> Kernel:
     """``dK`` and ``dV`` of attention forward, key-major: one program per key
     tile ``(blockIdx.x, head, batch)``; the loop walks query tiles.  Scores
     are computed transposed (``S^T = K Q^T``), so the per-query LSE and Dv
@@ -430,12 +445,16 @@ def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 
     are that query head's fp32 contributions ``dK_part`` / ``dV_part``
     ``[B, H, S, D]``; the ``HR`` contributions of a key/value head are then
     summed (the reference adds them with TMA reduce-add stores,
-    ``mha_h100.cu:456-479``)."""
+    ``mha_h100.cu:456-479``).
+
+    With ``lse_log2`` the LSE input is ``L2``, already in log2 units
+    (``build_mha_bwd_prep_kernel`` writes it); otherwise ``L`` is scaled by
+    log2(e) in the loop."""
     scale = 1.0 / math.sqrt(d)
     kv_glob, vec_glob, kv_tile = _bwd_globals(d, block_kv)
     q_glob, qvec_glob, q_tile = _bwd_globals(d, block_q)
     Q, K, V, dO = Value("Q", q_glob), Value("K", kv_glob), Value("V", kv_glob), Value("dO", q_glob)
-    L, Dv = Value("L", qvec_glob), Value("Dv", qvec_glob)
+    L, Dv = Value("L2" if lse_log2 else "L", qvec_glob), Value("Dv", qvec_glob)
     if gqa:
         part_glob = GlobalType(GPUType.fp32, kv_tile)
         dK, dV = Value("dK_part", part_glob), Value("dV_part", part_glob)
@@ -490,8 +509,8 @@ def build_mha_bwd_dkdv_kernel(d: int = 128, block_kv: int = 128, block_q: int = 
             MMAOp(result=st, a=k_sh, b=q_sh, accum=zero, transpose_b=True),
             *mask,
             MulScalarOp(result=st_sc, input=scores, scalar=scale * LOG2E),
-            MulScalarOp(result=lse2, input=lse, scalar=LOG2E),
-            SubColOp(result=st_sh, tile=st_sc, vec=lse2),
+            *([] if lse_log2 else [MulScalarOp(result=lse2, input=lse, scalar=LOG2E)]),
+            SubColOp(result=st_sh, tile=st_sc, vec=lse if lse_log2 else lse2),
             Exp2Op(result=pt, input=st_sh),
             ZeroOp(result=dpt_zero),
             MMAOp(result=dpt, a=v_sh, b=do_sh, accum=dpt_zero, transpose_b=True),
