@@ -73,3 +73,29 @@ def test_noalloc_split_k_validates_operands_on_the_host():
         api.gemm_split_k_noalloc(a, b, torch.zeros(64, 128, dtype=torch.bfloat16), splits=4)
     with pytest.raises(ValueError, match="must be on one GPU"):
         api.gemm_split_k_noalloc(a, b, torch.zeros(64, 256, dtype=torch.bfloat16), splits=4)
+
+
+def test_source_flag_marker_is_parsed_and_restricted():
+    """A generated source's first line may ask for the MFMA VGPR form; nothing else passes."""
+    from warpir_amd.lowering.cdna4 import HIPCC_FLAGS_MARKER
+    from warpir_amd.runtime import CompileError, hsaco_path, source_flags
+
+    body = "// Generated\nextern \"C\" __global__ void k() {}\n"
+    assert source_flags(body) == ()
+    marked = f"{HIPCC_FLAGS_MARKER} -mllvm -amdgpu-mfma-vgpr-form=1\n" + body
+    assert source_flags(marked) == ("-mllvm", "-amdgpu-mfma-vgpr-form=1")
+    assert hsaco_path(marked) != hsaco_path(body)   # the flags are part of the cache key
+    for bad in ("-O0", "-mllvm -amdgpu-mfma-vgpr-form=1 -fsanitize=address", "-mllvm"):
+        with pytest.raises(CompileError):
+            source_flags(f"{HIPCC_FLAGS_MARKER} {bad}\n" + body)
+
+
+def test_dkdv_d128_kernels_ask_for_the_vgpr_form_and_others_do_not():
+    from warpir_amd.runtime import source_flags
+
+    for name in ("mha_bwd_dkdv_d128", "mha_bwd_dkdv_d128_causal", "mha_bwd_dkdv_d128_gqa"):
+        src = kernels.lowerer(name).lower(kernels.kernel(name))
+        assert source_flags(src) == ("-mllvm", "-amdgpu-mfma-vgpr-form=1"), name
+    for name in ("gemm_256_k64", "mha_d128", "mha_bwd_dq_d128", "mha_bwd_dkdv_d64"):
+        src = kernels.lowerer(name).lower(kernels.kernel(name))
+        assert source_flags(src) == (), name

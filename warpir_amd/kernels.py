@@ -213,6 +213,14 @@ TARGETS: Dict[str, dict] = {
     "mha_d64_causal_ovl": {"attn_overlap": True, "lazy_softmax": False},
 }
 
+# The D=128 dK/dV kernels hold dK, dV and the score tiles in more than 256 registers.  With
+# the MFMAs' VGPR form the S and dP tiles stay in arch VGPRs (no v_accvgpr_read per score
+# before the softmax algebra) and dK, dV take the AGPRs: 4.21-4.24 against 4.38-4.51 ms at
+# B16 H16 S4096, bitwise the same gradients.  (The GEMM does not compile in that form.)
+for _name in ("mha_bwd_dkdv_d128", "mha_bwd_dkdv_d128_causal", "mha_bwd_dkdv_d128_gqa",
+              "mha_bwd_dkdv_d128_causal_gqa"):
+    TARGETS[_name] = {"mfma_vgpr_form": True}
+
 
 def lowerer(name: str):
     """The ``CDNA4Lowerer`` variant *name* is built with."""

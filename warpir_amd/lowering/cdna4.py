@@ -123,6 +123,12 @@ class CDNA4Target:
     # second bf16 rounding of Q makes the score error grow with the logits'
     # magnitude (O error 1.3e-2 at LSE ~47, against 3.6e-3 unfolded).
     fold_softmax_scale: bool = False
+    # Ask the compiler for the VGPR form of the MFMAs (LLVM's
+    # -amdgpu-mfma-vgpr-form): accumulators that VALU code reads (scores)
+    # stay in arch VGPRs instead of AGPRs, which removes their
+    # v_accvgpr_read copies.  The flag travels in the source's first line
+    # (``HIPCC_FLAGS_MARKER``), so it is part of the code-object cache key.
+    mfma_vgpr_form: bool = False
     # Warp specialisation for ring-pipelined MMA loops: the workgroup gets a
     # second set of wavefronts (waves NW..2NW-1) that only issue the LDS-DMA
     # loads, while waves 0..NW-1 only read LDS and issue MFMAs.  Both sets pass
@@ -136,6 +142,11 @@ class LaunchConfig:
     grid: Tuple[int, int, int]
     block: Tuple[int, int, int]
     dyn_lds: int = 0
+
+
+# A generated source whose first line starts with this marker is compiled with
+# the hipcc flags that follow it on that line (``runtime.compile_source``).
+HIPCC_FLAGS_MARKER = "// wir-hipcc-flags:"
 
 
 @dataclass
@@ -2107,6 +2118,7 @@ class CDNA4Lowerer:
         nt = self.num_threads
         pid = _pid_code(dims, self.target, reverse_x=causal_x)
         src = [
+            *([f"{HIPCC_FLAGS_MARKER} -mllvm -amdgpu-mfma-vgpr-form=1"] if self.target.mfma_vgpr_form else []),
             "// Generated by warpir_amd.lowering.CDNA4Lowerer for gfx950 -- do not edit.",
             _header_text(),
             "",

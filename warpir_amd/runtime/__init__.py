@@ -31,6 +31,7 @@ from typing import Dict, Optional, Sequence, Tuple
 
 from warpir_amd.ir.ops import Kernel, Value
 from warpir_amd.ir.types import GPUType, GlobalType, ScalarType
+from warpir_amd.lowering.cdna4 import HIPCC_FLAGS_MARKER
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_DIR, "libwarpir_rt.so")
@@ -131,6 +132,22 @@ def hsaco_path(source: str) -> str:
     return os.path.join(CACHE_DIR, source_key(source) + ".hsaco")
 
 
+# Extra hipcc flags a generated source may ask for on its first line (after
+# the lowering's HIPCC_FLAGS_MARKER); only these are accepted.
+_ALLOWED_SOURCE_FLAGS = {("-mllvm", "-amdgpu-mfma-vgpr-form=1")}
+
+
+def source_flags(source: str) -> Tuple[str, ...]:
+    """The hipcc flags named on *source*'s first line, if it carries the marker."""
+    first = source.split("\n", 1)[0]
+    if not first.startswith(HIPCC_FLAGS_MARKER):
+        return ()
+    words = first[len(HIPCC_FLAGS_MARKER):].split()
+    if len(words) % 2 or any(tuple(words[i:i + 2]) not in _ALLOWED_SOURCE_FLAGS for i in range(0, len(words), 2)):
+        raise CompileError(f"unsupported hipcc flags in the source marker: {' '.join(words)}")
+    return tuple(words)
+
+
 def compile_source(source: str, force: bool = False) -> str:
     """Compile *source* for gfx950 into the cache; returns the ``.hsaco`` path."""
     out = hsaco_path(source)
@@ -145,7 +162,8 @@ def compile_source(source: str, force: bool = False) -> str:
     with open(src_path, "w") as f:
         f.write(source)
     tmp = f"{base}.{os.getpid()}.tmp"
-    cmd = [hipcc, *HIPCC_FLAGS, "-Rpass-analysis=kernel-resource-usage", src_path, "-o", tmp]
+    cmd = [hipcc, *HIPCC_FLAGS, *source_flags(source), "-Rpass-analysis=kernel-resource-usage", src_path,
+           "-o", tmp]
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     with open(base + ".log", "w") as f:
         f.write(" ".join(cmd) + "\n" + proc.stdout)
