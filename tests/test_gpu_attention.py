@@ -97,6 +97,27 @@ def test_mha_lazy_rescale_with_growing_scores(gpu, variant, d, causal):
     assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-3 * ref_lse.abs().max().item() + 1e-3
 
 
+@pytest.mark.parametrize("variant,d,causal", [("mha_d128_fold", 128, False), ("mha_d64_causal_fold", 64, True)])
+def test_mha_fold_rescale_with_growing_scores(gpu, variant, d, causal):
+    """The folded-scale variants on keys that grow along the sequence, so their mid-loop
+    rescale (a new running max moves the bias operands and rescales O and l) runs.
+    Their documented envelope: the second bf16 rounding of c*q makes the score error
+    grow with the logits, so the keys stop at 3x (max LSE ~14); within it the O error
+    stays under the 1e-2 bar and the LSE error under 2e-2 absolute."""
+    b, h, s = 1, 2, 1024
+    announce(f"{variant} growing keys (fold envelope) B={b} H={h} S={s}")
+    q, k, v = (seeded_normal((b, h, s, d), sd) for sd in (6, 7, 8))
+    k = (k.float() * torch.linspace(0.5, 3.0, s).view(1, 1, s, 1)).to(torch.bfloat16)
+    o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda(), causal=causal, variant=variant)
+    torch.cuda.synchronize()
+    ref, ref_lse = attention_ref(q, k, v, causal=causal)
+    err = rel_err(o.cpu(), ref)
+    lse_err = (lse.cpu() - ref_lse).abs().max().item()
+    print(f"{variant}: O rel_err {err:.3e}, LSE max abs {lse_err:.3e}", flush=True)
+    assert err <= TOL, err
+    assert lse_err <= 2e-2, lse_err
+
+
 def test_mha_full_size_sampled(gpu):
     """Config 4 at full size; the oracle runs on 2 of the 256 (b, h) heads."""
     shape = (16, 16, 4096, 128)

@@ -103,6 +103,24 @@ def test_api_gemm_routes_short_m_to_split_k(gpu):
     assert rel_err(c.cpu(), gemm_ref(a, b)) <= TOL
 
 
+def test_api_gemm_row_strided_short_m(gpu):
+    """M=128 with long K and row-strided A and out: api.gemm takes the tiled kernel (split-K
+    needs dense operands) and reads and writes through the row strides."""
+    from warpir_amd import api
+
+    m, n, k = 128, 1024, 8192
+    announce(f"api.gemm {m}x{n}x{k} row-strided A and out")
+    a_full = seeded_normal((m, k + 64), 25, 0.1)
+    b = seeded_normal((k, n), 26, 0.1)
+    out_full = torch.full((m, n + 64), float("nan"), dtype=torch.bfloat16, device="cuda")
+    a_dev = a_full.cuda()[:, :k]
+    out = out_full[:, :n]
+    api.gemm(a_dev, b.cuda(), out=out)
+    torch.cuda.synchronize()
+    assert rel_err(out.cpu(), gemm_ref(a_full[:, :k].contiguous(), b)) <= TOL
+    assert torch.isnan(out_full[:, n:].float()).all()   # the padding columns stay untouched
+
+
 def test_gemm_repeated_launches_bitwise_stable(gpu):
     """GEMM 8192^3 (the headline kernel), 6 launches into the same C: no atomics and a fixed
     accumulation order, so every launch reproduces the first bit for bit."""

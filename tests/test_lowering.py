@@ -13,6 +13,7 @@ import re
 import shutil
 
 import pytest
+import torch
 
 from warpir_amd import kernels
 from warpir_amd.lowering import CDNA4Lowerer, CDNA4Target, LoweringError
@@ -165,6 +166,28 @@ def test_attention_pingpong_one_barrier_per_iteration():
     assert "if (wir_grp == 1) wir::wait_vm_barrier" not in pp2 and "wir_grp == 0 ? 1 : 0" in pp2
 
 
+def test_lazy_softmax_fusion_needs_its_inputs_defined_first():
+    """The lazy-softmax group is emitted as one call at its first member.  With the copy of the
+    running max moved ahead of the QK MMA (still valid IR: it reads only the max), that call would
+    read the scores before the MMA defines them, so the fusion is skipped and the ops are lowered
+    one by one instead."""
+    import copy
+
+    from warpir_amd.ir.ops import CopyOp, ForOp, MMAOp
+    k = copy.deepcopy(kernels.kernel("mha_d64_causal"))
+    low = kernels.lowerer("mha_d64_causal")
+    assert "wir::lazy_softmax_fast(" in low.lower(k)
+    loop = next(op for op in k.body if isinstance(op, ForOp))
+    cp = next(o for o in loop.body if isinstance(o, CopyOp) and o.result.name == "max_prev")
+    qk = next(o for o in loop.body if isinstance(o, MMAOp))
+    body = [o for o in loop.body if o is not cp]
+    body.insert(body.index(qk), cp)
+    object.__setattr__(loop, "body", tuple(body))   # the IR dataclasses are frozen
+    src = kernels.lowerer("mha_d64_causal").lower(k)
+    body = src[src.rindex('extern "C" __global__'):]
+    assert "wir::lazy_softmax_fast(" not in body and "wir::lazy_softmax_exact(" not in body
+
+
 def test_lazy_softmax_folds_scale_into_q_and_max_into_the_score_mfmas():
     """``fold_softmax_scale`` (opt-in): with the lazy softmax on hoisted Q, the fused loop scales
     the fragments once, declares the score bias, starts each QK MMA with the bias MFMA and calls
@@ -304,6 +327,34 @@ def test_gemm_variant_selection():
     assert api.gemm_variant(64, 8192, 100) == "gemm_128x32_k64"   # K too short to split
     for v in ("gemm_256_k64", "gemm_128_k64", "gemm_128x32_k64"):
         assert v in kernels.VARIANTS
+
+
+def test_gemm_routes_strided_short_m_away_from_split_k(monkeypatch):
+    """api.gemm sends M <= 128, long-K products to split-K only when every tensor is dense:
+    the split-K entry points address a, b and out as contiguous arrays, while the tiled
+    kernel reads row-strided views through the globals' row stride."""
+    from warpir_amd import api
+
+    taken = []
+    monkeypatch.setattr(api, "gemm_split_k", lambda a, b, out=None, workspace=None: taken.append("splitk") or out)
+
+    class _Handle:
+        def __init__(self, name):
+            self.name = name
+
+        def __call__(self, **kw):
+            taken.append(self.name)
+
+    monkeypatch.setattr(kernels, "handle", _Handle)
+    a_full = torch.zeros(128, 8192 + 64, dtype=torch.bfloat16)
+    b = torch.zeros(8192, 1024, dtype=torch.bfloat16)
+    api.gemm(a_full[:, :8192].contiguous(), b)
+    api.gemm(a_full[:, :8192], b)                       # row-strided A
+    out_full = torch.zeros(128, 1024 + 64, dtype=torch.bfloat16)
+    api.gemm(a_full[:, :8192].contiguous(), b, out=out_full[:, :1024])   # row-strided out
+    assert taken == ["splitk", api.SKINNY_GEMM_VARIANT, api.SKINNY_GEMM_VARIANT]
+    assert api._splitk_operands_ok(a_full[:, :8192].contiguous(), b, torch.zeros(128, 1024, dtype=torch.bfloat16))
+    assert not api._splitk_operands_ok(a_full[:, :8192], b, torch.zeros(128, 1024, dtype=torch.bfloat16))
 
 
 def test_dkdv_cost_model_follows_its_query_tile():

@@ -173,6 +173,15 @@ def gemm_split_k_noalloc(a, b, out, splits: Optional[int] = None, stream=None):
     return out
 
 
+def _splitk_operands_ok(a, b, out) -> bool:
+    """Whether ``gemm_split_k`` accepts these tensors: bf16, contiguous and
+    16-byte aligned (it addresses them as dense row-major arrays)."""
+    import torch
+
+    return all(t.dtype == torch.bfloat16 and t.is_contiguous() and t.data_ptr() % 16 == 0
+               for t in (a, b, out))
+
+
 def gemm(a, b, out=None, variant: Optional[str] = None, workspace=None):
     """``out[M, N] = a[M, K] @ b[K, N]`` in bf16 with fp32 accumulation.
 
@@ -192,6 +201,10 @@ def gemm(a, b, out=None, variant: Optional[str] = None, workspace=None):
         out = torch.empty(m, n, dtype=torch.bfloat16, device=a.device)
     if variant is None:
         variant = gemm_variant(m, n, k)
+        if variant == SPLITK_GEMM_VARIANT and not _splitk_operands_ok(a, b, out):
+            # the split-K entry points take dense operands only; the tiled
+            # kernel reads row-strided views through the globals' row stride
+            variant = SKINNY_GEMM_VARIANT
     if variant == SPLITK_GEMM_VARIANT:
         return gemm_split_k(a, b, out=out, workspace=workspace)
     kernels.handle(variant)(A=a, B=b, N=k, C_global=out)

@@ -680,6 +680,12 @@ class CDNA4Lowerer:
             last = max(ops.index(g) for g in group)
             if any(id(o) not in ids and any(v.name in outputs for v in _op_values(o)) for o in ops[first:last + 1]):
                 continue
+            # the fused group is emitted at its first member, so every value it
+            # reads from outside (the scores, l, O) must be defined before that
+            external = {s_v.name, norm.name, mr.tile.name}
+            if any(isinstance(getattr(o, "result", None), Value) and o.result.name in external
+                   for o in ops[first:last + 1] if id(o) not in ids):
+                continue
             plan = dict(s=s_v, m_in=m_v, m_out=lz.result, l_in=norm, l_out=rs.result, o_in=mr.tile,
                         o_out=mr.result, p=cv.result, c=c, slack=lz.slack, ids=ids)
             for g in group:
