@@ -415,7 +415,7 @@ def mfma_ceiling(iters: int = 20000):
 # options): the evidence behind the default choices.
 COMPARE_GEMM = ["gemm_256_k64", "gemm_256_k32", "gemm_256_pp", "gemm_256x128", "gemm_256x128_ws_all",
                 "gemm_256x128_ws", "gemm_128_k64"]
-COMPARE_FA = ["mha_d128", "mha_d128_fold", "mha_d128_pp2b", "mha_d128_s5", "mha_d128_w4", "mha_d128_online", "mha_d128_q256",
+COMPARE_FA = ["mha_d128", "mha_d128_u2", "mha_d128_fold", "mha_d128_pp2b", "mha_d128_s5", "mha_d128_w4", "mha_d128_online", "mha_d128_q256",
               "mha_d128_ovl"]
 COMPARE_BWD_DQ = ["mha_bwd_dq_d128", "mha_bwd_dq_d128_kv64"]
 

@@ -33,7 +33,7 @@ def test_reference_attention_ir(gpu, n):
 
 @pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp_swapped", "mha_d128_w4",
                                      "mha_d128_online", "mha_d128_ovl", "mha_d128_s5", "mha_d128_pp2b",
-                                     "mha_d128_fold"])
+                                     "mha_d128_fold", "mha_d128_u2"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 1, 64)])
 def test_mha_d128(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")
@@ -81,6 +81,7 @@ def test_mha_d64_causal(gpu, variant, b, h, s):
 
 
 @pytest.mark.parametrize("variant,d,causal", [("mha_d128", 128, False), ("mha_d128_w4", 128, False),
+                                              ("mha_d128_u2", 128, False),
                                               ("mha_d64_causal", 64, True), ("mha_d128_ovl", 128, False),
                                               ("mha_d64_causal_ovl", 64, True), ("mha_d64_causal_pp", 64, True)])
 def test_mha_lazy_rescale_with_growing_scores(gpu, variant, d, causal):
@@ -135,6 +136,7 @@ def test_mha_full_size_sampled(gpu):
 @pytest.mark.parametrize("variant,causal,shape", [
     (None, True, (8, 32, 8192, 64)), (None, False, (16, 16, 4096, 128)), (None, True, (16, 16, 4096, 128)),
     ("mha_d128_online", False, (16, 16, 4096, 128)), ("mha_d128_ovl", False, (16, 16, 4096, 128)),
+    ("mha_d128_u2", False, (16, 16, 4096, 128)),
     ("mha_d64_causal_ovl", True, (8, 32, 8192, 64)), ("mha_d64_causal_pp", True, (8, 32, 8192, 64))])
 def test_mha_repeated_launches_bitwise_stable(gpu, variant, causal, shape):
     """Configs 5 and 4 at full size (default kernels and the ping-pong / overlapped

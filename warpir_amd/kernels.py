@@ -91,6 +91,10 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # the same with a 5-slot ring (the whole 160 KB of LDS), loaded three tiles ahead
     "mha_d128_s5": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=160 * 1024, min_stages=5,
                                 rescale_slack=LAZY_SLACK),
+    # the 5-slot ring with a workgroup barrier every second iteration only (K and V both loaded
+    # three tiles ahead)
+    "mha_d128_u2": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=160 * 1024, min_stages=5,
+                                rescale_slack=LAZY_SLACK),
     # the same with the K and V load streams on the opposite wave groups from the warp assigner's answer
     "mha_d128_pp_swapped": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
                                         rescale_slack=LAZY_SLACK),
@@ -196,6 +200,7 @@ TARGETS: Dict[str, dict] = {
     "mha_d128_ovl": {"attn_overlap": True, "lazy_softmax": False},
     "mha_d128_pp_swapped": {"wave_groups": {"k": 1, "v": 0}},
     "mha_d128_pp2b": {"pingpong_one_barrier": False},
+    "mha_d128_u2": {"pingpong_barrier_every": 2},
     "mha_d128_fold": {"fold_softmax_scale": True},
     "mha_d64_causal_fold": {"fold_softmax_scale": True},
     # tile orders of the 8192^3 GEMM: GROUP_M rows of tiles per group, and without the XCD remap

@@ -115,6 +115,11 @@ class CDNA4Target:
     # one per phase: group A passes it after its V phase, group B after its
     # M phase, so the two groups' phases interleave without lock-step.
     pingpong_one_barrier: bool = True
+    # With the one-barrier ping-pong on a ring of at least 5 slots: pass the
+    # workgroup barrier only every second iteration (both groups load K and
+    # V tiles S - 2 ahead, and each barrier still leaves the wave's newest
+    # batch in flight).  1 keeps a barrier every iteration.
+    pingpong_barrier_every: int = 1
     # With the lazy softmax on scores from hoisted Q fragments: the scale c is
     # folded into those fragments (bf16 of c*q, once per program) and the
     # running max into the score MFMAs (one extra MFMA per column block
@@ -1408,7 +1413,11 @@ class CDNA4Lowerer:
         writes was last read two intervals (K) or one interval (V) before.
         """
         plan = self._attention_pingpong_plan(loop)
-        if plan is None or plan["S"] < 4:
+        one = self.target.pingpong_one_barrier
+        every = self.target.pingpong_barrier_every if one else 1
+        if every not in (1, 2):
+            raise LoweringError(f"pingpong_barrier_every must be 1 or 2, not {every}")
+        if plan is None or plan["S"] < (4 if every == 1 else 5):
             return False
         swap = self._pingpong_group_swap(plan)
         if swap is None:
@@ -1417,6 +1426,11 @@ class CDNA4Lowerer:
         p1 = pad + "  "
         S, qk, pv = plan["S"], plan["qk"], plan["pv"]
         dist = S - 2
+        # V load distance: B's V(i) runs in interval i + 1.  With a barrier every
+        # iteration it loads V tile i + S - 1; with one every second iteration
+        # tile i + S - 2, so that the slot's previous tile was read in an
+        # earlier barrier interval.
+        dv = dist + 1 if every == 1 else dist
         iv = self._var(loop.induction_var)
         ivn = self.resolve(loop.induction_var.name)
         start = loop.start
@@ -1471,12 +1485,15 @@ class CDNA4Lowerer:
         out.append(f"{q}  }}")
         out.append(f"{q}}}")
         out.append(f"{q}wir::wait_vm_barrier<{per}>();")
-        one = self.target.pingpong_one_barrier
-        out.append(f"{q}if (wir_grp == 1) {{   // group B's first V phase: its first ring load only")
-        out.extend(dma(v_ld, f"({start}) + {dist}", depth + 2)[0])
-        if not one:
-            out.append(f"{q}  wir::wait_vm_barrier<{per}>();")
-        out.append(f"{q}}}")
+        if every == 1:
+            out.append(f"{q}if (wir_grp == 1) {{   // group B's first V phase: its first ring load only")
+            out.extend(dma(v_ld, f"({start}) + {dist}", depth + 2)[0])
+            if not one:
+                out.append(f"{q}  wir::wait_vm_barrier<{per}>();")
+            out.append(f"{q}}}")
+        # barrier intervals of `every` iterations: a group passes its barrier in
+        # iteration i only when (i - start) % every == every - 1
+        odd = "" if every == 1 else f" && ((({iv}) - ({start})) & 1)"
 
         # Ring loads of tiles past the loop's end are skipped; a barrier whose
         # wave's latest batch was skipped drains all its loads instead (the
@@ -1484,15 +1501,15 @@ class CDNA4Lowerer:
         # i + dist, B's batch of V(i) is V tile i + dist + 1.
         def m_barrier(d: int) -> None:   # end of an M phase
             pd = "  " * d
-            if one:   # B's latest batch: from its V(i-1)
-                out.append(f"{pd}if (wir_grp == 1) wir::wait_vm_barrier_after<{per}>(({iv}) + {dist} < {stop});")
+            if one:   # B's latest batch: from its V(i-1), V tile i - 1 + dv
+                out.append(f"{pd}if (wir_grp == 1{odd}) wir::wait_vm_barrier_after<{per}>(({iv}) + {dv - 1} < {stop});")
             else:
                 out.append(f"{pd}wir::wait_vm_barrier_after<{per}>(({iv}) + {dist} - (wir_grp == 0 ? 1 : 0) < {stop});")
 
         def v_barrier(d: int) -> None:   # end of a V phase
             pd = "  " * d
             if one:   # A's latest batch: from this V(i)
-                out.append(f"{pd}if (wir_grp == 0) wir::wait_vm_barrier_after<{per}>(({iv}) + {dist} < {stop});")
+                out.append(f"{pd}if (wir_grp == 0{odd}) wir::wait_vm_barrier_after<{per}>(({iv}) + {dist} < {stop});")
             else:
                 out.append(f"{pd}wir::wait_vm_barrier_after<{per}>(({iv}) + {dist} + (wir_grp == 1 ? 1 : 0) < {stop});")
         softmax = plan["softmax"]
@@ -1504,8 +1521,8 @@ class CDNA4Lowerer:
             out.append(f"{qq}  if (({iv}) + {dist} < {stop})")
             out.extend(dma(k_ld, f"({iv}) + {dist}", d + 2)[0])
             out.append(f"{qq}}} else {{")
-            out.append(f"{qq}  if (({iv}) + {dist + 1} < {stop})")
-            out.extend(dma(v_ld, f"({iv}) + {dist + 1}", d + 2)[0])
+            out.append(f"{qq}  if (({iv}) + {dv} < {stop})")
+            out.extend(dma(v_ld, f"({iv}) + {dv}", d + 2)[0])
             out.append(f"{qq}}}")
 
         def v_tail(ops, d: int) -> None:
