@@ -438,22 +438,45 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
     for name in names:
         if name not in kernels.VARIANTS:
             raise ValueError(f"--compare: unknown variant {name!r}")
-    # the shapes timed here: GEMM 8192^3 (not the split-K kernels, whose C is fp32 partials),
-    # FA forward and dQ at D=128 without masking or grouped heads
+    # the shapes timed here: GEMM 8192^3, the split-K kernels at config 3' (M=128, N=K=8192, four
+    # rotated B operands, through api.gemm_split_k), FA forward and dQ at D=128 without masking
+    # or grouped heads
     gemms = [x for x in names if x.startswith("gemm_") and "splitk" not in x]
+    sks = [x for x in names if x.startswith("gemm_") and "splitk" in x]
     dqs = [x for x in names if x.startswith("mha_bwd_dq_d128") and not x.endswith(("_causal", "_gqa"))]
     fas = [x for x in names if x.startswith("mha_d128") and "causal" not in x and "gqa" not in x]
-    untimed = [x for x in names if x not in gemms + dqs + fas]
+    untimed = [x for x in names if x not in gemms + sks + dqs + fas]
     if untimed:
-        raise ValueError(f"--compare times GEMM 8192^3, FA forward and dQ at the config-4 shape; "
-                         f"not {', '.join(untimed)}")
+        raise ValueError(f"--compare times GEMM 8192^3, split-K at M=128 N=K=8192, FA forward and dQ at "
+                         f"the config-4 shape; not {', '.join(untimed)}")
     stream = torch.cuda.current_stream().cuda_stream
     out = {}
+    timed = collections.defaultdict(list)
+    if sks:
+        import itertools
+
+        from warpir_amd import api
+
+        m, n, k = 128, 8192, 8192
+        a = seeded_normal((m, k), 5, 0.1).cuda()
+        bs = [seeded_normal((k, n), 6 + i, 0.1).cuda() for i in range(4)]
+        c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(api.splitk_count(m, n, k) * m * n, dtype=torch.float32, device="cuda")
+        nxt = itertools.cycle(bs).__next__
+        for _ in range(reps):
+            for name in sks:
+                timed[name].append(_time_launches(
+                    lambda: api.gemm_split_k(a, nxt(), out=c, workspace=ws, variant=name),  # noqa: B023
+                    steps, warmup, stream)[0])
+        for name in sks:
+            ms = statistics.median(timed[name])
+            out[name] = {"ms": ms, "ms_reps": timed[name], "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
+                         "shape": [m, n, k], "options": kernels.TARGETS.get(name, {})}
+        del a, bs, c, ws
     n = 8192
     a = seeded_normal((n, n), 0, 0.1).cuda() if gemms else None
     b = seeded_normal((n, n), 1, 0.1).cuda() if gemms else None
     c = torch.empty(n, n, dtype=torch.bfloat16, device="cuda") if gemms else None
-    timed = collections.defaultdict(list)
     for _ in range(reps):
         for name in gemms:
             h = kernels.handle(name)

@@ -10,9 +10,11 @@ pipelined IR relies on it (``warpir/lowering/lowering.py``):
   they are different storages and accumulates ``a @ b`` into ``result``;
   with ``transpose_b`` it computes ``a @ b^T`` only (``lowering.py:454-470``);
 * ``MMABufOp`` accumulates in place into ``accum`` and then advances the
-  drain counter ``(c + 1) % modulus`` (``lowering.py:472-488``);
-* a drain slot (``BufSlotExpr(value=None)``) reads the drain counter, its
-  offset is not used (``lowering.py:196-207``);
+  drain counter by one (``lowering.py:472-488``, which keeps it reduced by
+  the single ring size; here it counts MMAs, and each read reduces it);
+* a drain slot (``BufSlotExpr(value=None)``) reads the drain counter modulo
+  its ring size, its offset is not used (``lowering.py:196-207``);
+  ``DrainIndexOp`` (additive) reads the unreduced counter plus its offset;
 * register values are block-level tiles (all wavefront slices together);
   ``zero`` / ``neg_infty`` are scalars that broadcast to the first shape
   they are combined with;
@@ -39,7 +41,7 @@ from typing import Dict, Tuple
 import torch
 
 from warpir_amd.ir import (
-    AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, ColVecType, CopyOp, DivRowOp, Exp2Op,
+    AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, ColVecType, CopyOp, DivRowOp, DrainIndexOp, Exp2Op,
     ForOp, GPUType, IntAffineOp, IntDivOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp,
     NegInftyOp, RegTileType, RowMaxOp, RowSumOp, RowVecType, SlotViewOp, SubColOp, SubOp, SubRowOp, LazyMaxOp,
     TMALoadBufOp, TMALoadOp, TMAStoreOp, Value, WaitBufOp, WaitOp, YieldOp, ZeroOp,
@@ -117,7 +119,7 @@ class Interpreter:
         if isinstance(slot, int):
             return slot
         if slot.value is None:
-            return self.drain
+            return self.drain % slot.modulus
         return (self._int(slot.value) + slot.offset) % slot.modulus
 
     def _load(self, src: Value, coords, rows: int, cols: int) -> torch.Tensor:
@@ -168,6 +170,8 @@ class Interpreter:
         elif isinstance(op, TMALoadOp):
             t = op.result.type
             s(op.result, self._load(op.source, op.coords, t.rows, t.cols))
+        elif isinstance(op, DrainIndexOp):
+            s(op.result, self.drain + op.offset)
         elif isinstance(op, AllocSharedOp):
             s(op.result, [None] * op.result.type.count)
         elif isinstance(op, SlotViewOp):
@@ -188,7 +192,7 @@ class Interpreter:
             s(op.accum, acc)
             s(op.result, acc)
             if isinstance(op.a_slot, BufSlotExpr):
-                self.drain = (self.drain + 1) % op.a_slot.modulus
+                self.drain += 1
         elif isinstance(op, CopyOp):
             x = g(op.input).clone()
             rt = op.result.type

@@ -322,7 +322,7 @@ def test_gemm_variant_selection():
     assert api.gemm_variant(2048, 2048) == "gemm_128_k64"      # 64 tiles of 256x256
     assert api.gemm_variant(128, 8192) == "gemm_128x32_k64"          # K unknown: no split
     assert api.gemm_variant(256, 8192) == "gemm_128x64_k64"
-    assert api.gemm_variant(64, 8192, 8192) == api.SPLITK_GEMM_VARIANT == "gemm_128_splitk_k128"
+    assert api.gemm_variant(64, 8192, 8192) == api.SPLITK_GEMM_VARIANT == "gemm_128_splitk_k128_b3"
     assert api.gemm_variant(128, 8192, 8192) == api.SPLITK_GEMM_VARIANT
     assert api.gemm_variant(64, 8192, 100) == "gemm_128x32_k64"   # K too short to split
     for v in ("gemm_256_k64", "gemm_128_k64", "gemm_128x32_k64"):
@@ -379,3 +379,17 @@ def test_split_k_count_and_ir():
     assert api.splitk_count(128, 8192, 8256) == 3        # 8256 = 3 * 2752 = 3 * 43 * 64
     src = CDNA4Lowerer().lower(kernels.kernel("gemm_128_splitk"))
     assert "wir::gl<float> C_global" in src and "pid_z, (pid_y) * 128" in src
+
+
+def test_per_ring_gemm_lowering_merges_ring_waits():
+    """Rings of two depths (A 2, B 3): the loop is unrolled by their period 6, the two ring
+    waits of an iteration share one barrier that leaves B's newest tile (8 DMAs per wave) in
+    flight, and the drain counter counts MMAs (a drain_index reads it) and is reduced per ring."""
+    name = "gemm_128_splitk_k128_b3"
+    src = kernels.lowerer(name).lower(kernels.kernel(name))
+    loop = src[src.index("for (; wir_base_i + 6 <="):src.index("pipe0.finish")]
+    assert loop.count("const int v_i = wir_base_i + ") == 6
+    assert loop.count("wir::wait_vm_barrier<8>();") == 7   # six copies and the remainder loop
+    assert "wir::wait_vm_barrier<" not in loop.replace("wir::wait_vm_barrier<8>();", "")
+    assert "wir_drain += 1;" in src and "(wir_drain % 2)" in src and "(wir_drain % 3)" in src
+    assert "const int v_i_d0_1 = wir_drain + 1;" in src

@@ -177,3 +177,39 @@ def test_wait_goes_before_first_use_not_after_load():
     last_mma = len(kinds) - 1 - kinds[::-1].index("MMAOp")
     assert kinds[last_mma - 1] == "WaitOp"
     assert [v.name for v in loop.body[last_mma - 1].values] == ["v_shared"]
+
+
+def _ring_slots(kernel) -> int:
+    from warpir_amd.ir import AllocSharedOp
+    return next(op.result.type.count for op in kernel.body if isinstance(op, AllocSharedOp))
+
+
+@pytest.mark.skipif(not HAVE_HIPCC, reason="needs hipcc")
+def test_kernel_pass_refuses_a_spilling_ring():
+    """Registers as a kernel_pass constraint.  The D=128 dK/dV kernel runs at one wave per
+    SIMD (512 registers per lane); with LDS for four 32 KiB ring slots the schedule asks for
+    four.  hipcc gives that ring 512 registers plus 139 spilled (the loop is unrolled by the
+    slot count, and each copy keeps its own LDS addresses), three slots 508 and no spill --
+    while the IR's liveness peak is 320 for every depth, because those address registers are
+    not IR values.  With the compiled count as the estimator and a 512 budget the pass gives
+    the four-slot form up and emits three slots; without a budget it keeps four."""
+    from warpir_amd.lowering import CDNA4Target
+    from warpir_amd.runtime import compiled_register_count
+
+    k = workloads.build_mha_bwd_dkdv_kernel(d=128, block_kv=128, block_q=64, wave_rows=32)
+    compiled = compiled_register_count(CDNA4Target(mfma_vgpr_form=True))
+    seen = {}
+
+    def estimate(kern):
+        seen[_ring_slots(kern)] = compiled(kern)
+        return seen[_ring_slots(kern)]
+
+    free = kernel_pass(k, cost_model=gfx950_attention_cost_model(128, 64, 128, lds_budget=128 * 1024,
+                                                                 min_stages=4))
+    assert _ring_slots(free) == 4
+    bounded = kernel_pass(k, cost_model=gfx950_attention_cost_model(128, 64, 128, lds_budget=128 * 1024,
+                                                                    min_stages=4, register_budget=512,
+                                                                    register_estimate=estimate))
+    assert _ring_slots(bounded) == 3
+    assert seen[4] > 512 >= seen[3], seen
+    assert count_registers(free).peak == count_registers(bounded).peak

@@ -107,3 +107,80 @@ def test_gfx950_cost_model_gives_three_stage_ring():
     assert loop.start == 2
     drains = [op for op in k.body if isinstance(op, MMABufOp)]
     assert len(drains) == 2
+
+
+# ---------------------------------------------------------------------------
+# per-ring depths (short-M GEMM: B streams from HBM, A stays in L2)
+# ---------------------------------------------------------------------------
+def _per_ring_gemm(lds_budget=160 * 1024):
+    from warpir_amd.passes.modulo_scheduler import gfx950_cost_model
+    ssa = build_gemm_kernel(block_m=128, block_n=128, block_k=128, wave_m=64, wave_n=64, name="gemm_splitk",
+                            split_k=True)
+    return ssa, kernel_pass(ssa, cost_model=gfx950_cost_model(128, 128, 128, lds_budget=lds_budget,
+                                                              hbm_sources=("B",)))
+
+
+def _ring_counts(kernel):
+    from warpir_amd.ir import AllocSharedOp
+    return {op.result.name: op.result.type.count for op in kernel.body if isinstance(op, AllocSharedOp)}
+
+
+def test_per_ring_depths_follow_each_loads_latency():
+    """B (16 units, from HBM) gets three 32 KiB slots and A (8 units, L2) two, filling 160 KiB.
+    Pinned by brute force over every pair of depths that fits: (A2, B3) leaves the least load
+    latency uncovered, max(latency - (slots - 1) * ii) with ii = 4 (the MMA's four units)."""
+    _ssa, k = _per_ring_gemm()
+    assert _ring_counts(k) == {"a_bufs": 2, "b_bufs": 3}
+    lat, ii, slot_bytes = {"a": 8, "b": 16}, 4, 32 * 1024
+    fits = [(a, b) for a in range(2, 8) for b in range(2, 8) if (a + b) * slot_bytes <= 160 * 1024]
+    exposed = {p: max(lat["a"] - (p[0] - 1) * ii, lat["b"] - (p[1] - 1) * ii) for p in fits}
+    best = min(exposed.values())
+    assert [p for p, e in exposed.items() if e == best] == [(2, 3)]
+    # with room for everything the rings take the depths the schedule asks for:
+    # A loaded as late as the MMA allows (two stages ahead), B four stages ahead
+    _ssa, wide = _per_ring_gemm(lds_budget=1 << 20)
+    assert _ring_counts(wide) == {"a_bufs": 3, "b_bufs": 5}
+
+
+def test_per_ring_form_interprets_bitwise_like_the_ssa_form():
+    """The per-ring buffer form (a stage-1 A load with its int_affine tile, waits per ring
+    depth, a drain_index load in the drain) computes what the SSA loop computes, bit for bit,
+    also for slices of one and two K tiles, where the drain consumes the prologue's slots."""
+    import torch
+
+    from oracle.ir_interp import run_kernel
+    ssa, pip = _per_ring_gemm()
+    for kc in (64, 128, 256, 384, 640, 1024):
+        s, m, n = 2, 128, 256
+        g = torch.Generator().manual_seed(kc)
+        a = (torch.randn(m, kc * s, generator=g) * 0.1).bfloat16()
+        b = (torch.randn(kc * s, n, generator=g) * 0.1).bfloat16()
+        outs = []
+        for kern in (ssa, pip):
+            c = torch.zeros(1, s, m, n)
+            run_kernel(kern, {"A": a.view(m, s, kc).permute(1, 0, 2).unsqueeze(0), "B": b.view(s, kc, n).unsqueeze(0),
+                              "C_global": c}, {"N": kc})
+            outs.append(c)
+        assert torch.equal(outs[0], outs[1]), kc
+        ref = torch.stack([a[:, j * kc:(j + 1) * kc].float() @ b[j * kc:(j + 1) * kc].float() for j in range(s)])
+        assert (outs[1][0] - ref).abs().max() < 1e-5
+
+
+def test_per_ring_form_structure():
+    """Loop body: one wait per ring depth, A's load of tile i - 1 through int_affine, B's of tile
+    i; the drain loads A's last tile through drain_index(+1)."""
+    from warpir_amd.ir import DrainIndexOp, IntAffineOp, TMALoadBufOp, WaitBufOp
+    from warpir_amd.printing import format_kernel
+    _ssa, k = _per_ring_gemm()
+    loop = next(op for op in k.body if isinstance(op, ForOp))
+    assert loop.start == 2
+    waits = [op for op in loop.body if isinstance(op, WaitBufOp)]
+    assert [(w.bufs[0].name, w.slot.offset, w.slot.modulus) for w in waits] == [("a_bufs", -2, 2), ("b_bufs", -2, 3)]
+    aff = [op for op in loop.body if isinstance(op, IntAffineOp)]
+    assert len(aff) == 1 and aff[0].add == -1
+    loads = {op.buf.name: op for op in loop.body if isinstance(op, TMALoadBufOp)}
+    assert loads["a_bufs"].coords[3] == aff[0].result and loads["a_bufs"].slot.offset == -1
+    assert loads["b_bufs"].slot.offset == 0 and loads["b_bufs"].slot.modulus == 3
+    drains = [op for op in k.body if isinstance(op, DrainIndexOp)]
+    assert len(drains) == 1 and drains[0].offset == 1
+    assert "drain_index(+1)" in format_kernel(k)

@@ -38,9 +38,10 @@ def gemm_variant(m: int, n: int, k: Optional[int] = None) -> str:
     return GEMM_VARIANT
 
 
-# 128x128 tiles, 128-deep K steps double-buffered in 128 KiB of LDS: each
-# slice's B panel streams with 64 KiB in flight per CU.
-SPLITK_GEMM_VARIANT = "gemm_128_splitk_k128"
+# 128x128 tiles, 128-deep K steps; kernel_pass sizes the rings per operand:
+# B (streamed from HBM) three slots loaded two steps ahead, A (the row panel
+# every program re-reads from L2) two slots, filling 160 KiB of LDS.
+SPLITK_GEMM_VARIANT = "gemm_128_splitk_k128_b3"
 _reduce_kernel = None
 
 

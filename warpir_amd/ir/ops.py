@@ -337,6 +337,21 @@ class IntDivOp(Op):
     divisor: Union[Value, int]
 
 
+@dataclass(frozen=True)
+class DrainIndexOp(Op):
+    """*Additive.* Integer ``result`` = the logical iteration of the next
+    buffered MMA (the drain counter, not reduced by any ring size) plus
+    ``offset``.
+
+    Lets a drain step of a pipeline whose rings differ in depth load a
+    later tile: a load scheduled ``k`` stages ahead of its MMA fetches
+    tile ``drain + k`` in the drain, as it would have in the loop.
+    """
+
+    result: Value
+    offset: int = 0
+
+
 # --- buffer operations (post-pipeline form) --------------------------------
 
 @dataclass(frozen=True)

@@ -45,7 +45,7 @@ from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence, Tuple, Union
 
 from warpir_amd.ir.ops import (
-    AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, CopyOp, DivRowOp, Exp2Op, ForOp,
+    AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, CopyOp, DivRowOp, DrainIndexOp, Exp2Op, ForOp,
     IntAffineOp, IntDivOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp, NegInftyOp,
     LazyMaxOp, Op, RowMaxOp, RowSumOp, SubColOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
     WaitBufOp, WaitOp, YieldOp, ZeroOp,
@@ -184,6 +184,7 @@ class CDNA4Lowerer:
         """Return HIP C++ for *kernel* (``lowering.py:67-81``)."""
         self._reset()
         self.kernel = kernel
+        self._drain_unreduced = any(isinstance(o, DrainIndexOp) for o in _walk(kernel.body))
         self._build_aliases(kernel.body)
         self._classify(kernel)
         self.geo = self._geometry(kernel)
@@ -307,6 +308,10 @@ class CDNA4Lowerer:
         self._stage_barrier_done = False
         self.globals: List[Value] = []
         self.drain_modulus: Optional[int] = None
+        # The drain counter counts buffered MMAs without reduction when a
+        # drain_index op reads it (rings of different depths); otherwise it
+        # is kept reduced by the one ring size.
+        self._drain_unreduced = False
         self._loop_of_yield: Dict[int, ForOp] = {}
         self._hoisted: Dict[str, Tuple[str, int]] = {}
         self._pending_hoist: Dict[str, tuple] = {}
@@ -574,7 +579,7 @@ class CDNA4Lowerer:
         if isinstance(slot, int):
             return str(slot)
         if slot.value is None:
-            return "wir_drain"
+            return f"(wir_drain % {slot.modulus})" if self._drain_unreduced else "wir_drain"
         m = slot.modulus
         name = self.resolve(slot.value.name)
         off = slot.offset + self._slot_shift.get(name, 0)
@@ -782,7 +787,15 @@ class CDNA4Lowerer:
         self._lazy_exact_only = False
 
     def _emit_ops(self, ops, out: List[str], depth: int) -> None:
-        for op in ops:
+        ops = list(ops)
+        for k, op in enumerate(ops):
+            if (isinstance(op, WaitBufOp) and k + 1 < len(ops) and isinstance(ops[k + 1], WaitBufOp)
+                    and id(op) not in self._pp_ops and id(ops[k + 1]) not in self._pp_ops):
+                # consecutive ring waits (rings of different depths) share one
+                # barrier: the last one waits for the fewest loads in flight
+                nxt = ops[k + 1]
+                self.wait_n[id(nxt)] = min(self.wait_n.get(id(op), 0), self.wait_n.get(id(nxt), 0))
+                continue
             self._emit_op(op, out, depth)
 
     def _emit_op(self, op: Op, out: List[str], depth: int) -> None:  # noqa: C901
@@ -905,7 +918,7 @@ class CDNA4Lowerer:
                 w(f"{pad}{self._var(op.result)} = {acc};")
             if isinstance(op.a_slot, BufSlotExpr):
                 self.drain_modulus = op.a_slot.modulus
-                w(f"{pad}wir_drain = (wir_drain + 1) % {op.a_slot.modulus};")
+                w(f"{pad}{self._drain_advance(op)}")
             return
         if isinstance(op, CopyOp):
             rt, it = op.result.type, op.input.type
@@ -1000,6 +1013,9 @@ class CDNA4Lowerer:
         if isinstance(op, IntDivOp):
             w(f"{pad}const int {self._var(op.result)} = ({self._int(op.input)}) / ({self._int(op.divisor)});")
             return
+        if isinstance(op, DrainIndexOp):
+            w(f"{pad}const int {self._var(op.result)} = wir_drain + {op.offset};")
+            return
         if isinstance(op, TMAStoreOp):
             self._emit_store(op, out, depth)
             return
@@ -1054,7 +1070,12 @@ class CDNA4Lowerer:
         if self._var(op.result) != acc:
             out.append(f"{pad}{self._var(op.result)} = {acc};")
         if isinstance(op.a_slot, BufSlotExpr):
-            out.append(f"{pad}wir_drain = (wir_drain + 1) % {op.a_slot.modulus};")
+            out.append(f"{pad}{self._drain_advance(op)}")
+
+    def _drain_advance(self, op: MMABufOp) -> str:
+        if self._drain_unreduced:
+            return "wir_drain += 1;"
+        return f"wir_drain = (wir_drain + 1) % {op.a_slot.modulus};"
 
     def _emit_yield(self, op: YieldOp, out: List[str], depth: int) -> None:
         pad = "  " * depth
@@ -1166,16 +1187,21 @@ class CDNA4Lowerer:
                 [f"{pad}{self._rotated[id(rotated[0])]}.finish({self._var(rotated[0].accum)});"], pad))
 
     def _ring_modulus(self, loop: ForOp) -> Optional[int]:
-        """Slot count of the ring slots this loop indexes by its induction variable."""
+        """Slot count of the ring slots this loop indexes by its induction
+        variable; for rings of different depths, their least common multiple
+        (the period after which every slot index repeats)."""
         iv = self.resolve(loop.induction_var.name)
         mods = set()
         for o in loop.body:
             for f in vars(o).values():
                 if isinstance(f, BufSlotExpr) and f.value is not None and self.resolve(f.value.name) == iv:
                     mods.add(f.modulus)
-        if len(mods) != 1:
+        if not mods:
             return None
-        return mods.pop()
+        m = 1
+        for x in mods:
+            m = m * x // math.gcd(m, x)
+        return m
 
     def _emit_loop(self, op: ForOp, stop: str, out: List[str], depth: int, mve: bool = True) -> None:
         """Emit the loop; ring loops are unrolled by their slot count S
@@ -1193,7 +1219,10 @@ class CDNA4Lowerer:
             self._emit_loop_lazy(op, stop, out, depth, fused_at)
             return
         m = self._ring_modulus(op) if self.target.mve and mve else None
-        if m is None or m < 2 or m > 4 or not isinstance(op.start, int) or op.step != 1:
+        # one ring size: unroll up to 4 copies; rings of different depths: up to their period 6
+        m_max = 4 if m is None or len({f.modulus for o in op.body for f in vars(o).values()
+                                        if isinstance(f, BufSlotExpr) and f.value is not None}) == 1 else 6
+        if m is None or m < 2 or m > m_max or not isinstance(op.start, int) or op.step != 1:
             out.append(f"{pad}for (int {iv} = {self._int(op.start)}; {iv} < {stop}; {iv} += {self._int(op.step)}) {{")
             self._emit_ops(op.body, out, depth + 1)
             out.append(f"{pad}}}")
@@ -2028,12 +2057,17 @@ class CDNA4Lowerer:
         body = [o for o in loop.body if not isinstance(o, YieldOp)]
         if not body or not isinstance(body[0], WaitBufOp):
             return None
+        nwait = next(k for k, o in enumerate(body + [None]) if not isinstance(o, WaitBufOp))
+        waits = body[:nwait]
         mmas = [o for o in body if isinstance(o, MMABufOp)]
-        rest = [o for o in body[1:] if not isinstance(o, (TMALoadBufOp, MMABufOp))]
+        rest = [o for o in body[nwait:] if not isinstance(o, (TMALoadBufOp, MMABufOp, IntAffineOp))]
         if len(mmas) != 1 or rest or body[-1] is not mmas[0]:
             return None
-        mma, wait = mmas[0], body[0]
-        if mma.a_slot != wait.slot or mma.b_slot != wait.slot:
+        mma = mmas[0]
+        # each operand's slot is the one its ring's wait names
+        slot_of = {self.resolve(b.name): w.slot for w in waits for b in w.bufs}
+        if (slot_of.get(self.resolve(mma.a_buf.name)) != mma.a_slot
+                or slot_of.get(self.resolve(mma.b_buf.name)) != mma.b_slot):
             return None
         t = self._rtype(mma.accum)
         k = mma.a_buf.type.tile_type.cols
@@ -2240,7 +2274,7 @@ class _Sim:
         if isinstance(s, int):
             return s
         if s.value is None:
-            return self.drain
+            return self.drain % s.modulus
         return (self.val(s.value) + s.offset) % s.modulus
 
     def key_of_tile(self, v: Value) -> Tuple[str, int]:
@@ -2298,7 +2332,9 @@ class _Sim:
                 self.read((low.resolve(op.a_buf.name), self.slot(op.a_slot)))
                 self.read((low.resolve(op.b_buf.name), self.slot(op.b_slot)))
                 if isinstance(op.a_slot, BufSlotExpr):
-                    self.drain = (self.drain + 1) % op.a_slot.modulus
+                    self.drain += 1
+            elif isinstance(op, DrainIndexOp):
+                self.env[low.resolve(op.result.name)] = self.drain + op.offset
             elif isinstance(op, IntAffineOp):
                 self.env[low.resolve(op.result.name)] = self.val(op.input) * op.mul + op.add
             elif isinstance(op, IntDivOp):

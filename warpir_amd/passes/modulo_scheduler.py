@@ -18,11 +18,12 @@ becomes LDS slots filled by ``global_load_lds`` DMA and the waits become
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Dict, List, Optional, Tuple
+from typing import Callable, Dict, List, Optional, Tuple
 
 from warpir_amd.ir.ops import (
     AllocSharedOp,
     BufSlotExpr,
+    DrainIndexOp,
     ForOp,
     IntAffineOp,
     Kernel,
@@ -38,7 +39,7 @@ from warpir_amd.ir.ops import (
     WaitOp,
     YieldOp,
 )
-from warpir_amd.ir.types import SharedBufferType
+from warpir_amd.ir.types import GPUType, SharedBufferType
 
 from . import _modsched_search
 
@@ -69,6 +70,31 @@ class CostModel:
     # can stall that wave for tens of cycles each; after the MMA they fall in
     # the shadow of its MFMAs, whose results the next op waits for anyway.
     loads_after_first_mma: bool = False
+    # Load latency per source global (by name), overriding the op type's:
+    # an operand that streams from HBM lands later than one that every
+    # program re-reads from L2.
+    source_latency: Dict[str, int] = field(default_factory=dict)
+    # Reference form: give every ring its own depth, the distance from its
+    # load's stage to the MMA's.  Loads are first moved as late as the
+    # schedule allows (their MMA's start minus their latency, where the load
+    # resource is free), so a ring holds only the tiles its latency needs;
+    # rings over ``lds_budget`` lose slots where the least latency is then
+    # exposed.  False keeps the reference's one depth for every ring.
+    per_ring_depth: bool = False
+    # LDS bytes per workgroup for the rings (per-ring depths).
+    lds_budget: Optional[int] = None
+    # Registers per lane the kernel may use, and an estimator of a rewritten
+    # kernel's registers per lane.  A ring depth whose kernel the estimator
+    # puts over the budget is not emitted; the pass takes the next shallower
+    # one (down to two slots).
+    register_budget: Optional[int] = None
+    register_estimate: Optional[Callable[["Kernel"], int]] = None
+
+    def load_latency(self, op) -> Optional[Tuple[str, int]]:
+        kind = self.latency.get(type(op))
+        if kind is not None and isinstance(op, TMALoadOp) and op.source.name in self.source_latency:
+            return kind[0], self.source_latency[op.source.name]
+        return kind
 
 
 REFERENCE_COST_MODEL = CostModel(latency=dict(LATENCY), resources=dict(RESOURCE_COUNTS))
@@ -76,7 +102,7 @@ REFERENCE_COST_MODEL = CostModel(latency=dict(LATENCY), resources=dict(RESOURCE_
 
 
 def gfx950_cost_model(block_m: int, block_n: int, block_k: int, load_units: int = 8,
-                      lds_budget: int = 160 * 1024) -> CostModel:
+                      lds_budget: int = 160 * 1024, hbm_sources: Tuple[str, ...] = ()) -> CostModel:
     """Cost model of one K-step on an MI355X CU, in units of 256 cycles.
 
     The MMA's latency is the block tile's MFMA time spread over the CU's 4
@@ -87,19 +113,28 @@ def gfx950_cost_model(block_m: int, block_n: int, block_k: int, load_units: int 
     2-slot ring.  ``load_units`` raises the load latency for schedules that
     keep more tiles in flight (12 units: a 4-slot ring at K=32).  The ring
     depth is capped by ``lds_budget`` bytes per workgroup.
+
+    ``hbm_sources`` names the operands that stream from HBM while the others
+    stay in L2 (short-M GEMM: every program re-reads the one A row panel,
+    and each B tile is read by one program).  Their loads take twice
+    ``load_units``, the L2-resident ones ``load_units``, and each ring gets
+    its own depth (``CostModel.per_ring_depth``).
     """
     mma_units = max(1, round(2 * block_m * block_n * block_k / (4 * 1024) / 256))
     stage_bytes = (block_m + block_n) * block_k * 2
     return CostModel(latency={TMALoadOp: ("tma", load_units), MMAOp: ("tc", mma_units),
                               TMAStoreOp: ("tma", load_units)},
-                     resources={"tma": 8, "tc": 1}, max_stages=max(2, lds_budget // stage_bytes))
+                     resources={"tma": 8, "tc": 1}, max_stages=max(2, lds_budget // stage_bytes),
+                     source_latency={name: 2 * load_units for name in hbm_sources},
+                     per_ring_depth=bool(hbm_sources), lds_budget=lds_budget)
 
 
 GFX950_COST_MODEL = gfx950_cost_model(256, 256, 32)
 
 
 def gfx950_attention_cost_model(block_q: int, block_kv: int, d: int, lds_budget: int = 64 * 1024,
-                                min_stages: int = 2) -> CostModel:
+                                min_stages: int = 2, register_budget: Optional[int] = None,
+                                register_estimate: Optional[Callable[[Kernel], int]] = None) -> CostModel:
     """Cost model of one FlashAttention KV step on an MI355X CU.
 
     Each of the two MMAs (S = Q K^T and O += P V) is ``2*block_q*block_kv*d``
@@ -107,13 +142,15 @@ def gfx950_attention_cost_model(block_q: int, block_kv: int, d: int, lds_budget:
     LDS budget per workgroup (64 KiB by default, so two workgroups share a
     CU and one's softmax overlaps the other's MFMAs).  ``min_stages`` = 3
     suits the 8-wavefront ping-pong lowering, which reads each V tile one
-    iteration after its K tile.
+    iteration after its K tile.  ``register_budget`` / ``register_estimate``
+    as in ``CostModel``: a ring too deep for the registers is not emitted.
     """
     mma_units = max(1, round(2 * block_q * block_kv * d / (4 * 1024) / 256))
     stage_bytes = 2 * block_kv * d * 2
     return CostModel(latency={TMALoadOp: ("tma", 8), MMAOp: ("tc", mma_units), TMAStoreOp: ("tma", 8)},
                      resources={"tma": 4, "tc": 1}, max_stages=max(2, lds_budget // stage_bytes),
-                     min_stages=min_stages, loads_after_first_mma=True)
+                     min_stages=min_stages, loads_after_first_mma=True, register_budget=register_budget,
+                     register_estimate=register_estimate)
 
 
 @dataclass
@@ -225,7 +262,7 @@ def _loop_instructions(loop: ForOp, cost: CostModel, transitive: bool = False) -
     """One ``MSInstruction`` per load / MMA / store, keyed by the op's text (``:183-217``)."""
     instrs: Dict[str, MSInstruction] = {}
     for op in loop.body:
-        kind = cost.latency.get(type(op))
+        kind = cost.load_latency(op)
         if kind is not None:
             instrs[str(op)] = MSInstruction(resource=kind[0], latency=kind[1], name=str(op),
                                             parent_edges=[])
@@ -283,81 +320,229 @@ def _reference_form_applies(loop: ForOp) -> bool:
     return True
 
 
-def _pipeline_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
+def _pipeline_loop(loop: ForOp, cost: CostModel,
+                   rebuild: Optional[Callable[[List[Op]], Kernel]] = None) -> Optional[List[Op]]:
     if not _reference_form_applies(loop) and any(isinstance(op, TMALoadOp) for op in loop.body):
-        return _prefetch_loop(loop, cost)
+        return _prefetch_loop(loop, cost, rebuild)
     instrs = _loop_instructions(loop, cost)
     manager = MSInstructionManager()
     for ins in instrs.values():
         manager.add_instruction(ins)
-    prologue, steady, epilogue, _ii, stages, stage_of = manager.solve(
+    prologue, _steady, _epilogue, ii, stages, stage_of = manager.solve(
         max_cycles=cost.max_cycles, depth=cost.depth, resource_counts=cost.resources)
     if prologue is None:
         return None
-    if cost.max_stages is not None and stages > cost.max_stages:
-        # The LDS budget holds fewer slots than the schedule wants: pull the
-        # late instructions forward to the last stage that fits.
-        stage_of = {n: min(st, cost.max_stages - 1) for n, st in stage_of.items()}
-        prologue, steady, epilogue, stages = _shape_from_stages(list(stage_of), stage_of, cost.depth)
-
-    by_name: Dict[str, Op] = {str(op): op for op in loop.body}
     loads = [op for op in loop.body if isinstance(op, TMALoadOp)]
     mmas = [op for op in loop.body if isinstance(op, MMAOp)]
     if not mmas:
         raise PipelineError("loop has no MMA to pipeline")
-    ring = {ld.result: Value(f"{ld.source.name.lower()}_bufs",
-                             SharedBufferType(tile_type=ld.result.type, count=stages))
-            for ld in loads}
+    loaded = {ld.result for ld in loads}
     for mma in mmas:
         for operand in (mma.a, mma.b):
-            if operand not in ring:
+            if operand not in loaded:
                 raise PipelineError(f"MMA operand {operand!r} is not loaded inside the loop")
-    all_rings = tuple(ring[ld.result] for ld in loads)
 
-    out: List[Op] = [AllocSharedOp(result=ring[ld.result]) for ld in loads]
-    # Fill: prologue step i loads logical iteration i - stage into slot i (:255-269).
-    for step, items in enumerate(prologue):
-        for logical, name in items:
-            op = by_name[name]
-            if isinstance(op, TMALoadOp):
-                fixed = op.substitute({loop.induction_var: logical})
-                out.append(TMALoadBufOp(buf=ring[op.result], slot=step, source=op.source,
-                                        coords=fixed.coords))
-
-    def slot_of(stage: int) -> BufSlotExpr:
-        return BufSlotExpr(value=loop.induction_var, offset=-stage, modulus=stages)
-
-    body: List[Op] = [WaitBufOp(bufs=all_rings, slot=slot_of(stage_of[str(mmas[0])]))]
-    for name, _offset in steady[0]:
-        op = by_name[name]
-        slot = slot_of(stage_of[name])
-        if isinstance(op, TMALoadOp):
-            body.append(TMALoadBufOp(buf=ring[op.result], slot=slot, source=op.source,
-                                     coords=op.coords))
-        elif isinstance(op, MMAOp):
-            body.append(MMABufOp(result=op.result, a_buf=ring[op.a], a_slot=slot,
-                                 b_buf=ring[op.b], b_slot=slot, accum=op.accum))
-    body.append(next(op for op in loop.body if isinstance(op, YieldOp)))
-    out.append(ForOp(induction_var=loop.induction_var, start=stages - 1, stop=loop.stop,
-                     step=loop.step, tile_size=loop.tile_size, iter_args=loop.iter_args,
-                     body=tuple(body), results=loop.results))
-
-    # Drain: step e waits on drain slot e and runs the MMAs still in flight (:329-356).
-    for e, items in enumerate(epilogue):
-        slot = BufSlotExpr(value=None, offset=e, modulus=stages)
-        out.append(WaitBufOp(bufs=all_rings, slot=slot))
-        for name, _offset in items:
-            op = by_name[name]
-            if not isinstance(op, MMAOp):
-                continue
-            k = next(j for j, ia in enumerate(loop.iter_args) if ia.block_arg == op.accum)
-            out.append(MMABufOp(result=Value(f"{op.result.name}_ep{e}", op.result.type),
-                                a_buf=ring[op.a], a_slot=slot, b_buf=ring[op.b], b_slot=slot,
-                                accum=loop.results[k]))
+    if cost.per_ring_depth and len(mmas) == 1:
+        plans = _ring_depth_plans(loop, cost, manager, instrs, ii, loads, mmas[0])
+    else:
+        if cost.max_stages is not None and stages > cost.max_stages:
+            # The LDS budget holds fewer slots than the schedule wants: pull the
+            # late instructions forward to the last stage that fits.
+            stage_of = {n: min(st, cost.max_stages - 1) for n, st in stage_of.items()}
+        stages = max(stage_of.values()) + 1
+        plans = [(stage_of, {str(ld): stages for ld in loads})]
+        if cost.register_budget is not None:
+            # shallower uniform rings for the register check: the loads keep
+            # their stage, the MMAs move one stage earlier per step
+            mma_names = {str(op) for op in mmas}
+            for depth in range(stages - 1, 1, -1):
+                st = {n: (min(v, depth - 1) if n in mma_names else v) for n, v in stage_of.items()}
+                plans.append((st, {str(ld): depth for ld in loads}))
+    out = None
+    for stage_plan, depths in plans:
+        out = _buffer_form(loop, stage_plan, depths, loads)
+        if _fits_registers(cost, rebuild, out):
+            return out
     return out
 
 
-def _prefetch_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
+def _fits_registers(cost: CostModel, rebuild: Optional[Callable[[List[Op]], Kernel]], ops: List[Op]) -> bool:
+    """Whether the kernel with this rewritten loop fits ``cost.register_budget``
+    (always true without a budget and an estimator)."""
+    if cost.register_budget is None or cost.register_estimate is None or rebuild is None:
+        return True
+    return cost.register_estimate(rebuild(ops)) <= cost.register_budget
+
+
+def _modulo_fits(instrs: Dict[str, MSInstruction], offsets: Dict[str, int], ii: int, depth: int,
+                 capacity: Dict[str, int]) -> bool:
+    """The solver's cumulative resource limits, for given offsets."""
+    usage: Dict[Tuple[str, int], int] = {}
+    for name, ins in instrs.items():
+        if ins.resource not in capacity:
+            continue
+        for d in range(depth):
+            for t in range(offsets[name] + d * ii, offsets[name] + d * ii + ins.latency):
+                usage[(ins.resource, t)] = usage.get((ins.resource, t), 0) + 1
+                if usage[(ins.resource, t)] > capacity[ins.resource]:
+                    return False
+    return True
+
+
+def _ring_depth_plans(loop: ForOp, cost: CostModel, manager: MSInstructionManager,
+                      instrs: Dict[str, MSInstruction], ii: int, loads: List[TMALoadOp], mma: MMAOp):
+    """Per-ring depths for the one-MMA reference form, deepest first.
+
+    Every load is moved as late as its MMA allows (the MMA's start minus the
+    load's latency, at the latest offset where the load resource is free),
+    so its ring needs ``stage(MMA) - stage(load) + 1`` slots.  Rings over the
+    LDS budget lose slots one at a time: each time the ring whose loss
+    leaves the least load latency uncovered,
+    ``max_r(latency_r - (slots_r - 1) * ii)``.  Further plans continue that
+    order down to two slots per ring (the register check's candidates).
+    Returns ``[(stage_of, slots_of_load)]``.
+    """
+    offsets = {name: manager.intervals[(0, name)][0] for name in instrs}
+    m_name = str(mma)
+    for ld in loads:
+        n = str(ld)
+        latest = offsets[m_name] - instrs[n].latency
+        for t in range(latest, offsets[n], -1):
+            trial = dict(offsets, **{n: t})
+            if _modulo_fits(instrs, trial, ii, cost.depth, cost.resources):
+                offsets = trial
+                break
+    s_m = offsets[m_name] // ii
+    want = {str(ld): max(2, s_m - offsets[str(ld)] // ii + 1) for ld in loads}
+    nbytes = {str(ld): _tile_nbytes(ld.result.type) for ld in loads}
+    lat = {str(ld): instrs[str(ld)].latency for ld in loads}
+
+    def exposed(depths) -> int:
+        return max(lat[n] - (d - 1) * ii for n, d in depths.items())
+
+    def shrink(depths):
+        options = [n for n, d in depths.items() if d > 2]
+        if not options:
+            return None
+        best = min(options, key=lambda n: (exposed(dict(depths, **{n: depths[n] - 1})), -nbytes[n],
+                                           list(depths).index(n)))
+        return dict(depths, **{best: depths[best] - 1})
+
+    depths = dict(want)
+    budget = cost.lds_budget
+    while budget is not None and sum(depths[n] * nbytes[n] for n in depths) > budget:
+        nxt = shrink(depths)
+        if nxt is None:
+            break
+        depths = nxt
+    plans = []
+    while depths is not None:
+        top = max(depths.values()) - 1
+        stage_of = {n: top - depths[n] + 1 for n in depths}
+        stage_of[m_name] = top
+        plans.append((stage_of, dict(depths)))
+        depths = shrink(depths) if cost.register_budget is not None else None
+    return plans
+
+
+def _tile_nbytes(t) -> int:
+    return t.rows * t.cols * (2 if t.data_type == GPUType.bf16 else 4)
+
+
+def _buffer_form(loop: ForOp, stage_of: Dict[str, int], depths: Dict[str, int],
+                 loads: List[TMALoadOp]) -> List[Op]:
+    """The reference buffer form (``:244-358``) for given stages and ring depths.
+
+    With one depth for every ring this is the reference rewrite: prologue
+    step ``p`` loads tile ``p - stage`` into its slot, the loop from
+    ``num_stages - 1`` waits on the MMA's slot, refills the slots its loads
+    own and runs the MMA, and drain step ``e`` waits on drain slot ``e``
+    and runs the MMAs still in flight.  With depths that differ, each ring
+    ``r`` of ``m_r`` slots holds tile ``t`` in slot ``t % m_r``: the loop
+    waits once per ring depth, a load ``k`` stages ahead of its MMA names
+    tile ``i - stage`` through an ``int_affine`` of the induction variable,
+    and in the drain it loads tile ``drain + k`` (``drain_index``).
+    """
+    iv = loop.induction_var
+    by_name: Dict[str, Op] = {str(op): op for op in loop.body}
+    names = list(by_name)
+    stages = max(stage_of.values()) + 1
+    ring = {ld.result: Value(f"{ld.source.name.lower()}_bufs",
+                             SharedBufferType(tile_type=ld.result.type, count=depths[str(ld)]))
+            for ld in loads}
+    mod = {ld.result: depths[str(ld)] for ld in loads}
+    groups: Dict[int, List[Value]] = {}
+    for ld in loads:
+        groups.setdefault(mod[ld.result], []).append(ring[ld.result])
+
+    out: List[Op] = [AllocSharedOp(result=ring[ld.result]) for ld in loads]
+    # Fill: prologue step p loads logical iteration p - stage (:255-269).
+    for step in range(stages - 1):
+        for name in names:
+            op = by_name[name]
+            st = stage_of.get(name)
+            if isinstance(op, TMALoadOp) and st is not None and st <= step:
+                fixed = op.substitute({iv: step - st})
+                out.append(TMALoadBufOp(buf=ring[op.result], slot=(step - st) % mod[op.result],
+                                        source=op.source, coords=fixed.coords))
+
+    def slot(v: Value, stage: int, value: Optional[Value] = None) -> BufSlotExpr:
+        if value is not None:
+            return BufSlotExpr(value=value, offset=0, modulus=mod[v])
+        return BufSlotExpr(value=iv, offset=-stage, modulus=mod[v])
+
+    mmas = [by_name[n] for n in names if isinstance(by_name[n], MMAOp)]
+    s_m = stage_of[str(mmas[0])]
+    body: List[Op] = [WaitBufOp(bufs=tuple(bufs), slot=BufSlotExpr(value=iv, offset=-s_m, modulus=m))
+                      for m, bufs in groups.items()]
+    shifted: Dict[int, Value] = {}
+    for name in names:
+        op = by_name[name]
+        st = stage_of.get(name)
+        if isinstance(op, TMALoadOp):
+            coords = op.coords
+            if st:
+                if st not in shifted:
+                    shifted[st] = Value(f"{iv.name}_s{st}", iv.type)
+                    body.append(IntAffineOp(result=shifted[st], input=iv, mul=1, add=-st))
+                coords = op.substitute({iv: shifted[st]}).coords
+            body.append(TMALoadBufOp(buf=ring[op.result], slot=slot(op.result, st), source=op.source,
+                                     coords=coords))
+        elif isinstance(op, MMAOp):
+            body.append(MMABufOp(result=op.result, a_buf=ring[op.a], a_slot=slot(op.a, st),
+                                 b_buf=ring[op.b], b_slot=slot(op.b, st), accum=op.accum))
+    body.append(next(op for op in loop.body if isinstance(op, YieldOp)))
+    out.append(ForOp(induction_var=iv, start=stages - 1, stop=loop.stop, step=loop.step,
+                     tile_size=loop.tile_size, iter_args=loop.iter_args, body=tuple(body),
+                     results=loop.results))
+
+    # Drain: step e waits on drain slot e and runs the MMAs still in flight
+    # (:329-356); a load k stages ahead of the MMA still fetches its tile.
+    for e in range(stages - 1):
+        waits = [WaitBufOp(bufs=tuple(bufs), slot=BufSlotExpr(value=None, offset=e, modulus=m))
+                 for m, bufs in groups.items()]
+        out.extend(waits)
+        for name in names:
+            op = by_name[name]
+            st = stage_of.get(name)
+            if st is None or st < e + 1:
+                continue
+            if isinstance(op, TMALoadOp):
+                ahead = Value(f"{iv.name}_d{e}_{s_m - st}", iv.type)
+                out.append(DrainIndexOp(result=ahead, offset=s_m - st))
+                out.append(TMALoadBufOp(buf=ring[op.result], slot=slot(op.result, st, ahead),
+                                        source=op.source, coords=op.substitute({iv: ahead}).coords))
+            elif isinstance(op, MMAOp):
+                k = next(j for j, ia in enumerate(loop.iter_args) if ia.block_arg == op.accum)
+                out.append(MMABufOp(result=Value(f"{op.result.name}_ep{e}", op.result.type),
+                                    a_buf=ring[op.a], a_slot=BufSlotExpr(value=None, offset=e, modulus=mod[op.a]),
+                                    b_buf=ring[op.b], b_slot=BufSlotExpr(value=None, offset=e, modulus=mod[op.b]),
+                                    accum=loop.results[k]))
+    return out
+
+
+def _prefetch_loop(loop: ForOp, cost: CostModel,
+                   rebuild: Optional[Callable[[List[Op]], Kernel]] = None) -> Optional[List[Op]]:
     """Buffer form for loops the reference rewrite cannot take: an MMA reads
     a loop-invariant tile (the resident Q of FlashAttention), a register
     value, or the body carries non-MMA work (the online-softmax chain).
@@ -370,7 +555,9 @@ def _prefetch_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
     by iteration ``i - 1``, and names the tiles it reads through
     ``slot_view``.  Loads past the end of the data read zeros (TMA
     out-of-bounds semantics), so no drain steps are needed: the last
-    ``S - 1`` iterations simply prefetch tiles that are never read.
+    ``S - 1`` iterations simply prefetch tiles that are never read.  With a
+    register budget, a depth whose kernel the estimator puts over it gives
+    way to the next shallower one (down to 2 slots).
     """
     instrs = _loop_instructions(loop, cost, transitive=True)
     manager = MSInstructionManager()
@@ -389,6 +576,16 @@ def _prefetch_loop(loop: ForOp, cost: CostModel) -> Optional[List[Op]]:
         stages = max(2, min(stages, cost.max_stages))
     if loop.step != 1:
         raise PipelineError("the prefetch form needs a unit step")
+    out: List[Op] = []
+    for depth in range(stages, 1, -1):
+        out = _prefetch_form(loop, cost, loads, depth)
+        if _fits_registers(cost, rebuild, out):
+            break
+    return out
+
+
+def _prefetch_form(loop: ForOp, cost: CostModel, loads: List[TMALoadOp], stages: int) -> List[Op]:
+    """``_prefetch_loop``'s rewrite for a ring of ``stages`` slots."""
     iv = loop.induction_var
     ring = {ld.result: Value(f"{ld.source.name.lower()}_bufs",
                              SharedBufferType(tile_type=ld.result.type, count=stages)) for ld in loads}
@@ -450,11 +647,17 @@ def kernel_pass(kernel: Kernel, cost_model: Optional[CostModel] = None) -> Kerne
     """
     cost = cost_model or REFERENCE_COST_MODEL
     body: List[Op] = []
-    for op in kernel.body:
+    for k, op in enumerate(kernel.body):
         if not isinstance(op, ForOp) or op.step != 1:
             body.append(op)
             continue
-        rewritten = _pipeline_loop(op, cost)
+
+        def rebuild(ops: List[Op], k=k) -> Kernel:
+            # the kernel with this loop rewritten as ``ops`` (for the register check)
+            return Kernel(name=kernel.name, inputs=kernel.inputs, outputs=kernel.outputs,
+                          body=tuple(body) + tuple(ops) + tuple(kernel.body[k + 1:]))
+
+        rewritten = _pipeline_loop(op, cost, rebuild)
         body.extend([op] if rewritten is None else rewritten)
     return Kernel(name=kernel.name, inputs=kernel.inputs, outputs=kernel.outputs, body=tuple(body))
 

@@ -16,6 +16,7 @@ from warpir_amd.ir.ops import (
     CausalMaskOp,
     CopyOp,
     DivRowOp,
+    DrainIndexOp,
     Exp2Op,
     ForOp,
     IntAffineOp,
@@ -133,6 +134,7 @@ _LINE: Dict[type, Callable[[Op], str]] = {
     LoadVecOp: lambda op: f"{op.result!r} = load_vec({op.source!r}, {_coords(op.coords)})",
     LazyMaxOp: lambda op: f"{op.result!r} = lazy_max({op.prev!r}, {op.cand!r}, {op.slack})",
     IntDivOp: lambda op: f"{op.result!r} = int_div({_coord(op.input)}, {_coord(op.divisor)})",
+    DrainIndexOp: lambda op: f"{op.result!r} = drain_index(+{op.offset})",
 }
 
 

@@ -193,6 +193,23 @@ def resource_usage(source: str) -> Dict[str, int]:
     return usage
 
 
+
+def compiled_register_count(target=None):
+    """A register estimator for ``CostModel.register_estimate``: the registers
+    per lane hipcc gives the kernel's gfx950 lowering (VGPRs + AGPRs + spilled
+    VGPRs), from the compile remarks.  Compiles through the code-object cache,
+    so each distinct kernel is compiled once.  ``target`` is the
+    ``CDNA4Target`` the kernel will be lowered with."""
+    from warpir_amd.lowering import CDNA4Lowerer
+
+    def estimate(kernel: Kernel) -> int:
+        src = CDNA4Lowerer(target).lower(kernel)
+        compile_source(src)
+        u = resource_usage(src)
+        return u.get("vgpr", 0) + u.get("agpr", 0) + u.get("vgpr_spill", 0)
+
+    return estimate
+
 # ---------------------------------------------------------------------------
 # kernel arguments
 # ---------------------------------------------------------------------------
