@@ -43,7 +43,7 @@ import torch
 from warpir_amd.ir import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, ColVecType, CopyOp, DivRowOp, DrainIndexOp, Exp2Op,
     ForOp, GPUType, IntAffineOp, IntDivOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp,
-    NegInftyOp, RegTileType, RowMaxOp, RowSumOp, RowVecType, SlotViewOp, SubColOp, SubOp, SubRowOp, LazyMaxOp,
+    NegInftyOp, PipelineStageOp, RegTileType, RowMaxOp, RowSumOp, RowVecType, SlotViewOp, SubColOp, SubOp, SubRowOp, LazyMaxOp,
     TMALoadBufOp, TMALoadOp, TMAStoreOp, Value, WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
 
@@ -161,7 +161,7 @@ class Interpreter:
 
     def _op(self, op) -> None:  # noqa: C901 - one branch per op kind
         g, s = self._get, self._set
-        if isinstance(op, (WaitOp, WaitBufOp, YieldOp)):
+        if isinstance(op, (WaitOp, WaitBufOp, YieldOp, PipelineStageOp)):
             return
         if isinstance(op, ZeroOp):
             s(op.result, torch.tensor(0.0))

@@ -108,8 +108,10 @@ def test_attention_overlap_form():
         assert body.count("wir::mma_rAB_slots") == 3
         assert "wir::e_pairs<0, 16>" in body                   # the peeled last tile
         assert ("causal_mask" in body) == ("causal" in name)
-    # eight-wave kernels are not matched
-    src = CDNA4Lowerer(CDNA4Target(attn_overlap=True)).lower(kernels.kernel("mha_d128"))
+    # eight-wave kernels are not matched, even with the overlapped placement
+    eight = kernels._mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
+                         rescale_slack=kernels.LAZY_SLACK, phases="mixed")
+    src = CDNA4Lowerer(CDNA4Target(lazy_softmax=False)).lower(eight)
     assert "mma_ABt_frags_slots" not in src[src.rindex('extern "C" __global__'):]
 
 

@@ -352,6 +352,24 @@ class DrainIndexOp(Op):
     offset: int = 0
 
 
+@dataclass(frozen=True)
+class PipelineStageOp(Op):
+    """*Additive.* Placement mark of a software-pipelined loop body: the ops
+    after it, up to the next mark or the yield, run ``stage`` iterations
+    later than the ops before the body's first mark -- each iteration
+    issues them for iteration ``i - stage``, ahead of its own stage-0 work.
+
+    It computes nothing: the loop means the same with or without it (the
+    interpreter skips it).  ``kernel_pass`` writes it from the modulo
+    schedule of the loop's compute ops, and the lowering follows it: with
+    the PV MMA behind a ``pipeline_stage(1)``, iteration ``i`` starts with
+    ``O += P_{i-1} V_{i-1}`` next to ``S_i = Q K_i^T``; with the softmax ops
+    behind it, tile ``i``'s softmax runs beside ``S_{i+1}``'s MFMAs.
+    """
+
+    stage: int = 1
+
+
 # --- buffer operations (post-pipeline form) --------------------------------
 
 @dataclass(frozen=True)

@@ -122,8 +122,9 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "mha_d64_causal_pp": lambda: _mha(64, 256, 64, 32, causal=True, lds_budget=128 * 1024, min_stages=4,
                                       rescale_slack=LAZY_SLACK),
     # software-pipelined attention loop (QK of tile i+1 and PV of tile i carry tile i's softmax)
-    "mha_d128_ovl": lambda: _mha(128, 128, 64, 32, causal=False, rescale_slack=8.0),
-    "mha_d64_causal_ovl": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=8.0, lds_budget=32 * 1024),
+    "mha_d128_ovl": lambda: _mha(128, 128, 64, 32, causal=False, rescale_slack=8.0, phases="mixed"),
+    "mha_d64_causal_ovl": lambda: _mha(64, 128, 64, 32, causal=True, rescale_slack=8.0, lds_budget=32 * 1024,
+                                       phases="mixed"),
     # FlashAttention backward: Dv = rowsum(dO * O); query-major dQ; key-major dK, dV.
     "mha_bwd_prep_d128": lambda: build_mha_bwd_prep_kernel(d=128, block_q=128, wave_rows=32),
     "mha_bwd_dq_d128": lambda: _bwd_dq(128, causal=False),
@@ -192,16 +193,23 @@ def _bwd_dq(d: int, causal: bool) -> Kernel:
 
 
 def _mha(d: int, block_q: int, block_kv: int, wave_rows: int, causal: bool, lds_budget: int = 64 * 1024,
-         min_stages: int = 2, rescale_slack: Optional[float] = None, gqa: bool = False) -> Kernel:
+         min_stages: int = 2, rescale_slack: Optional[float] = None, gqa: bool = False,
+         phases: Optional[str] = None) -> Kernel:
+    """Forward FlashAttention through kernel_pass.  The lazy-max kernels have
+    their softmax chain placed by the pass's phase schedule (``phases``,
+    default "auto": the MFMA / VALU phase alternation at their waves per
+    SIMD); the exact online-softmax kernels keep program order."""
     name = ("mha_fwd_causal" if causal else "mha_fwd") + ("_gqa" if gqa else "")
     k = build_mha_forward_kernel(d=d, block_q=block_q, block_kv=block_kv, wave_rows=wave_rows, causal=causal,
                                  name=name, rescale_slack=rescale_slack, gqa=gqa)
+    if phases is None and rescale_slack == LAZY_SLACK:
+        phases = "auto"
     return kernel_pass(k, cost_model=gfx950_attention_cost_model(block_q, block_kv, d, lds_budget=lds_budget,
-                                                                 min_stages=min_stages))
+                                                                 min_stages=min_stages, phase_schedule=phases))
 
 # Lowering options of variants that differ from the defaults.
 TARGETS: Dict[str, dict] = {
-    "mha_d128_ovl": {"attn_overlap": True, "lazy_softmax": False},
+    "mha_d128_ovl": {"lazy_softmax": False},
     "mha_d128_pp_swapped": {"wave_groups": {"k": 1, "v": 0}},
     "mha_d128_pp2b": {"pingpong_one_barrier": False},
     "mha_d128_u2": {"pingpong_barrier_every": 2},
@@ -219,7 +227,7 @@ TARGETS: Dict[str, dict] = {
     "gemm_256x128_ws_k32": {"warp_specialize": True, "rotate_mma": False},
     "gemm_256x128_ws_all": {"warp_specialize": True, "rotate_mma": False, "mve": False,
                             "wave_groups": {"a": 1, "b": 1}},
-    "mha_d64_causal_ovl": {"attn_overlap": True, "lazy_softmax": False},
+    "mha_d64_causal_ovl": {"lazy_softmax": False},
 }
 
 # The D=128 dK/dV kernels hold dK, dV and the score tiles in more than 256 registers.  With

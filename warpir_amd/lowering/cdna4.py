@@ -47,7 +47,7 @@ from typing import Dict, List, Optional, Sequence, Tuple, Union
 from warpir_amd.ir.ops import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, CopyOp, DivRowOp, DrainIndexOp, Exp2Op, ForOp,
     IntAffineOp, IntDivOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp, NegInftyOp,
-    LazyMaxOp, Op, RowMaxOp, RowSumOp, SubColOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
+    LazyMaxOp, Op, PipelineStageOp, RowMaxOp, RowSumOp, SubColOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
     WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
 from warpir_amd.ir.ops import SlotViewOp
@@ -97,10 +97,6 @@ class CDNA4Target:
     mve: bool = True
     # Final bf16 stores of register tiles go through LDS as whole rows.
     staged_stores: bool = True
-    # Attention loops (4 wavefronts, 2-slot K/V ring) as a software pipeline:
-    # S_{i+1} = Q K_{i+1}^T and O += P_i V_i each carry, MFMA by MFMA, a
-    # share of the softmax and running-max VALU work of the other tile.
-    attn_overlap: bool = False
     # Wave group (0 or 1) that issues each load stream (named by its ring,
     # e.g. "k", "v") in the 8-wavefront attention ping-pong.  None: take it
     # from the warp assigner's solution for the kernel (passes.warp_assigner).
@@ -329,6 +325,7 @@ class CDNA4Lowerer:
         self._ws = False                          # warp-specialised form (producer / consumer waves)
         self._softmax_fused: Dict[int, object] = {}  # id(op) -> fused lazy-softmax plan, or "skip"
         self._no_fusion = False                      # emit the fused groups' ops one by one
+        self._overlapped = False                     # an attention loop took the overlapped ("mixed") form
         self._lazy_exact_only = False                # fused groups emit only the exact half
         self._score_folds: Dict[int, dict] = {}      # id(QK MMA) -> fold of its lazy-softmax group
         self._fold_live = False                      # inside a fused loop whose ScoreBias is declared
@@ -807,7 +804,9 @@ class CDNA4Lowerer:
             if fused != "skip":
                 self._emit_lazy_softmax(fused, out, depth)
             return
-        if isinstance(op, (AllocSharedOp, YieldOp)):
+        if isinstance(op, (AllocSharedOp, YieldOp, PipelineStageOp)):
+            # a pipeline_stage mark is realised by the loop emitters that take
+            # its placement; elsewhere the loop runs in program order
             if isinstance(op, YieldOp):
                 self._emit_yield(op, out, depth)
             return
@@ -1250,11 +1249,12 @@ class CDNA4Lowerer:
         register assignment.  The first iteration always takes the exact path
         (the running max starts at -inf), so it is peeled.
 
-        When the ops after the step are the PV MMA (reading this iteration's
-        ring slot) and the yield, they are rotated to the top of the next
-        iteration, ahead of its wait: the exact path is then the softmax step
-        alone, and the prefetch that overwrites that slot still comes after the
-        barrier that follows the PV."""
+        When the ops after the step are a ``pipeline_stage(1)`` mark, the PV
+        MMA (reading this iteration's ring slot) and the yield -- kernel_pass
+        placed the PV one stage later -- the PV is rotated to the top of the
+        next iteration, ahead of its wait: the exact path is then the softmax
+        step alone, and the prefetch that overwrites that slot still comes
+        after the barrier that follows the PV."""
         pad = "  " * depth
         q = pad + "  "
         iv = self._var(op.induction_var)
@@ -1263,9 +1263,13 @@ class CDNA4Lowerer:
         fz = self._softmax_fused[id(body[fused_at])]
         pre = body[:fused_at]
         post = [o for o in body[fused_at + 1:] if self._softmax_fused.get(id(o)) != "skip"]
-        rotate = (isinstance(op.start, int) and op.step == 1 and len(post) == 2 and isinstance(post[0], MMAOp)
-                  and isinstance(post[1], YieldOp) and not post[0].transpose_b
+        # kernel_pass's placement: a pipeline_stage(1) in front of the PV MMA
+        rotate = (isinstance(op.start, int) and op.step == 1 and len(post) == 3
+                  and isinstance(post[0], PipelineStageOp) and post[0].stage == 1 and isinstance(post[1], MMAOp)
+                  and isinstance(post[2], YieldOp) and not post[1].transpose_b
                   and isinstance(pre[0], (WaitBufOp, WaitOp)))
+        if rotate:
+            post = post[1:]
 
         def fast_call(d: int) -> None:
             qq = "  " * d
@@ -1352,6 +1356,12 @@ class CDNA4Lowerer:
         mmas = [o for o in body if isinstance(o, MMAOp)]
         if len(mmas) != 2 or not mmas[0].transpose_b or mmas[1].transpose_b or body[-2] is not mmas[1]:
             return None
+        # the placement kernel_pass marks: the PV MMA one stage behind the rest
+        # (it runs at the top of the next iteration, beside S = Q K^T)
+        if not (isinstance(body[-3], PipelineStageOp) and body[-3].stage == 1):
+            return None
+        if any(isinstance(o, PipelineStageOp) for o in body[:-3]):
+            return None
         qk, pv = mmas
         views = self._views()
         vk, vv = views.get(self.resolve(qk.b.name)), views.get(self.resolve(pv.b.name))
@@ -1381,7 +1391,7 @@ class CDNA4Lowerer:
         affine = [o for o in body if isinstance(o, IntAffineOp)]
         if len(affine) != 1 or affine[0].mul != 1 or affine[0].add != S - 1:
             return None
-        mid = body[body.index(qk) + 1: body.index(pv)]
+        mid = body[body.index(qk) + 1: body.index(pv) - 1]
         lds_ops = (TMALoadOp, WaitOp, WaitBufOp, MMAOp, MMABufOp, SlotViewOp, ForOp)
         if any(isinstance(o, lds_ops) for o in mid):
             return None
@@ -1620,7 +1630,10 @@ class CDNA4Lowerer:
         return True
 
     def _attention_overlap_plan(self, loop: ForOp):
-        """Match the prefetch-form attention loop for the overlapped emitter.
+        """Match the prefetch-form attention loop for the overlapped emitter:
+        the placement ``kernel_pass`` marks by a ``pipeline_stage(1)`` between
+        S = Q K^T and the softmax ops (tile i's softmax and PV run beside
+        tile i+1's score MFMAs; the "mixed" phase schedule).
 
         Required: four wavefronts; body = wait on slot i, slot views, S = Q K^T
         with hoisted Q, one prefetch per ring into slot i + 1 of a 2-slot
@@ -1634,9 +1647,15 @@ class CDNA4Lowerer:
              carried values, constants and other M results.
         Every loop-carried value must be updated in place.
         """
-        if not self.target.attn_overlap or self.geo.nw != 4 or loop not in list(self.kernel.body):
+        if self.geo.nw != 4 or loop not in list(self.kernel.body):
             return None
         body = list(loop.body)
+        marks = [o for o in body if isinstance(o, PipelineStageOp)]
+        qk_at = next((k for k, o in enumerate(body) if isinstance(o, MMAOp)), None)
+        if len(marks) != 1 or marks[0].stage != 1 or qk_at is None or body.index(marks[0]) < qk_at:
+            return None
+        if not any(isinstance(o, (Exp2Op, RowSumOp)) for o in body[body.index(marks[0]):]):
+            return None
         if len(body) < 4 or not isinstance(body[0], WaitBufOp) or not isinstance(body[-1], YieldOp):
             return None
         if loop.start != 0 or loop.step != 1:
@@ -1683,7 +1702,7 @@ class CDNA4Lowerer:
         for v in (vk, vv):
             if v.slot.value is None or R(v.slot.value.name) != ivn or v.slot.offset % 2:
                 return None
-        skip = (TMALoadBufOp, IntAffineOp, SlotViewOp)
+        skip = (TMALoadBufOp, IntAffineOp, SlotViewOp, PipelineStageOp)
         mid = [o for o in body[body.index(qk) + 1: body.index(pv)] if not isinstance(o, skip)]
         if any(isinstance(o, (TMALoadOp, WaitOp, WaitBufOp, MMAOp, MMABufOp, ForOp)) for o in mid):
             return None
@@ -1775,7 +1794,7 @@ class CDNA4Lowerer:
                     m_ops=m_ops, rowmax=rowmaxes[0], k_load=k_load, v_load=v_load)
 
     def _emit_attention_overlap(self, loop: ForOp, stop: str, out: List[str], depth: int) -> bool:
-        """Software-pipelined attention loop (see ``CDNA4Target.attn_overlap``).
+        """Software-pipelined attention loop (the "mixed" phase placement).
 
         Tile j's scores S_j are computed one step ahead.  Step j (j + 1 < n):
           wait + barrier (K_{j+1} and V_j landed; every wave is done with
@@ -1792,6 +1811,7 @@ class CDNA4Lowerer:
         plan = self._attention_overlap_plan(loop)
         if plan is None:
             return False
+        self._overlapped = True
         R = self.resolve
         pad = "  " * depth
         ms = self.geo.ms
@@ -2170,7 +2190,7 @@ class CDNA4Lowerer:
             # more than two waves per SIMD only where as many workgroups fit in the LDS, and not in
             # the overlapped attention form (its second score tile is not in the register count)
             by_lds = self.target.lds_bytes // max(self.lds_total, 1024) * self.geo.nw // 4
-            wpe = 2 if self.target.attn_overlap else max(2, min(wpe, by_lds))
+            wpe = 2 if self._overlapped else max(2, min(wpe, by_lds))
         self.waves_per_simd = wpe
         nt = self.num_threads
         pid = _pid_code(dims, self.target, reverse_x=causal_x)

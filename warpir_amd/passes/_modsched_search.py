@@ -22,6 +22,12 @@ optimum with the smallest ``ii`` and, among those, the
 lexicographically smallest offsets in topological order -- a
 deterministic choice among
 CP-SAT's equally optimal answers.
+
+Additive: ``slot_class`` restricts instruction ``i`` to offsets with
+``offset % ii == slot_class[i]`` (``None`` = unrestricted), so an ``ii``
+of ``P`` slots can stand for a cycle of ``P`` phases that each admit one
+class of work (the attention loop's MFMA and VALU phases).  An ``ii`` at
+or below the largest class is skipped.
 """
 from __future__ import annotations
 
@@ -33,7 +39,7 @@ class Problem:
 
     def __init__(self, latencies: Sequence[int], resources: Sequence[str],
                  edges: Sequence[Tuple[int, int, int]], depth: int, max_cycles: int,
-                 capacity: Dict[str, int]):
+                 capacity: Dict[str, int], slot_class: Optional[Sequence[Optional[int]]] = None):
         self.lat = list(latencies)
         self.res = list(resources)
         self.edges = list(edges)  # (parent, child, distance)
@@ -41,6 +47,7 @@ class Problem:
         self.max_cycles = max_cycles
         self.cap = dict(capacity)
         self.n = len(self.lat)
+        self.slot_class = list(slot_class) if slot_class is not None else [None] * self.n
 
 
 def _topo_order(p: Problem) -> List[int]:
@@ -77,7 +84,8 @@ def solve(p: Problem) -> Optional[Tuple[int, List[int], int]]:
     order = _topo_order(p)
     best: Optional[Tuple[int, List[int], int]] = None
     span_floor = max(p.lat)  # any schedule spans at least its longest interval
-    for ii in range(0, p.max_cycles):
+    min_ii = max([c + 1 for c in p.slot_class if c is not None], default=0)
+    for ii in range(min_ii, p.max_cycles):
         base = (p.depth - 1) * ii
         if base + span_floor > p.max_cycles - 1:
             break
@@ -143,9 +151,12 @@ def _best_offsets(p: Problem, order: List[int], ii: int, limit: int):
         for b, k in outof[i]:
             if assigned[b] and b != i:
                 hi = min(hi, s[b] + k * ii - p.lat[i])
+        cls = p.slot_class[i]
         for v in range(lo, hi + 1):
             if max(span, v + p.lat[i]) >= best[0]:
                 break  # this and every later offset cannot beat the incumbent
+            if cls is not None and v % ii != cls:
+                continue
             s[i] = v
             assigned[i] = True
             if place(i, +1):

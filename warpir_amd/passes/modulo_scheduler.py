@@ -21,16 +21,32 @@ from dataclasses import dataclass, field
 from typing import Callable, Dict, List, Optional, Tuple
 
 from warpir_amd.ir.ops import (
+    AddOp,
     AllocSharedOp,
     BufSlotExpr,
+    CausalMaskOp,
+    CopyOp,
+    DivRowOp,
     DrainIndexOp,
+    Exp2Op,
     ForOp,
     IntAffineOp,
     Kernel,
+    LazyMaxOp,
+    Log2Op,
     MMABufOp,
     MMAOp,
+    MulOp,
+    MulRowOp,
+    MulScalarOp,
     Op,
+    PipelineStageOp,
+    RowMaxOp,
+    RowSumOp,
     SlotViewOp,
+    SubColOp,
+    SubOp,
+    SubRowOp,
     TMALoadBufOp,
     TMALoadOp,
     TMAStoreOp,
@@ -39,7 +55,7 @@ from warpir_amd.ir.ops import (
     WaitOp,
     YieldOp,
 )
-from warpir_amd.ir.types import GPUType, SharedBufferType
+from warpir_amd.ir.types import ColVecType, GPUType, RegTileType, RowVecType, SharedBufferType
 
 from . import _modsched_search
 
@@ -89,6 +105,15 @@ class CostModel:
     # one (down to two slots).
     register_budget: Optional[int] = None
     register_estimate: Optional[Callable[["Kernel"], int]] = None
+    # Prefetch form: schedule the loop's compute ops -- the MMAs and the
+    # softmax chain -- into MFMA and VALU phases (``_phase_stages``) and mark
+    # the placement with ``pipeline_stage``.  "alternate": an iteration of a
+    # wavefront is an MFMA phase then a VALU phase, the other wavefronts on
+    # its SIMD filling each phase's idle unit; "mixed": one phase in which a
+    # wavefront co-issues its VALU work beside its own MFMAs; "auto": the one
+    # with the shorter estimated iteration (``phase_estimates``) at the
+    # kernel's waves per SIMD.  None keeps the compute ops in program order.
+    phase_schedule: Optional[str] = None
 
     def load_latency(self, op) -> Optional[Tuple[str, int]]:
         kind = self.latency.get(type(op))
@@ -134,7 +159,8 @@ GFX950_COST_MODEL = gfx950_cost_model(256, 256, 32)
 
 def gfx950_attention_cost_model(block_q: int, block_kv: int, d: int, lds_budget: int = 64 * 1024,
                                 min_stages: int = 2, register_budget: Optional[int] = None,
-                                register_estimate: Optional[Callable[[Kernel], int]] = None) -> CostModel:
+                                register_estimate: Optional[Callable[[Kernel], int]] = None,
+                                phase_schedule: Optional[str] = None) -> CostModel:
     """Cost model of one FlashAttention KV step on an MI355X CU.
 
     Each of the two MMAs (S = Q K^T and O += P V) is ``2*block_q*block_kv*d``
@@ -144,13 +170,14 @@ def gfx950_attention_cost_model(block_q: int, block_kv: int, d: int, lds_budget:
     suits the 8-wavefront ping-pong lowering, which reads each V tile one
     iteration after its K tile.  ``register_budget`` / ``register_estimate``
     as in ``CostModel``: a ring too deep for the registers is not emitted.
+    ``phase_schedule`` as in ``CostModel``: the softmax chain's placement.
     """
     mma_units = max(1, round(2 * block_q * block_kv * d / (4 * 1024) / 256))
     stage_bytes = 2 * block_kv * d * 2
     return CostModel(latency={TMALoadOp: ("tma", 8), MMAOp: ("tc", mma_units), TMAStoreOp: ("tma", 8)},
                      resources={"tma": 4, "tc": 1}, max_stages=max(2, lds_budget // stage_bytes),
                      min_stages=min_stages, loads_after_first_mma=True, register_budget=register_budget,
-                     register_estimate=register_estimate)
+                     register_estimate=register_estimate, phase_schedule=phase_schedule)
 
 
 @dataclass
@@ -547,7 +574,10 @@ def _prefetch_loop(loop: ForOp, cost: CostModel,
     a loop-invariant tile (the resident Q of FlashAttention), a register
     value, or the body carries non-MMA work (the online-softmax chain).
 
-    The loop keeps every compute op in place; only its loads move.  With
+    The loads move into a ring; the compute ops keep program order unless
+    the cost model asks for a phase schedule (``CostModel.phase_schedule``),
+    which places every MMA and softmax op by its unit and marks the
+    placement with ``pipeline_stage`` (``_place_phases``).  With
     ``S`` ring slots chosen by the modulo schedule (the MMAs' stage behind
     their loads, at least 2, at most ``cost.max_stages``), the prologue
     loads tiles ``start .. start+S-2``; iteration ``i`` waits on slot
@@ -581,6 +611,14 @@ def _prefetch_loop(loop: ForOp, cost: CostModel,
         out = _prefetch_form(loop, cost, loads, depth)
         if _fits_registers(cost, rebuild, out):
             break
+    if cost.phase_schedule is not None:
+        from .register_counter import count_registers
+        waves = count_registers(rebuild(out)).waves_per_simd if rebuild is not None else 2
+        rewritten = out[-1]
+        body = _place_phases(rewritten, list(rewritten.body), cost, waves)
+        out[-1] = ForOp(induction_var=rewritten.induction_var, start=rewritten.start, stop=rewritten.stop,
+                        step=rewritten.step, iter_args=rewritten.iter_args, body=tuple(body),
+                        results=rewritten.results, tile_size=rewritten.tile_size)
     return out
 
 
@@ -635,15 +673,160 @@ def _prefetch_form(loop: ForOp, cost: CostModel, loads: List[TMALoadOp], stages:
     return out
 
 
+# ---------------------------------------------------------------------------
+# Phase scheduling of an attention loop's compute ops
+# ---------------------------------------------------------------------------
+# gfx950 issue costs per wavefront, in shader cycles (in-bounds probes):
+MFMA_CYCLES = 32            # one v_mfma_f32_32x32x16_bf16 (32.004 measured back to back)
+VALU_CYCLES = 4             # one wave64 fp32 VALU instruction
+TRANS_CYCLES = 8            # v_exp_f32 / v_log_f32: about two FMAs' cost beside an MFMA
+COISSUE_PER_MFMA = 4        # independent VALU instructions an MFMA hides on its own wavefront
+DEPENDENT_VALU_CYCLES = 10  # a lone wavefront's dependent VALU chain: one instruction per ~10 cycles
+
+_VALU_OPS = (CopyOp, MulScalarOp, SubOp, MulOp, AddOp, Exp2Op, Log2Op, RowMaxOp, RowSumOp, SubRowOp,
+             MulRowOp, DivRowOp, LazyMaxOp, CausalMaskOp, SubColOp)
+
+
+def op_unit(op: Op) -> Optional[str]:
+    """The SIMD unit a compute op of a loop body occupies: "mfma" for an MMA,
+    "valu" for the element-wise, row and column ops of the softmax chain,
+    None for ops that cost nothing there (zero fills, index arithmetic,
+    waits, views, loads)."""
+    if isinstance(op, MMAOp):
+        return "mfma"
+    if isinstance(op, _VALU_OPS):
+        return "valu"
+    return None
+
+
+def _lane_elems(t) -> int:
+    if isinstance(t, RegTileType):
+        return max(1, t.rows * t.cols // 64)
+    if isinstance(t, ColVecType):
+        return max(1, t.rows // 32)
+    if isinstance(t, RowVecType):
+        return max(1, t.cols // 2)
+    return 1
+
+
+def op_cycles(op: Op) -> int:
+    """Issue cycles of one wavefront's share of a compute op: MFMAs of the
+    32x32x16 shape for an MMA (its per-wavefront result tile times the
+    reduction depth), VALU instructions for the softmax chain (one per fp32
+    element a lane holds; transcendentals count two; the bf16 pack converts
+    two per instruction; a row reduction adds its cross-lane swap)."""
+    if isinstance(op, MMAOp):
+        t = op.result.type
+        k = op.a.type.cols
+        return max(1, t.rows * t.cols * k // (32 * 32 * 16)) * MFMA_CYCLES
+    if isinstance(op, (RowMaxOp, RowSumOp)):
+        return (_lane_elems(op.tile.type) + 1) * VALU_CYCLES
+    e = _lane_elems(op.result.type)
+    if isinstance(op, (Exp2Op, Log2Op)):
+        return e * TRANS_CYCLES
+    if isinstance(op, CopyOp) and getattr(op.result.type, "data_type", None) == GPUType.bf16:
+        return max(1, e // 2) * VALU_CYCLES
+    return e * VALU_CYCLES
+
+
+def phase_estimates(ops: List[Op], waves_per_simd: int) -> Dict[str, int]:
+    """Estimated SIMD cycles per iteration of all ``waves_per_simd``
+    wavefronts for the two phase structures.  "alternate": each wavefront's
+    MFMA phase runs beside the others' VALU phases, so the SIMD is bound by
+    the larger of its total MFMA and VALU time (and one wavefront's own
+    sequence).  "mixed": each wavefront co-issues up to COISSUE_PER_MFMA
+    VALU instructions per MFMA, and the rest of its chain issues at the lone
+    wavefront's dependent rate; the wavefronts then take turns."""
+    mfma = sum(op_cycles(o) for o in ops if op_unit(o) == "mfma")
+    valu = sum(op_cycles(o) for o in ops if op_unit(o) == "valu")
+    w = max(1, waves_per_simd)
+    alternate = max(w * mfma, w * valu, mfma + valu)
+    hidden = COISSUE_PER_MFMA * (mfma // MFMA_CYCLES) * VALU_CYCLES
+    own = mfma + max(0, valu - hidden) * DEPENDENT_VALU_CYCLES // VALU_CYCLES
+    return {"alternate": alternate, "mixed": w * own}
+
+
+def _phase_stages(loop: ForOp, body: List[Op], mode: str) -> Dict[int, int]:
+    """Stage of each compute op of ``body`` (by ``id``) in a modulo schedule
+    of phases.
+
+    Every MMA and softmax op is an ``MSInstruction`` on its unit.  With
+    "alternate" the initiation interval is two slots, an MFMA phase (slot 0)
+    and a VALU phase (slot 1): ``slot_class`` pins MMAs to even and VALU ops
+    to odd offsets.  With "mixed" it is one slot holding both.  An MMA's
+    result is ready in the next slot (latency 1); VALU ops chain inside
+    their slot (latency 0).  Data dependences have distance 0, values
+    carried through the loop's iter_args distance 1.  The exact search
+    (``_modsched_search``) returns the smallest interval and the earliest
+    offsets; an op's stage is its offset divided by the interval, counted
+    from the earliest compute op.
+    """
+    ops = [o for o in body if op_unit(o) is not None]
+    if not ops:
+        return {}
+    index = {id(o): k for k, o in enumerate(ops)}
+    producer = {o.result: o for o in ops if isinstance(getattr(o, "result", None), Value)}
+    yld = next(o for o in body if isinstance(o, YieldOp))
+    carried = {ia.block_arg: yld.values[k] for k, ia in enumerate(loop.iter_args)}
+    edges = []
+    for o in ops:
+        for name, v in vars(o).items():
+            if name == "result" or not isinstance(v, Value):
+                continue
+            if v in producer:
+                edges.append((index[id(producer[v])], index[id(o)], 0))
+            elif v in carried and carried[v] in producer:
+                edges.append((index[id(producer[carried[v]])], index[id(o)], 1))
+    units = [op_unit(o) for o in ops]
+    if mode == "alternate":
+        slot_class = [0 if u == "mfma" else 1 for u in units]
+    elif mode == "mixed":
+        slot_class = [0] * len(ops)
+    else:
+        raise ValueError(f"phase schedule {mode!r}: expected 'alternate' or 'mixed'")
+    problem = _modsched_search.Problem(
+        latencies=[1 if u == "mfma" else 0 for u in units], resources=units, edges=edges,
+        depth=DEPTH, max_cycles=64, capacity={}, slot_class=slot_class)
+    found = _modsched_search.solve(problem)
+    if found is None:
+        raise PipelineError("the loop's compute ops have no phase schedule")
+    ii, offsets, _span = found
+    first = min(offsets) // ii
+    return {id(o): off // ii - first for o, off in zip(ops, offsets)}
+
+
+def _place_phases(loop: ForOp, body: List[Op], cost: CostModel, waves_per_simd: int) -> List[Op]:
+    """``body`` reordered by the phase schedule: stage-0 ops in program
+    order, then ``pipeline_stage(s)`` and the stage-``s`` ops, then the
+    yield.  Ops that are no compute op (waits, views, index arithmetic,
+    loads, zero fills) stay at stage 0."""
+    mode = cost.phase_schedule
+    if mode == "auto":
+        est = phase_estimates([o for o in body if op_unit(o)], waves_per_simd)
+        mode = "mixed" if est["mixed"] < est["alternate"] else "alternate"
+    stages = _phase_stages(loop, body, mode)
+    last = max(stages.values(), default=0)
+    if last == 0:
+        return body
+    yld = body[-1]
+    out = [o for o in body[:-1] if stages.get(id(o), 0) == 0]
+    for st in range(1, last + 1):
+        out.append(PipelineStageOp(stage=st))
+        out.extend(o for o in body[:-1] if stages.get(id(o), 0) == st)
+    out.append(yld)
+    return out
+
+
 def kernel_pass(kernel: Kernel, cost_model: Optional[CostModel] = None) -> Kernel:
     """Pipeline every top-level unit-step loop of *kernel* (``:168-358``).
 
     Loops whose schedule has no solution are kept unchanged, as in the
-    reference.  Loops of loads and MMAs get the reference's buffer form;
-    loops with a softmax chain, loop-invariant or register MMA operands
-    (FlashAttention) get the prefetch form of ``_prefetch_loop`` where the
-    reference raises ``KeyError`` (``:309``).  ``cost_model`` defaults to
-    the reference's constants.
+    reference.  Loops of loads and MMAs get the reference's buffer form
+    (with per-ring depths when the cost model asks); loops with a softmax
+    chain, loop-invariant or register MMA operands (FlashAttention) get the
+    prefetch form of ``_prefetch_loop`` where the reference raises
+    ``KeyError`` (``:309``), with the softmax chain phase-scheduled when the
+    cost model asks.  ``cost_model`` defaults to the reference's constants.
     """
     cost = cost_model or REFERENCE_COST_MODEL
     body: List[Op] = []
@@ -664,4 +847,4 @@ def kernel_pass(kernel: Kernel, cost_model: Optional[CostModel] = None) -> Kerne
 
 __all__ = ["MSInstructionEdge", "MSInstruction", "MSInstructionManager", "PipelineError",
            "CostModel", "REFERENCE_COST_MODEL", "GFX950_COST_MODEL", "gfx950_cost_model",
-           "gfx950_attention_cost_model", "kernel_pass"]
+           "gfx950_attention_cost_model", "kernel_pass", "op_unit", "op_cycles", "phase_estimates"]

@@ -31,6 +31,7 @@ from warpir_amd.ir.ops import (
     MulScalarOp,
     NegInftyOp,
     Op,
+    PipelineStageOp,
     RowMaxOp,
     RowSumOp,
     SlotViewOp,
@@ -135,6 +136,7 @@ _LINE: Dict[type, Callable[[Op], str]] = {
     LazyMaxOp: lambda op: f"{op.result!r} = lazy_max({op.prev!r}, {op.cand!r}, {op.slack})",
     IntDivOp: lambda op: f"{op.result!r} = int_div({_coord(op.input)}, {_coord(op.divisor)})",
     DrainIndexOp: lambda op: f"{op.result!r} = drain_index(+{op.offset})",
+    PipelineStageOp: lambda op: f"pipeline_stage({op.stage})",
 }
 
 
