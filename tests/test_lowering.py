@@ -236,13 +236,18 @@ def test_warp_specialized_gemm_form():
             assert line.strip().startswith(("if (wir_producer)", "if (!wir_producer)")), line
     assert body.count("if (!wir_producer) {") >= 3
     assert low.launch_config(k, {"A": (512, 512), "B": (512, 512), "C_global": (512, 512)}).block == (512, 1, 1)
-    # the warp assigner places A with the MMA and B on another warp: the MFMA waves issue A,
-    # the DMA waves B, and each set waits on its own share of the in-flight DMAs
-    assert "if (!wir_producer) wir::Loader<wir::STile<256, 64, 0>, 4>::load" in body
-    assert "if (wir_producer) wir::Loader<wir::STile<64, 128, 1>, 4>::load" in body
-    assert "if (wir_producer) wir::wait_vm_barrier<4>(); else wir::wait_vm_barrier<8>();" in body
+    # the warp assigner's steady-state assignment with the gfx950 costs puts both streams on the
+    # DMA waves: the same kernel as the forced _all split
     allp = kernels.lowerer("gemm_256x128_ws_all").lower(kernels.kernel("gemm_256x128_ws_all"))
     assert "if (!wir_producer) wir::Loader" not in allp and "wir::wait_vm_barrier<12>();" in allp
+    assert src == allp
+    # the split the reference demo's constants give (_ab): the MFMA waves issue A, the DMA waves
+    # B, and each set waits on its own share of the in-flight DMAs
+    ab = kernels.lowerer("gemm_256x128_ws_ab").lower(kernels.kernel("gemm_256x128_ws_ab"))
+    ab = ab[ab.rindex('extern "C" __global__'):]
+    assert "if (!wir_producer) wir::Loader<wir::STile<256, 64, 0>, 4>::load" in ab
+    assert "if (wir_producer) wir::Loader<wir::STile<64, 128, 1>, 4>::load" in ab
+    assert "if (wir_producer) wir::wait_vm_barrier<4>(); else wir::wait_vm_barrier<8>();" in ab
     # the same kernel without the option is the plain 4-wave form
     plain = kernels.lowerer("gemm_256x128").lower(kernels.kernel("gemm_256x128"))
     assert "wir_producer" not in plain

@@ -98,3 +98,28 @@ def test_ir_connected_assignment_of_pipelined_gemm():
     assert sol is not None and sol.makespan > 0
     # the MMA chain never pays the sync cost: every MMA sits on the MMA type's warp
     assert len({sol.warp_of[str(i)] for i in ins if i.name == "mma"}) == 1
+
+
+def test_gfx950_costs_give_the_measured_faster_split():
+    """With the gfx950 costs (an LDS-DMA instruction stalls its issuing wave ~20 cycles, an MFMA
+    32, a tile lands ~2048 cycles after issue, a barrier between wave sets ~80; units of 32
+    cycles) the steady-state periods of the warp-specialised 256x128 GEMM rank the splits as
+    the timings do: both streams on the DMA waves (ws_all, 1113 TFLOP/s) ahead of A with the
+    MFMA waves and B on the DMA waves (1015) -- the reference demo's constants chose the
+    latter.  Periods by hand: the MMA warp issues 32 units of MFMAs, A's DMAs take 5 units of
+    its issuing wave (32 KiB over 4 waves: 8 instructions), B's 3 (4 instructions); each
+    3-slot ring needs (32 + issue + 64 + sync 3 off the MMA warp) / 3."""
+    from warpir_amd import kernels
+    from warpir_amd.passes.warp_assigner import assign_streams, gfx950_wave_costs, steady_state_period
+
+    k = kernels.kernel("gemm_256x128_ws")
+    c = gfx950_wave_costs(k)
+    assert (c.load_issue, c.mma_issue, c.load_latency, c.sync) == ({"a_load": 5, "b_load": 3}, 32, 64, 3)
+    period = {(a, b): steady_state_period(k, {"a_load": a, "b_load": b, "mma": 0}, c)
+              for a in (0, 1) for b in (0, 1)}
+    assert period[(1, 1)] == pytest.approx((32 + 5 + 64 + 3) / 3)
+    assert period[(0, 1)] == 37 and period[(0, 0)] == 40 and period[(1, 0)] == 35
+    assert assign_streams(k, c).type_warp == {"a_load": 1, "b_load": 1, "mma": 0}
+    # the reference demo's constants over the one-iteration window keep A with the MMA
+    from warpir_amd.passes.warp_assigner import assign_waves
+    assert assign_waves(k, num_warps=2, iterations=1).type_warp == {"a_load": 0, "b_load": 1, "mma": 0}

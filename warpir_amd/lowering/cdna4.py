@@ -244,18 +244,18 @@ class CDNA4Lowerer:
         """Ring buffers whose loads the DMA-only waves issue; the MFMA waves
         issue the others.  The split comes from ``CDNA4Target.wave_groups``
         (stream -> group; group 1 = DMA waves) or, when that is None, from the
-        warp assigner: a load type placed on the MMA's warp stays with the
-        MFMA waves, one placed on another warp goes to the DMA waves.  None
-        if the vmcnt thresholds do not split between the two sets."""
+        warp assigner's steady-state assignment with the gfx950 costs (each
+        stream's DMA issue stalls the wave that issues it): a load type placed
+        on the MMA's warp stays with the MFMA waves, one placed on another
+        warp goes to the DMA waves.  None if the vmcnt thresholds do not split
+        between the two sets."""
         def stream(buf_name: str) -> str:
             return buf_name[:-len("_bufs")] if buf_name.endswith("_bufs") else buf_name
         bufs = sorted({self.resolve(op.buf.name) for op in _walk(kernel.body) if isinstance(op, TMALoadBufOp)})
         groups = self.target.wave_groups
         if groups is None:
-            from warpir_amd.passes.warp_assigner import assign_waves
-            sol = assign_waves(kernel, num_warps=2, iterations=ASSIGN_ITERATIONS)
-            if sol is None:
-                return None
+            from warpir_amd.passes.warp_assigner import assign_streams, gfx950_wave_costs
+            sol = assign_streams(kernel, gfx950_wave_costs(kernel, waves_per_group=self.geo.nw), num_warps=2)
             mma_warp = next((w for t, w in sol.type_warp.items() if t.startswith("mma")), 0)
             groups = {t[:-len("_load")]: int(w != mma_warp) for t, w in sol.type_warp.items() if t.endswith("_load")}
         producers = {b for b in bufs if groups.get(stream(b), 1) == 1}

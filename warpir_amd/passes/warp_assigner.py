@@ -249,8 +249,62 @@ class _BranchAndBound:
 # ---------------------------------------------------------------------------
 # IR-connected entry point
 # ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class WaveCosts:
+    """Costs of the unrolled instructions, in one time unit: how long an
+    instruction keeps its warp busy (``cuda_latency``) and how long until its
+    result is usable (``total_latency``), per load stream and for the MMAs,
+    and the synchronisation cost of a dependence across warps."""
+
+    load_issue: Dict[str, int]
+    load_latency: int
+    mma_issue: int
+    mma_latency: int
+    sync: int
+    default_load_issue: int = 1
+
+
+# The reference demo's constants (warp_assigner.py:147-152; load 12, MMA 4, sync 80), with
+# every instruction holding its warp for one cycle.
+REFERENCE_WAVE_COSTS = WaveCosts(load_issue={}, load_latency=12, mma_issue=1, mma_latency=4, sync=80)
+
+# gfx950 measurements, in shader cycles: a global_load_lds_dwordx4 (1 KiB per wave) stalls the
+# issuing wave ~20 cycles; a 32x32x16 bf16 MFMA occupies its SIMD 32 cycles; an LDS-DMA tile
+# lands ~2048 cycles after issue under load; a workgroup barrier between two wave sets ~80.
+DMA_ISSUE_CYCLES = 20
+DMA_LANDING_CYCLES = 2048
+BARRIER_CYCLES = 80
+
+
+def gfx950_wave_costs(kernel, waves_per_group: int = 4, unit: int = 32) -> WaveCosts:
+    """Costs of *kernel*'s pipelined loop on gfx950 in units of ``unit``
+    cycles (one MFMA): each load stream keeps its issuing wave busy for its
+    DMA instructions (tile bytes / 1 KiB spread over ``waves_per_group``
+    waves, ~20 cycles each), and the MMA keeps its wave busy for its MFMAs
+    (the per-wavefront result tile times the reduction depth)."""
+    from warpir_amd.ir.ops import ForOp, MMABufOp, TMALoadBufOp
+
+    loop = next((op for op in kernel.body if isinstance(op, ForOp)), None)
+    if loop is None:
+        raise ValueError("kernel has no loop")
+    issue = {}
+    for op in loop.body:
+        if isinstance(op, TMALoadBufOp):
+            t = op.buf.type.tile_type
+            instr = max(1, t.rows * t.cols * 2 // 1024 // waves_per_group)
+            issue[op.buf.name.replace("_bufs", "") + "_load"] = -(-instr * DMA_ISSUE_CYCLES // unit)
+    mma = next(op for op in loop.body if isinstance(op, MMABufOp))
+    acc = mma.accum.type
+    k = mma.a_buf.type.tile_type.cols
+    cycles = max(1, acc.rows * acc.cols * k // (32 * 32 * 16)) * 32
+    mma_units = -(-cycles // unit)
+    return WaveCosts(load_issue=issue, load_latency=-(-DMA_LANDING_CYCLES // unit), mma_issue=mma_units,
+                     mma_latency=mma_units, sync=-(-BARRIER_CYCLES // unit))
+
+
 def instructions_from_pipeline(kernel, iterations: int = 4, ii: Optional[int] = None,
-                               load_latency: int = 12, mma_latency: int = 4) -> List[WAInstruction]:
+                               load_latency: int = 12, mma_latency: int = 4,
+                               costs: Optional[WaveCosts] = None) -> List[WAInstruction]:
     """Unroll the steady state of *kernel*'s pipelined loop into WAInstructions.
 
     Loads (``tma_load_buf``) are asynchronous with ``load_latency``; MMAs
@@ -258,8 +312,12 @@ def instructions_from_pipeline(kernel, iterations: int = 4, ii: Optional[int] = 
     iteration ``k`` consumes the loads of the slot it waits on, as the
     buffer form's slot expressions say, and the accumulator chains MMA to
     MMA.  A load that refills a slot is ordered after the MMA that last
-    read it (the buffer form's write-after-read rule).
+    read it (the buffer form's write-after-read rule).  ``costs`` (a
+    ``WaveCosts``) replaces the latencies and sets how long each
+    instruction keeps its warp busy (one cycle without it).
     """
+    if costs is not None:
+        load_latency, mma_latency = costs.load_latency, costs.mma_latency
     from warpir_amd.ir.ops import BufSlotExpr, ForOp, MMABufOp, MMAOp, TMALoadBufOp
 
     loop = next((op for op in kernel.body if isinstance(op, ForOp)), None)
@@ -285,7 +343,8 @@ def instructions_from_pipeline(kernel, iterations: int = 4, ii: Optional[int] = 
     for t in range(total):
         for j, op in enumerate(loads):
             name = op.buf.name.replace("_bufs", "") + "_load"
-            ld[(t, j)] = WAInstruction(name, t, [], [], True, 1, load_latency, t * ii)
+            busy = costs.load_issue.get(name, costs.default_load_issue) if costs is not None else 1
+            ld[(t, j)] = WAInstruction(name, t, [], [], True, busy, load_latency, t * ii)
     for t in range(total):
         for j, op in enumerate(mmas):
             tile = t  # logical tile consumed by this MMA copy
@@ -296,7 +355,8 @@ def instructions_from_pipeline(kernel, iterations: int = 4, ii: Optional[int] = 
                 parents.append(mm[(t - 1, j)])
             if j > 0:
                 parents.append(mm[(t, j - 1)])
-            mm[(t, j)] = WAInstruction("mma" if len(mmas) == 1 else f"mma{j}", t, parents, [], False, 1,
+            mm[(t, j)] = WAInstruction("mma" if len(mmas) == 1 else f"mma{j}", t, parents, [], False,
+                                       costs.mma_issue if costs is not None else 1,
                                        mma_latency, (t + distance) * ii + j * mma_latency)
     for (t, j), ins in ld.items():
         if t - stages >= 0 and (t - stages, 0) in mm:
@@ -306,14 +366,19 @@ def instructions_from_pipeline(kernel, iterations: int = 4, ii: Optional[int] = 
 
 
 def assign_waves(kernel, num_warps: int = 2, synchronization_cost: int = 80, iterations: int = 4,
-                 max_cycles: int = 500, verbose: bool = False) -> Optional[WASolution]:
+                 max_cycles: int = 500, verbose: bool = False,
+                 costs: Optional[WaveCosts] = None) -> Optional[WASolution]:
     """Solve the warp assignment of *kernel*'s pipelined loop.
 
     Types are pinned as in the reference demo (every load stream and the
     MMA each get one warp), so the answer is a producer / consumer split:
     which wave group issues which load stream relative to the MMAs.
+    ``costs`` (e.g. ``gfx950_wave_costs(kernel)``) replaces the reference
+    demo's latencies and its ``synchronization_cost``.
     """
-    instrs = instructions_from_pipeline(kernel, iterations=iterations)
+    if costs is not None:
+        synchronization_cost = costs.sync
+    instrs = instructions_from_pipeline(kernel, iterations=iterations, costs=costs)
     mgr = WAInstructionManager()
     for ins in instrs:
         mgr.add_instruction(ins)
@@ -328,5 +393,59 @@ def assign_waves(kernel, num_warps: int = 2, synchronization_cost: int = 80, ite
     return sol
 
 
-__all__ = ["WAInstruction", "WAInstructionManager", "WASolution", "instructions_from_pipeline",
-           "assign_waves"]
+def steady_state_period(kernel, type_warp: Dict[str, int], costs: WaveCosts) -> float:
+    """Cycles (in ``costs``' unit) per iteration of *kernel*'s pipelined loop
+    in steady state with the load streams and the MMA on the warps
+    ``type_warp`` names: the busiest warp's issue time per iteration (each
+    stream's DMA issue plus the MMA's), the accumulator recurrence (one MMA
+    per iteration), and each ring's recurrence -- the MMA frees a slot, the
+    stream refills it (issue, landing, and the synchronisation when the
+    stream is on another warp than the MMA), and the MMA reads it again
+    ``slots`` iterations later."""
+    from warpir_amd.ir.ops import ForOp, TMALoadBufOp
+
+    loop = next(op for op in kernel.body if isinstance(op, ForOp))
+    slots = {op.buf.name.replace("_bufs", "") + "_load": op.buf.type.count
+             for op in loop.body if isinstance(op, TMALoadBufOp)}
+    mma_warp = type_warp["mma"]
+    busy: Dict[int, float] = {}
+    busy[mma_warp] = float(costs.mma_issue)
+    period = float(costs.mma_latency)
+    for name, n in slots.items():
+        issue = costs.load_issue.get(name, costs.default_load_issue)
+        w = type_warp[name]
+        busy[w] = busy.get(w, 0.0) + issue
+        sync = costs.sync if w != mma_warp else 0
+        period = max(period, (costs.mma_latency + issue + costs.load_latency + sync) / n)
+    return max(period, max(busy.values()))
+
+
+def assign_streams(kernel, costs: WaveCosts, num_warps: int = 2) -> WASolution:
+    """Warp of every load stream and of the MMA that minimises the loop's
+    steady-state period (``steady_state_period``), by enumeration (the MMA
+    on warp 0; ties go to fewer streams off the MMA's warp).  The exact
+    makespan search over an unrolled window (``assign_waves``) does not see
+    a stream's per-iteration issue cost until the window spans a ring's
+    refill, and that window is out of its reach for these loops; the
+    period is what a loop's throughput follows.  ``makespan`` holds the
+    period."""
+    import itertools
+
+    from warpir_amd.ir.ops import ForOp, TMALoadBufOp
+
+    loop = next(op for op in kernel.body if isinstance(op, ForOp))
+    streams = sorted({op.buf.name.replace("_bufs", "") + "_load" for op in loop.body
+                      if isinstance(op, TMALoadBufOp)})
+    best = None
+    for warps in itertools.product(range(num_warps), repeat=len(streams)):
+        tw = dict(zip(streams, warps), mma=0)
+        key = (steady_state_period(kernel, tw, costs), sum(1 for w in warps if w != 0), warps)
+        if best is None or key < best[0]:
+            best = (key, tw)
+    (period, _off, _w), tw = best
+    return WASolution(makespan=period, warp_of={}, start_of={}, type_warp=tw)
+
+
+__all__ = ["WAInstruction", "WAInstructionManager", "WASolution", "WaveCosts", "REFERENCE_WAVE_COSTS",
+           "gfx950_wave_costs", "instructions_from_pipeline", "assign_waves", "steady_state_period",
+           "assign_streams"]
