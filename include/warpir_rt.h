@@ -35,7 +35,7 @@ typedef void* wir_function_t; /* a kernel inside a module (hipFunction_t) */
 typedef void* wir_event_t;    /* a timing event (hipEvent_t)              */
 
 /* ABI version of this header; bumped on any signature change. */
-#define WIR_RT_ABI_VERSION 3
+#define WIR_RT_ABI_VERSION 4
 int wir_abi_version(void);
 
 /* Make `device` current for the calling thread. */
@@ -101,6 +101,21 @@ const char* wir_error_string(int code);
 int wir_gemm_splitk(wir_function_t gemm, wir_function_t reduce, const void* a, const void* b,
                     void* out, void* workspace, size_t workspace_floats, int m, int n, int k,
                     int splits, void* stream);
+
+/* out[M][N] (bf16) = a[M][K] @ b[K][N] (bf16, row-major, contiguous) as
+ * `splits` K slices in ONE launch: `gemm` is a fused split-K variant
+ * (gemm_128_splitk_fused) whose last slice to store a 128x128 output tile
+ * sums the tile's fp32 partials (in `workspace`, as for wir_gemm_splitk) in
+ * slice order and writes the bf16 tile.  `arrivals` holds one 32-bit
+ * counter per output tile, at least ceil(M/128) * ceil(N/128) of its
+ * `arrival_count`, all zero before the call; the kernel leaves them zero.
+ * Calls that share `workspace` or `arrivals` must be ordered (one stream).
+ * The reference has no split-K path; this is the host side of
+ * warpir_amd.api.gemm_split_k with its fused variant.  Same limits as
+ * wir_gemm_splitk. */
+int wir_gemm_splitk_fused(wir_function_t gemm, const void* a, const void* b, void* out, void* workspace,
+                          size_t workspace_floats, void* arrivals, size_t arrival_count, int m, int n,
+                          int k, int splits, void* stream);
 
 /* out[M][N] (bf16) = a[M][K] @ b[K][N] (bf16, row-major, contiguous) as
  * `splits` K slices plus an fp32 reduction, with no device allocation: the

@@ -200,3 +200,46 @@ def test_split_k_per_ring_depth_agrees(gpu, m, n, k, splits):
     torch.cuda.synchronize()
     assert torch.equal(c, ref)
     assert rel_err(c.cpu(), gemm_ref(a.cpu(), b.cpu())) <= TOL
+
+
+@pytest.mark.parametrize("m,n,k,splits", [(128, 8192, 8192, 4), (128, 1024, 512, 4), (96, 384, 384, 2),
+                                          (128, 256, 8256, 3), (300, 520, 2048, 4), (64, 512, 1024, 16)])
+def test_split_k_fused_reduction_agrees(gpu, m, n, k, splits):
+    """One launch, the last slice of each output tile summing the partials (reduce_slices),
+    against the two-launch form (same GEMM, separate reduction kernel): both add the fp32
+    partials in slice order from 0, so bitwise equal.  Three products in a row on the same
+    counters, which the kernel leaves at zero."""
+    from warpir_amd import api
+
+    announce(f"split-K fused reduction {m}x{n}x{k} splits={splits}")
+    a = seeded_normal((m, k), 94, 0.1).cuda()
+    b = seeded_normal((k, n), 95, 0.1).cuda()
+    ref = api.gemm_split_k(a, b, splits=splits, variant=api.SPLITK_TWO_LAUNCH_VARIANT)
+    for it in range(3):
+        c = api.gemm_split_k(a, b, splits=splits, variant=api.SPLITK_FUSED_VARIANT)
+        torch.cuda.synchronize()
+        assert torch.equal(c, ref), it
+    stream = torch.cuda.current_stream().cuda_stream
+    arr = api._arrivals[(a.device.index, stream)]
+    assert int(arr.abs().sum()) == 0
+    assert rel_err(c.cpu(), gemm_ref(a.cpu(), b.cpu())) <= TOL
+
+
+def test_split_k_fused_on_two_streams(gpu):
+    """Products on two streams keep separate arrival counters; each matches the two-launch form."""
+    from warpir_amd import api
+
+    m, n, k, splits = 128, 2048, 4096, 4
+    announce(f"split-K fused on two streams {m}x{n}x{k}")
+    a = seeded_normal((m, k), 96, 0.1).cuda()
+    b = seeded_normal((k, n), 97, 0.1).cuda()
+    ref = api.gemm_split_k(a, b, splits=splits, variant=api.SPLITK_TWO_LAUNCH_VARIANT)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    for s in (s1, s2):
+        with torch.cuda.stream(s):
+            outs.append(api.gemm_split_k(a, b, splits=splits, variant=api.SPLITK_FUSED_VARIANT))
+    torch.cuda.synchronize()
+    assert all(torch.equal(o, ref) for o in outs)
+    assert (a.device.index, s1.cuda_stream) in api._arrivals and (a.device.index, s2.cuda_stream) in api._arrivals

@@ -300,11 +300,11 @@ def test_c_abi_library_exports_every_declared_symbol():
         pytest.skip("libwarpir_rt.so not built (run __graft_entry__.build())")
     lib = ctypes.CDLL(LIB_PATH)
     syms = _declared_symbols()
-    assert len(syms) == 17
+    assert len(syms) == 18
     for s in syms:
         assert hasattr(lib, s), s
     lib.wir_abi_version.restype = ctypes.c_int
-    assert lib.wir_abi_version() == 3
+    assert lib.wir_abi_version() == 4
     lib.wir_error_string.restype = ctypes.c_char_p
     assert lib.wir_error_string(0)
 

@@ -130,3 +130,30 @@ def test_causal_first_row_attends_only_to_first_key():
     q, k, v = (seeded_normal((1, 1, 64, 64), s) for s in (7, 8, 9))
     o, _ = attention_ref(q, k, v, causal=True)
     assert torch.allclose(o[0, 0, 0], v[0, 0, 0].float(), atol=1e-6)
+
+
+def test_fused_split_k_interprets_as_the_slice_sum():
+    """reduce_slices: after all slices of a ragged 200 x 384 product (2 x 3 tiles, 3 slices),
+    C holds bf16 of the partials summed in slice order from 0 -- what the two-launch
+    reduction computes -- and every arrival counter is back at zero."""
+    from warpir_amd.passes.modulo_scheduler import gfx950_cost_model
+    from warpir_amd.printing import format_kernel
+    from warpir_amd.workloads import build_gemm_kernel
+    k = kernel_pass(build_gemm_kernel(block_m=128, block_n=128, block_k=128, wave_m=64, wave_n=64, name="gemm_splitk",
+                                      split_k=True, fused_reduce=True),
+                    cost_model=gfx950_cost_model(128, 128, 128, lds_budget=160 * 1024, hbm_sources=("B",)))
+    assert "reduce_slices(%C_global" in format_kernel(k)
+    s, m, n, kc = 3, 200, 384, 256
+    a = seeded_normal((m, kc * s), 31, 0.1)
+    b = seeded_normal((kc * s, n), 32, 0.1)
+    part = torch.zeros(1, s, m, n)
+    out = torch.full((1, 1, m, n), float("nan"), dtype=torch.bfloat16)
+    arrivals = torch.zeros(6, dtype=torch.int64)
+    run_kernel(k, {"A": a.view(m, s, kc).permute(1, 0, 2).unsqueeze(0), "B": b.view(s, kc, n).unsqueeze(0),
+                   "C_global": part, "C": out, "Arrivals": arrivals}, {"N": kc})
+    total = torch.zeros(m, n)
+    for j in range(s):
+        total = total + part[0, j]
+    assert torch.equal(out[0, 0], total.bfloat16())
+    assert int(arrivals.abs().sum()) == 0
+    assert rel_err(out[0, 0], gemm_ref(a, b)) <= 1e-2

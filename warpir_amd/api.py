@@ -40,9 +40,45 @@ def gemm_variant(m: int, n: int, k: Optional[int] = None) -> str:
 
 # 128x128 tiles, 128-deep K steps; kernel_pass sizes the rings per operand:
 # B (streamed from HBM) three slots loaded two steps ahead, A (the row panel
-# every program re-reads from L2) two slots, filling 160 KiB of LDS.
-SPLITK_GEMM_VARIANT = "gemm_128_splitk_k128_b3"
+# every program re-reads from L2) two slots, filling 160 KiB of LDS.  The
+# slices are summed by the separate reduction kernel (two launches in one C
+# call), also the form of wir_gemm_splitk_noalloc.
+SPLITK_TWO_LAUNCH_VARIANT = "gemm_128_splitk_k128_b3"
+SPLITK_GEMM_VARIANT = SPLITK_TWO_LAUNCH_VARIANT
+# The same GEMM summing the slices itself (one launch: the last slice to store
+# an output tile adds the partials).  Correct, but slower on MI355X: its
+# device-scope release and acquire write back and invalidate an XCD's whole
+# L2 per workgroup (58 against 38 microseconds at M=128, N=K=8192).
+SPLITK_FUSED_VARIANT = "gemm_128_splitk_fused"
 _reduce_kernel = None
+# Zeroed per-tile arrival counters of the fused split-K kernels, one buffer
+# per (device, stream): the kernel leaves them zero, so launches ordered on
+# one stream share a buffer and launches on different streams never do.
+_arrivals: dict = {}
+_arrivals_lock = __import__("threading").Lock()
+
+
+def _arrival_counters(device, stream: int, count: int):
+    import torch
+
+    key = (device.index, stream)
+    with _arrivals_lock:
+        buf = _arrivals.get(key)
+        if buf is None or buf.numel() < count:
+            buf = torch.zeros(max(count, 256), dtype=torch.int32, device=device)
+            _arrivals[key] = buf
+        return buf
+
+
+_fused_variants: dict = {}
+
+
+def _fused(variant: str) -> bool:
+    """Whether the split-K variant sums its slices itself (a reduce_slices op)."""
+    from warpir_amd.ir import ReduceSlicesOp
+    if variant not in _fused_variants:
+        _fused_variants[variant] = any(isinstance(op, ReduceSlicesOp) for op in kernels.handle(variant).kernel.body)
+    return _fused_variants[variant]
 
 
 def splitk_count(m: int, n: int, k: int, num_cus: int = 256) -> int:
@@ -79,6 +115,8 @@ def _splitk_functions(variant: str):
                              "(128x128 tiles, 256 threads)")
         _splitk_checked.add(variant)
     h.load()
+    if _fused(variant):
+        return h._function, None
     if _reduce_kernel is None:
         _reduce_kernel = RawKernel("splitk_reduce.hsaco", "wir_splitk_reduce")
     _reduce_kernel._load()
@@ -88,7 +126,10 @@ def _splitk_functions(variant: str):
 def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None, variant: Optional[str] = None):
     """``out = a @ b`` as ``splits`` K slices run side by side (``blockIdx.z``)
     plus an fp32 reduction: the form for short M and long K, where the
-    output alone has too few tiles to fill the chip.  ``workspace`` is an
+    output alone has too few tiles to fill the chip.  The default variant
+    sums the slices with the separate reduction kernel; the fused variant
+    (``SPLITK_FUSED_VARIANT``) sums them inside the GEMM kernel (one launch,
+    per-tile arrival counters kept per device and stream).  ``workspace`` is an
     fp32 tensor of at least ``splits * M * N`` elements (allocated if
     omitted); ``variant`` names a split-K kernel variant (default
     ``SPLITK_GEMM_VARIANT``)."""
@@ -128,6 +169,14 @@ def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None, v
         raise ValueError("gemm_split_k: a, b, out and workspace must be 16-byte aligned")
     gemm_fn, reduce_fn = _splitk_functions(variant or SPLITK_GEMM_VARIANT)
     stream = torch.cuda.current_stream(a.device).cuda_stream
+    if reduce_fn is None:   # the slices are summed inside the GEMM kernel
+        tiles = math.ceil(m / 128) * math.ceil(n / 128)
+        arr = _arrival_counters(a.device, stream, tiles)
+        check(library().wir_gemm_splitk_fused(gemm_fn, a.data_ptr(), b.data_ptr(), out.data_ptr(),
+                                              workspace.data_ptr(), workspace.numel(), arr.data_ptr(),
+                                              arr.numel(), m, n, k, splits, ctypes.c_void_p(stream)),
+              "wir_gemm_splitk_fused")
+        return out
     check(library().wir_gemm_splitk(gemm_fn, reduce_fn, a.data_ptr(), b.data_ptr(), out.data_ptr(),
                                     workspace.data_ptr(), workspace.numel(), m, n, k, splits,
                                     ctypes.c_void_p(stream)), "wir_gemm_splitk")
@@ -138,8 +187,10 @@ NOALLOC_SCRATCH_FLOATS = 8 * 1024 * 1024   # WIR_NOALLOC_SCRATCH_FLOATS of inclu
 
 
 def gemm_split_k_noalloc(a, b, out, splits: Optional[int] = None, stream=None):
-    """``out = a @ b`` by the same two kernels as ``gemm_split_k``, with the
-    fp32 partials in the native library's own device scratch: no device
+    """``out = a @ b`` by the split-K GEMM and the separate reduction kernel
+    (``SPLITK_TWO_LAUNCH_VARIANT``; the same sums, bit for bit, as
+    ``gemm_split_k``), with the fp32 partials in the native library's own
+    device scratch: no device
     memory is allocated (``wir_gemm_splitk_noalloc``).  ``out`` is required.
     Raises ``HipError`` when ``splits * M * N`` exceeds the scratch
     (``NOALLOC_SCRATCH_FLOATS``).  Calls that overlap on one device share the
@@ -161,7 +212,7 @@ def gemm_split_k_noalloc(a, b, out, splits: Optional[int] = None, stream=None):
             raise ValueError(f"gemm_split_k_noalloc: {name} must be a contiguous bf16 {list(shape)} tensor")
     if not a.is_cuda or b.device != a.device or out.device != a.device:
         raise ValueError("gemm_split_k_noalloc: a, b and out must be on one GPU")
-    gemm_fn, reduce_fn = _splitk_functions(SPLITK_GEMM_VARIANT)
+    gemm_fn, reduce_fn = _splitk_functions(SPLITK_TWO_LAUNCH_VARIANT)
     if stream is None:
         stream = torch.cuda.current_stream(a.device).cuda_stream
     elif hasattr(stream, "cuda_stream"):

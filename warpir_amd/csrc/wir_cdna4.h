@@ -1526,6 +1526,57 @@ __device__ __forceinline__ void store_tile(const gl<T>& g, const RTile<MS, R, C>
   }
 }
 
+// Split-K fix-up (the IR's reduce_slices).  Every workgroup calls this, all
+// its threads, after storing its fp32 partial tile [row0, row0 + TR) x
+// [col0, col0 + TC) of slice blockIdx.z into `part` ([b][slice][row][col]).
+// arrivals[idx] counts the slices that have stored the tile.  The release
+// fence makes this workgroup's partial stores visible to every XCD before it
+// counts itself; the last of the part.d slices to arrive (the counter's old
+// value is part.d - 1) takes the acquire fence, sums the slices in slice
+// order in fp32 (from 0, as the separate reduction kernel does), writes the
+// bf16 tile with the usual bounds (N a multiple of 8) and puts the counter
+// back to zero, so a zeroed counter array stays zeroed across launches.  No
+// workgroup waits for another.  `flag` is one word of LDS that nothing else
+// uses here (the ring is drained by the loop's last wait).
+template <int TR, int TC, int NT>
+__device__ __forceinline__ void reduce_slices(const gl<float>& part, const gl<bf16>& dst, const gl<unsigned>& arrivals,
+                                              int b, int row0, int col0, int idx, char* flag) {
+  volatile unsigned* last = (volatile unsigned*)flag;
+  // The barrier makes every wave's stores visible within the workgroup; one
+  // wave's device-scope fence then releases them all (the fence writes back
+  // the XCD's whole L2, so one per workgroup is enough), and the same wave
+  // takes the acquire side for the workgroup.
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    __threadfence();
+    if (threadIdx.x == 0) *last = atomicAdd(arrivals.data + idx, 1u) == (unsigned)(part.d - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!*last) return;
+  if (threadIdx.x < 64) __threadfence();
+  __syncthreads();
+  const float* pb = part.data + (long long)b * part.sb;
+  bf16* db = dst.data + (long long)b * dst.sb;
+  for (int e = threadIdx.x * 8; e < TR * TC; e += NT * 8) {
+    const int r = row0 + e / TC, c = col0 + e % TC;
+    if (r >= dst.r || c >= dst.c) continue;
+    const float* p = pb + (long long)r * part.sr + c;
+    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
+    for (int sl = 0; sl < part.d; ++sl) {
+      lo += *(const f32x4*)(p + sl * part.sd);
+      hi += *(const f32x4*)(p + sl * part.sd + 4);
+    }
+    bf16x8 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = (bf16)lo[j];
+      v[4 + j] = (bf16)hi[j];
+    }
+    *(bf16x8*)(db + (long long)r * dst.sr + c) = v;
+  }
+  if (threadIdx.x == 0) arrivals.data[idx] = 0u;
+}
+
 // Register tile -> bf16 global through this wave's private LDS area `stage`
 // (R * C * 2 bytes, free for the rest of the kernel).  In the lane = row
 // layout one store instruction would touch MS rows with 8 bytes each; the

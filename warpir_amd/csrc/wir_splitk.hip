@@ -79,6 +79,18 @@ static_assert(offsetof(SplitKGemmArgs, B) == 48 && offsetof(SplitKGemmArgs, N) =
                   offsetof(SplitKGemmArgs, C) == 104 && sizeof(SplitKGemmArgs) == 152,
               "split-K GEMM globals layout");
 
+// Kernel arguments of the fused split-K variants (gemm_128_splitk_fused): the
+// same A, B, N and fp32 partials, then the bf16 result and the per-tile
+// arrival counters the kernel's reduce_slices uses.
+struct SplitKFusedArgs {
+  SplitKGemmArgs g;
+  GlobalView C;          // bf16 [1][1][M][N]
+  GlobalView arrivals;   // u32 [1][1][1][tiles]
+};
+static_assert(offsetof(SplitKFusedArgs, C) == 152 && offsetof(SplitKFusedArgs, arrivals) == 200 &&
+                  sizeof(SplitKFusedArgs) == 248,
+              "fused split-K GEMM globals layout");
+
 // Kernel arguments of wir_splitk_reduce (splitk_reduce.hip).
 struct SplitKReduceArgs {
   const float* partials;
@@ -102,10 +114,8 @@ int launch(hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned bx, 
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// The two launches of a split-K product with its fp32 partials in `ws`
-// (splits * m * n floats); arguments already validated.
-int splitk_launch(hipFunction_t gemm, hipFunction_t reduce, const void* a, const void* b, void* out, float* ws,
-                  int m, int n, int k, int splits, void* stream) {
+// The GEMM arguments of one split-K product (A and B as K slices, the partials in `ws`).
+SplitKGemmArgs splitk_args(const void* a, const void* b, float* ws, int m, int n, int k, int splits) {
   const long long split_elems = (long long)m * n;
   const int kc = k / splits;
   SplitKGemmArgs g;
@@ -113,6 +123,15 @@ int splitk_launch(hipFunction_t gemm, hipFunction_t reduce, const void* a, const
   g.B = {b, 1, splits, kc, n, (long long)k * n, (long long)kc * n, n};
   g.N = kc;
   g.C = {ws, 1, splits, m, n, (long long)splits * split_elems, split_elems, n};
+  return g;
+}
+
+// The two launches of a split-K product with its fp32 partials in `ws`
+// (splits * m * n floats); arguments already validated.
+int splitk_launch(hipFunction_t gemm, hipFunction_t reduce, const void* a, const void* b, void* out, float* ws,
+                  int m, int n, int k, int splits, void* stream) {
+  const long long split_elems = (long long)m * n;
+  SplitKGemmArgs g = splitk_args(a, b, ws, m, n, k, splits);
   int e = launch(gemm, (unsigned)((n + kTile - 1) / kTile), (unsigned)((m + kTile - 1) / kTile), (unsigned)splits,
                  kThreads, stream, &g, sizeof(g));
   if (e) return e;
@@ -140,6 +159,25 @@ extern "C" int wir_gemm_splitk(wir_function_t gemm, wir_function_t reduce, const
     return (int)hipErrorInvalidValue;
   return splitk_launch((hipFunction_t)gemm, (hipFunction_t)reduce, a, b, out, (float*)workspace, m, n, k, splits,
                        stream);
+}
+
+extern "C" int wir_gemm_splitk_fused(wir_function_t gemm, const void* a, const void* b, void* out, void* workspace,
+                                     size_t workspace_floats, void* arrivals, size_t arrival_count, int m, int n,
+                                     int k, int splits, void* stream) {
+  // the fused kernel has no separate reduction: pass the GEMM as both functions to the common checks
+  int e = splitk_check(gemm, gemm, a, b, out, m, n, k, splits);
+  if (e) return e;
+  if (!workspace || !aligned16(workspace) || (unsigned long long)splits * m * n > workspace_floats)
+    return (int)hipErrorInvalidValue;
+  const long long tiles = (long long)((m + kTile - 1) / kTile) * ((n + kTile - 1) / kTile);
+  if (!arrivals || ((uintptr_t)arrivals & 3) || (unsigned long long)tiles > arrival_count)
+    return (int)hipErrorInvalidValue;
+  SplitKFusedArgs f;
+  f.g = splitk_args(a, b, (float*)workspace, m, n, k, splits);
+  f.C = {out, 1, 1, m, n, (long long)m * n, (long long)m * n, n};
+  f.arrivals = {arrivals, 1, 1, 1, (int)tiles, tiles, tiles, tiles};
+  return launch((hipFunction_t)gemm, (unsigned)((n + kTile - 1) / kTile), (unsigned)((m + kTile - 1) / kTile),
+                (unsigned)splits, kThreads, stream, &f, sizeof(f));
 }
 
 extern "C" int wir_gemm_splitk_noalloc(wir_function_t gemm, wir_function_t reduce, const void* a,

@@ -353,6 +353,27 @@ class DrainIndexOp(Op):
 
 
 @dataclass(frozen=True)
+class ReduceSlicesOp(Op):
+    """*Additive.* Split-K fix-up of one output tile.
+
+    ``partials`` is an fp32 ``[1, S, M, N]`` global whose depth slices are
+    the K slices of a product: the program of slice ``d`` has just stored
+    its tile at ``coords = (batch, d, row_tile, col_tile)``.  ``dest`` is the
+    bf16 ``[1, 1, M, N]`` result and ``arrivals`` a u32 global of one
+    counter per output tile (row-major over the tiles of ``dest``), zero
+    before the first launch.  Once all ``S`` slices have stored the tile,
+    ``dest``'s tile becomes the bf16 rounding of their fp32 sum taken in
+    slice order (from 0), and its counter is zero again.  The lowering lets
+    the last program to arrive do the sum; no program waits for another.
+    """
+
+    partials: Value
+    dest: Value
+    arrivals: Value
+    coords: tuple
+
+
+@dataclass(frozen=True)
 class PipelineStageOp(Op):
     """*Additive.* Placement mark of a software-pipelined loop body: the ops
     after it, up to the next mark or the yield, run ``stage`` iterations

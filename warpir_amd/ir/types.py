@@ -30,6 +30,8 @@ class GPUType(str, Enum):
 
     bf16 = "bf16"
     fp32 = "fp32"
+    # additive: 32-bit unsigned counters (the split-K per-tile arrival counts)
+    u32 = "u32"
 
 
 class TileLayout(str, Enum):

@@ -18,10 +18,10 @@ from warpir_amd.workloads import (build_attention_kernel, build_gemm_kernel, bui
 
 def _gemm_mi355x(block_k: int = 32, block_m: int = 256, block_n: int = 256, wave_m: int = 128,
                  wave_n: int = 128, load_units: int = 8, lds_budget: int = 160 * 1024,
-                 split_k: bool = False, hbm_sources=()) -> Kernel:
+                 split_k: bool = False, hbm_sources=(), fused_reduce: bool = False) -> Kernel:
     return kernel_pass(build_gemm_kernel(block_m=block_m, block_n=block_n, block_k=block_k, wave_m=wave_m,
                                          wave_n=wave_n, name="gemm_splitk" if split_k else "gemm",
-                                         split_k=split_k),
+                                         split_k=split_k, fused_reduce=fused_reduce),
                        cost_model=gfx950_cost_model(block_m, block_n, block_k, load_units=load_units,
                                                     lds_budget=lds_budget, hbm_sources=tuple(hbm_sources)))
 
@@ -61,6 +61,11 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # rings per operand (B three slots, loaded two tiles ahead; A two slots, one tile ahead)
     "gemm_128_splitk_k128_b3": lambda: _gemm_mi355x(128, block_m=128, block_n=128, wave_m=64, wave_n=64,
                                                     lds_budget=160 * 1024, split_k=True, hbm_sources=("B",)),
+    # the same rings with the slices summed in the kernel: the last slice to store an output tile
+    # adds the fp32 partials in slice order and writes the bf16 tile (reduce_slices)
+    "gemm_128_splitk_fused": lambda: _gemm_mi355x(128, block_m=128, block_n=128, wave_m=64, wave_n=64,
+                                                  lds_budget=160 * 1024, split_k=True, hbm_sources=("B",),
+                                                  fused_reduce=True),
     "gemm_128x64_splitk": lambda: _gemm_mi355x(64, block_m=128, block_n=64, wave_m=64, wave_n=32,
                                                lds_budget=80 * 1024, split_k=True),
     "gemm_128_splitk_s5": lambda: _gemm_mi355x(64, block_m=128, block_n=128, wave_m=64, wave_n=64,

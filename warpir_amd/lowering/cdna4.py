@@ -47,7 +47,7 @@ from typing import Dict, List, Optional, Sequence, Tuple, Union
 from warpir_amd.ir.ops import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, CopyOp, DivRowOp, DrainIndexOp, Exp2Op, ForOp,
     IntAffineOp, IntDivOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp, NegInftyOp,
-    LazyMaxOp, Op, PipelineStageOp, RowMaxOp, RowSumOp, SubColOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
+    LazyMaxOp, Op, PipelineStageOp, ReduceSlicesOp, RowMaxOp, RowSumOp, SubColOp, SubOp, SubRowOp, TMALoadBufOp, TMALoadOp, TMAStoreOp, Value,
     WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
 from warpir_amd.ir.ops import SlotViewOp
@@ -1018,6 +1018,9 @@ class CDNA4Lowerer:
         if isinstance(op, TMAStoreOp):
             self._emit_store(op, out, depth)
             return
+        if isinstance(op, ReduceSlicesOp):
+            self._emit_reduce_slices(op, out, depth)
+            return
         if isinstance(op, ForOp):
             self._emit_for(op, out, depth)
             return
@@ -1146,6 +1149,21 @@ class CDNA4Lowerer:
                        f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols});")
         else:
             raise LoweringError("tma_store of a shared tile is not supported by the CDNA4 target")
+
+    def _emit_reduce_slices(self, op: ReduceSlicesOp, out: List[str], depth: int) -> None:
+        """Split-K fix-up after the partial store (``wir::reduce_slices``): the
+        tile's counter is ``row_tile * ceil(N / TC) + col_tile``."""
+        pad = "  " * depth
+        part, dest, arr = op.partials, op.dest, op.arrivals
+        if (part.type.data_type != GPUType.fp32 or dest.type.data_type != GPUType.bf16
+                or arr.type.data_type != GPUType.u32):
+            raise LoweringError("reduce_slices sums fp32 partials into a bf16 global with u32 arrivals")
+        sub = dest.type.sub_tile_type
+        b, _d, rt, ct = (self._int(c) for c in op.coords)
+        g = lambda v: f"globals.{_cname(v.name)[2:]}"   # noqa: E731
+        idx = f"({rt}) * (({g(dest)}.c + {sub.cols - 1}) / {sub.cols}) + ({ct})"
+        out.append(f"{pad}wir::reduce_slices<{sub.rows}, {sub.cols}, {self.num_threads}>({g(part)}, {g(dest)}, "
+                   f"{g(arr)}, {b}, ({rt}) * {sub.rows}, ({ct}) * {sub.cols}, {idx}, smem);")
 
     def _emit_for(self, op: ForOp, out: List[str], depth: int) -> None:
         pad = "  " * depth
@@ -2171,7 +2189,7 @@ class CDNA4Lowerer:
         fields = []
         for v in self.globals:
             if isinstance(v.type, GlobalType):
-                ctype = "wir::bf16" if v.type.data_type == GPUType.bf16 else "float"
+                ctype = {GPUType.bf16: "wir::bf16", GPUType.fp32: "float", GPUType.u32: "unsigned"}[v.type.data_type]
                 fields.append(f"  wir::gl<{ctype}> {_cname(v.name)[2:]};")
             else:
                 fields.append(f"  int {_cname(v.name)[2:]};")

@@ -32,6 +32,7 @@ from warpir_amd.ir.ops import (
     NegInftyOp,
     Op,
     PipelineStageOp,
+    ReduceSlicesOp,
     RowMaxOp,
     RowSumOp,
     SlotViewOp,
@@ -137,6 +138,9 @@ _LINE: Dict[type, Callable[[Op], str]] = {
     IntDivOp: lambda op: f"{op.result!r} = int_div({_coord(op.input)}, {_coord(op.divisor)})",
     DrainIndexOp: lambda op: f"{op.result!r} = drain_index(+{op.offset})",
     PipelineStageOp: lambda op: f"pipeline_stage({op.stage})",
+    ReduceSlicesOp: lambda op: (
+        f"reduce_slices({op.partials!r}, {op.dest!r}, {op.arrivals!r}, {_coords(op.coords)})"
+    ),
 }
 
 

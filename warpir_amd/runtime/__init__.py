@@ -93,6 +93,7 @@ def library() -> ctypes.CDLL:
             "wir_error_string": ([ci], ctypes.c_char_p),
             "wir_gemm_splitk": ([vp, vp, vp, vp, vp, vp, sz, ci, ci, ci, ci, vp], ci),
             "wir_gemm_splitk_noalloc": ([vp, vp, vp, vp, vp, ci, ci, ci, ci, vp], ci),
+            "wir_gemm_splitk_fused": ([vp, vp, vp, vp, vp, sz, vp, sz, ci, ci, ci, ci, vp], ci),
         }
         for name, (args, res) in sig.items():
             fn = getattr(lib, name)

@@ -39,6 +39,7 @@ from warpir_amd.ir import (
     MulScalarOp,
     NegInftyOp,
     RegTileType,
+    ReduceSlicesOp,
     RowMaxOp,
     RowSumOp,
     RowVecType,
@@ -68,7 +69,7 @@ def _bf16_global(tile: SharedTileType, batch: int = 1, depth: int = 1) -> Global
 
 def build_gemm_kernel(block_m: int = 64, block_n: int = 64, block_k: int = 64,
                       wave_m: int = 16, wave_n: int = 64, name: str = "gemm",
-                      split_k: bool = False) -> Kernel:
+                      split_k: bool = False, fused_reduce: bool = False) -> Kernel:
     """``C[M, N] = A[M, K] @ B[K, N]``, bf16 in, fp32 accumulate, bf16 out.
 
     One program per ``block_m x block_n`` tile of C at
@@ -85,7 +86,16 @@ def build_gemm_kernel(block_m: int = 64, block_n: int = 64, block_k: int = 64,
     ``[1, S, K/S, N]`` -- and C_global becomes an fp32 ``[1, S, M, N]`` of
     partial products, which the host sums (``warpir_amd.api.gemm``).  ``N``
     is then the slice's reduction extent.
+
+    ``fused_reduce`` (additive, with ``split_k``): the kernel sums the slices
+    itself -- a ``reduce_slices`` after the partial store writes the bf16
+    ``C`` ``[1, 1, M, N]`` once every slice of a tile has stored, counting
+    arrivals in ``Arrivals`` (u32, one counter per output tile, zero before
+    the first launch and left zero).  Outputs: ``C_global``, ``C``,
+    ``Arrivals``.
     """
+    if fused_reduce and not split_k:
+        raise ValueError("fused_reduce needs split_k")
     a_tile = SharedTileType(GPUType.bf16, block_m, block_k)
     b_tile = SharedTileType(GPUType.bf16, block_k, block_n)
     if split_k:
@@ -118,11 +128,15 @@ def build_gemm_kernel(block_m: int = 64, block_n: int = 64, block_k: int = 64,
         ),
         results=(c_final,),
     )
-    return Kernel(
-        name=name, inputs=(A, B, n_red), outputs=(C,),
-        body=(ZeroOp(result=c_init), loop,
-              TMAStoreOp(source=c_final, dest=C, coords=(0, depth, row, col))),
-    )
+    body = (ZeroOp(result=c_init), loop, TMAStoreOp(source=c_final, dest=C, coords=(0, depth, row, col)))
+    outputs = (C,)
+    if fused_reduce:
+        out = Value("C", _bf16_global(SharedTileType(GPUType.bf16, block_m, block_n)))
+        arrivals = Value("Arrivals", GlobalType(data_type=GPUType.u32, sub_tile_type=SharedTileType(GPUType.u32, 1, 1),
+                                                batch=1, depth=1, rows=1, cols=-1))
+        body += (ReduceSlicesOp(partials=C, dest=out, arrivals=arrivals, coords=(0, depth, row, col)),)
+        outputs = (C, out, arrivals)
+    return Kernel(name=name, inputs=(A, B, n_red), outputs=outputs, body=body)
 
 
 def build_attention_kernel(d: int = 64, block: int = 64, warp_rows: int = 16,
