@@ -31,7 +31,7 @@ def test_reference_attention_ir(gpu, n):
     assert rel_err(o.cpu(), ref) <= TOL
 
 
-@pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp_swapped", "mha_d128_w4",
+@pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_vp4", "mha_d128_vp8", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp_swapped", "mha_d128_w4",
                                      "mha_d128_online", "mha_d128_ovl", "mha_d128_s5", "mha_d128_pp2b",
                                      "mha_d128_fold", "mha_d128_u2"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 1, 64)])

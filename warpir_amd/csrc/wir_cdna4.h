@@ -806,6 +806,70 @@ __device__ __forceinline__ void mma_rAB(RTile<MS, R, C>& acc, const BTile<MS, R,
   __builtin_amdgcn_s_setprio(0);
 }
 
+// The first NPRE B operands of an mma_rAB, read ahead of it: the 8-wave
+// attention ping-pong reads part of the next PV's V tile in its VALU phase,
+// when the wave's own LDS reads have nothing else to do, so its next MFMA
+// phase reads that much less.  Item t is the t-th MFMA's B operand in
+// mma_rAB's order (k groups in pairs, column blocks inner).
+template <int NPRE>
+struct RABPre {
+  bf16x8 f[NPRE > 0 ? NPRE : 1];
+};
+
+template <int MS, int R, int K, int C, class TB>
+__device__ __forceinline__ bf16x8 rab_item(char* b_base, int b_col0, int t) {
+  constexpr int G = BTile<MS, R, K>::G;
+  constexpr int CB = RTile<MS, R, C>::CB;
+  const int lane = lane_id();
+  const int lh = lane / MS;
+  const int ngrp = (lane % MS) & ~15;
+  const int q = 2 * (t / CB), cb = t % CB;
+  const int kb0 = q / G, g0 = q % G, kb1 = (q + 1) / G, g1 = (q + 1) % G;
+  const int k0 = kb0 * MS + g0 * 4 * MF<MS>::LG + 4 * lh;
+  const int k1 = kb1 * MS + g1 * 4 * MF<MS>::LG + 4 * lh;
+  const int n0 = b_col0 + cb * MS + ngrp;
+  return cat(tr_operand4<TB>(b_base, k0, n0), tr_operand4<TB>(b_base, k1, n0));
+}
+
+template <int MS, int R, int K, int C, class TB, int NPRE>
+__device__ __forceinline__ void prefetch_rAB(RABPre<NPRE>& pre, char* b_base, int b_col0) {
+#pragma unroll
+  for (int t = 0; t < NPRE; ++t) pre.f[t] = rab_item<MS, R, K, C, TB>(b_base, b_col0, t);
+}
+
+// mma_rAB whose first NPRE B operands come from `pre` (prefetch_rAB of the
+// same tile); the others are read LOOK MFMAs ahead as in mma_rAB.
+template <int MS, int R, int K, int C, class TB, int NPRE>
+__device__ __forceinline__ void mma_rAB_pre(RTile<MS, R, C>& acc, const BTile<MS, R, K>& a, const RABPre<NPRE>& pre,
+                                            char* b_base, int b_col0) {
+  static_assert(TB::ROWS == K, "inner dimensions differ");
+  constexpr int G = BTile<MS, R, K>::G;
+  constexpr int NG = (K / MS) * G;
+  constexpr int CB = RTile<MS, R, C>::CB, RB = RTile<MS, R, C>::RB;
+  constexpr int ITEMS = (NG / 2) * CB;
+  static_assert(NPRE >= 0 && NPRE <= ITEMS, "prefetched operands must be items of this product");
+  constexpr int REST = ITEMS - NPRE;
+  constexpr int LOOK = REST < 4 ? REST : 4;
+  bf16x8 ring[LOOK + 1];
+  __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+  for (int p = 0; p < LOOK; ++p) ring[p] = rab_item<MS, R, K, C, TB>(b_base, b_col0, NPRE + p);
+#pragma unroll
+  for (int t = 0; t < ITEMS; ++t) {
+    const int u = t - NPRE;
+    if (u >= 0 && u + LOOK < REST) ring[(u + LOOK) % (LOOK + 1)] = rab_item<MS, R, K, C, TB>(b_base, b_col0, t + LOOK);
+    __builtin_amdgcn_sched_barrier(0);
+    const int q = 2 * (t / CB), cb = t % CB;
+    const int kb0 = q / G, g0 = q % G, kb1 = (q + 1) / G, g1 = (q + 1) % G;
+    const bf16x8 bop = u < 0 ? pre.f[t < NPRE ? t : 0] : ring[(u < 0 ? 0 : u) % (LOOK + 1)];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      acc.f[cb][rb] = MF<MS>::mma(bop, cat(a.f[kb0][rb][g0], a.f[kb1][rb][g1]), acc.f[cb][rb]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __builtin_amdgcn_s_setprio(0);
+}
+
 // ---------------------------------------------------------------------------
 // Software-pipelined attention (the lowering's overlapped form).
 //

@@ -116,6 +116,11 @@ class CDNA4Target:
     # V tiles S - 2 ahead, and each barrier still leaves the wave's newest
     # batch in flight).  1 keeps a barrier every iteration.
     pingpong_barrier_every: int = 1
+    # Attention ping-pong: B operands of the next PV MMA (V tile fragments,
+    # in mma_rAB's order) each wave reads at the end of its VALU phase, when
+    # its LDS reads are otherwise idle, so its MFMA phase reads that many
+    # fewer (4 VGPRs each).  0 reads them all in the MFMA phase.
+    pingpong_v_prefetch: int = 0
     # With the lazy softmax on scores from hoisted Q fragments: the scale c is
     # folded into those fragments (bf16 of c*q, once per program) and the
     # running max into the score MFMAs (one extra MFMA per column block
@@ -1513,10 +1518,28 @@ class CDNA4Lowerer:
         if dma(v_ld, "0", 0)[1] != per:
             return False
 
+        npre = self.target.pingpong_v_prefetch
+        pa_t, pr_t = pv.a.type, pv.result.type
+        _vptr, vkey = self._tile_ptr(pv.b)
+        rab = f"{self.geo.ms}, {pa_t.rows}, {pa_t.cols}, {pr_t.cols}, {self.stile(vkey)}"
+
         def emit_pv(dst: List[str], d: int) -> None:
             self._slot_shift[ivn] = -1
-            self._emit_op(pv, dst, d)
+            if npre:
+                pd = "  " * d
+                res, acc = self._var(pv.result), self._var(pv.accum)
+                if acc != res:
+                    dst.append(f"{pd}{res} = {acc};")
+                dst.append(f"{pd}wir::mma_rAB_pre<{rab}, {npre}>({res}, {self._var(pv.a)}, wir_vpre, "
+                           f"{self._tile_ptr(pv.b)[0]}, wave_col0);")
+            else:
+                self._emit_op(pv, dst, d)
             del self._slot_shift[ivn]
+
+        def v_prefetch(d: int) -> None:   # the next PV's first npre V operands (this iteration's tile)
+            if npre:
+                out.append(f"{'  ' * d}wir::prefetch_rAB<{rab}, {npre}>(wir_vpre, {self._tile_ptr(pv.b)[0]}, "
+                           f"wave_col0);")
 
         # Both groups run the same loop: M(i), then V(i) with the group's ring
         # load; group B has one extra V phase (its first ring load) in front,
@@ -1531,6 +1554,8 @@ class CDNA4Lowerer:
         out.append(f"{pad}}} else {{")
         out.append(f"{q}const int wir_grp = (wir_wave >> 2) ^ {swap}, wir_gw = wir_wave & 3;"
                    f"  // group A (K loads) = physical wave group {swap}")
+        if npre:
+            out.append(f"{q}wir::RABPre<{npre}> wir_vpre;")
         was_live = self._fold_live
         if any(isinstance(self._softmax_fused.get(id(o)), dict) for o in plan["softmax"]):
             self._fold_preamble([qk], out, depth + 1)
@@ -1585,6 +1610,7 @@ class CDNA4Lowerer:
         def v_tail(ops, d: int) -> None:
             self._emit_ops(ops, out, d)
             self._emit_op(plan["yld"], out, d)
+            v_prefetch(d)
             v_barrier(d)
 
         def m_phase(d: int) -> None:
