@@ -43,7 +43,7 @@ import torch
 from warpir_amd.ir import (
     AddOp, AllocSharedOp, BufSlotExpr, CausalMaskOp, ColVecType, CopyOp, DivRowOp, DrainIndexOp, Exp2Op,
     ForOp, GPUType, IntAffineOp, IntDivOp, Kernel, LoadVecOp, Log2Op, MMABufOp, MMAOp, MulOp, MulRowOp, MulScalarOp,
-    NegInftyOp, PipelineStageOp, RegTileType, RowMaxOp, RowSumOp, RowVecType, SlotViewOp, SubColOp, SubOp, SubRowOp, LazyMaxOp,
+    NegInftyOp, PipelineStageOp, ReduceSlicesOp, RegTileType, RowMaxOp, RowSumOp, RowVecType, SlotViewOp, SubColOp, SubOp, SubRowOp, LazyMaxOp,
     TMALoadBufOp, TMALoadOp, TMAStoreOp, Value, WaitBufOp, WaitOp, YieldOp, ZeroOp,
 )
 
@@ -143,6 +143,25 @@ class Interpreter:
         cols = max(0, min(tile.shape[1], g.shape[3] - c0))
         g[b, d, r0:r0 + rows, c0:c0 + cols] = tile[:rows, :cols].to(g.dtype)
 
+    def _reduce_slices(self, op) -> None:
+        """Split-K fix-up (``ReduceSlicesOp``): count this slice's arrival; the
+        last of the S slices sums them in slice order and resets the count."""
+        part = _as4d(self.tensors[op.partials.name], op.partials.type)
+        dest = _as4d(self.tensors[op.dest.name], op.dest.type)
+        arr = self.tensors[op.arrivals.name].view(-1)
+        sub = op.dest.type.sub_tile_type
+        b, _d, rt, ct = (self._int(c) for c in op.coords)
+        idx = rt * math.ceil(dest.shape[3] / sub.cols) + ct
+        arr[idx] += 1
+        if int(arr[idx]) < part.shape[1]:
+            return
+        r0, c0 = rt * sub.rows, ct * sub.cols
+        tile = torch.zeros_like(part[b, 0, r0:r0 + sub.rows, c0:c0 + sub.cols], dtype=torch.float32)
+        for s in range(part.shape[1]):
+            tile = tile + part[b, s, r0:r0 + sub.rows, c0:c0 + sub.cols].float()
+        dest[b, 0, r0:r0 + tile.shape[0], c0:c0 + tile.shape[1]] = tile.to(dest.dtype)
+        arr[idx] = 0
+
     # -- execution -----------------------------------------------------------
     def run(self, tensors: Dict[str, torch.Tensor], scalars: Dict[str, int], grid=None) -> None:
         self.tensors = tensors
@@ -170,6 +189,8 @@ class Interpreter:
         elif isinstance(op, TMALoadOp):
             t = op.result.type
             s(op.result, self._load(op.source, op.coords, t.rows, t.cols))
+        elif isinstance(op, ReduceSlicesOp):
+            self._reduce_slices(op)
         elif isinstance(op, DrainIndexOp):
             s(op.result, self.drain + op.offset)
         elif isinstance(op, AllocSharedOp):
