@@ -445,10 +445,12 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
     sks = [x for x in names if x.startswith("gemm_") and "splitk" in x]
     dqs = [x for x in names if x.startswith("mha_bwd_dq_d128") and not x.endswith(("_causal", "_gqa"))]
     fas = [x for x in names if x.startswith("mha_d128") and "causal" not in x and "gqa" not in x]
-    untimed = [x for x in names if x not in gemms + sks + dqs + fas]
+    c5s = [x for x in names if x.startswith("mha_d64_causal") and not x.endswith("_ssa")]
+    untimed = [x for x in names if x not in gemms + sks + dqs + fas + c5s]
     if untimed:
         raise ValueError(f"--compare times GEMM 8192^3, split-K at M=128 N=K=8192, FA forward and dQ at "
-                         f"the config-4 shape; not {', '.join(untimed)}")
+                         f"the config-4 shape and causal FA forward at the config-5 shape; not "
+                         f"{', '.join(untimed)}")
     stream = torch.cuda.current_stream().cuda_stream
     out = {}
     timed = collections.defaultdict(list)
@@ -488,6 +490,25 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
         out[name] = {"ms": ms, "ms_reps": timed[name], "tflops": 2.0 * n ** 3 / (ms * 1e-3) / 1e12,
                      "options": kernels.TARGETS.get(name, {}), "grid": list(lc.grid), "block": lc.block[0]}
     del a, b, c
+    if c5s:
+        # causal FA forward at config 5 (B8 H32 S8192 D64)
+        from warpir_amd import api
+
+        bsz, heads, seq, d = 8, 32, 8192, 64
+        q, k, v = (seeded_normal((bsz, heads, seq, d), sd).cuda() for sd in (3, 4, 5))
+        o = torch.empty_like(q)
+        lse = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
+        for _ in range(reps):
+            for name in c5s:
+                h = kernels.handle(name)
+                timed[name].append(_time_launches(lambda: h(Q=q, K=k, V=v, N=seq, O=o, L=lse), steps, warmup,
+                                                  stream)[0])
+        for name in c5s:
+            ms = statistics.median(timed[name])
+            out[name] = {"ms": ms, "ms_reps": timed[name],
+                         "tflops": api.attention_flops(bsz, heads, seq, d, causal=True) / (ms * 1e-3) / 1e12,
+                         "shape": [bsz, heads, seq, d], "options": kernels.TARGETS.get(name, {})}
+        del q, k, v, o, lse
     if dqs and not fas:
         fas = ["mha_d128"]   # the dQ kernels read the forward's O and LSE
     if not fas:

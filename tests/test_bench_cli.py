@@ -29,7 +29,7 @@ def test_unknown_only_name_is_rejected():
 
 
 @pytest.mark.parametrize("names,word", [(["no_such_variant"], "unknown variant"),
-                                        (["mha_d64_causal"], "not mha_d64_causal"),
+                                        (["mha_d64_causal_ssa"], "not mha_d64_causal_ssa"),
                                         (["mha_d128", "mha_d128_causal"], "not mha_d128_causal"),
                                         (["mha_bwd_dq_d64"], "not mha_bwd_dq_d64")])
 def test_compare_rejects_variants_it_does_not_time(names, word):
