@@ -8,11 +8,8 @@ for byte and, through it, that ``build_gemm_kernel`` /
 """
 import os
 
-import pytest
-
 import warpir
-from warpir.ir import (ForOp, GlobalType, GPUType, IterArg, Kernel, MMAOp, SharedTileType, TMALoadOp,
-                       Value, WaitOp, YieldOp, ZeroOp)
+from warpir.ir import GlobalType, GPUType, Kernel, SharedTileType, TMALoadOp, Value, WaitOp, YieldOp, ZeroOp
 from warpir.passes.modulo_scheduler import kernel_pass
 from warpir.printing import format_kernel
 from warpir_amd.workloads import build_attention_kernel, build_gemm_kernel, build_mha_forward_kernel
