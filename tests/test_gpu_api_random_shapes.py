@@ -94,3 +94,35 @@ def test_attention_backward_random_shapes(gpu, b, hq, hkv, s, d, causal):
     for name, out, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
         err = rel_err(out, ref)
         assert err <= TOL, (name, err)
+
+
+@pytest.mark.parametrize("m,n,k", [(0, 64, 64), (64, 0, 64), (0, 0, 0), (64, 64, 0), (128, 8192, 0),
+                                   (300, 4096, 0), (1024, 1024, 0)])
+def test_gemm_empty_products(gpu, m, n, k):
+    """M or N = 0 launches nothing; K = 0 runs the kernel with no loop step and
+    its tile loads reading the zero page, so every output element is 0 (the
+    output starts as NaN to show that the kernel wrote it)."""
+    announce(f"api.gemm empty {m}x{n}x{k} -> {api.gemm_variant(m, n, k)}")
+    a = torch.randn(m, k).to(torch.bfloat16).cuda()
+    b = torch.randn(k, n).to(torch.bfloat16).cuda()
+    out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+    c = api.gemm(a, b, out=out)
+    torch.cuda.synchronize()
+    assert c is out and tuple(c.shape) == (m, n)
+    assert torch.equal(c.float().cpu(), torch.zeros(m, n))
+
+
+@pytest.mark.parametrize("b,hq,hkv,s,d,causal", [(1, 2, 2, 0, 128, False), (0, 2, 2, 128, 128, False),
+                                                 (1, 2, 2, 0, 64, True), (1, 4, 2, 0, 128, False)])
+def test_attention_empty_shapes(gpu, b, hq, hkv, s, d, causal):
+    """No queries (S = 0) or no batch: the forward and backward return empty
+    tensors of the right shapes and launch nothing."""
+    announce(f"api.attention empty B={b} Hq={hq} Hkv={hkv} S={s} D={d} causal={causal}")
+    q = torch.randn(b, hq, s, d).to(torch.bfloat16).cuda()
+    k = torch.randn(b, hkv, s, d).to(torch.bfloat16).cuda()
+    v = torch.randn(b, hkv, s, d).to(torch.bfloat16).cuda()
+    o, lse = api.attention_forward(q, k, v, causal=causal)
+    dq, dk, dv = api.attention_backward(q, k, v, o, lse, torch.zeros_like(o), causal=causal)
+    torch.cuda.synchronize()
+    assert o.shape == q.shape and tuple(lse.shape) == (b, hq, s)
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape

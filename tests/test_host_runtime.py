@@ -99,3 +99,21 @@ def test_dkdv_d128_kernels_ask_for_the_vgpr_form_and_others_do_not():
     for name in ("gemm_256_k64", "mha_d128", "mha_bwd_dq_d128", "mha_bwd_dkdv_d64"):
         src = kernels.lowerer(name).lower(kernels.kernel(name))
         assert source_flags(src) == (), name
+
+
+@pytest.mark.parametrize("m,n,k", [(0, 8192, 8192), (128, 0, 8192), (128, 8192, 0), (64, 1024, 0)])
+def test_empty_products_stay_off_the_split_k_route(m, n, k):
+    """An empty product has no slices to split: splitk_count is 1 and api.gemm
+    routes it to the tiled kernels (which launch nothing for an empty output
+    and store zeros for K = 0)."""
+    assert api.splitk_count(m, n, k) == 1
+    assert api.gemm_variant(m, n, k) != api.SPLITK_GEMM_VARIANT
+
+
+def test_split_k_rejects_an_empty_k_before_touching_a_device():
+    a = torch.zeros(64, 0, dtype=torch.bfloat16)
+    b = torch.zeros(0, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="K must be positive"):
+        api.gemm_split_k(a, b)
+    with pytest.raises(ValueError, match="K must be positive"):
+        api.gemm_split_k_noalloc(a, b, torch.zeros(64, 256, dtype=torch.bfloat16))

@@ -52,6 +52,23 @@ def test_mi355x_gemm_ir_interpreted():
     assert rel_err(_gemm(k, a, b), gemm_ref(a, b)) <= 1e-2
 
 
+@pytest.mark.parametrize("variant", ["gemm_256_k64", "gemm_128x32_k64", "gemm_128_k64"])
+@pytest.mark.parametrize("k", [0, 8])
+def test_pipelined_gemm_with_fewer_steps_than_stages(variant, k):
+    """K = 0 and K = 8 (no loop trip after the prologue): the pipelined IR's
+    drain reads only ring slots its prologue loaded (an unloaded slot is None
+    here and would raise), and the product is A @ B (zeros for K = 0)."""
+    from warpir_amd import kernels
+
+    a = seeded_normal((256, k), 11, 0.1)
+    b = seeded_normal((k, 96), 12, 0.1)
+    c = _gemm(kernels.VARIANTS[variant](), a, b)
+    if k == 0:
+        assert torch.equal(c, torch.zeros_like(c))
+    else:
+        assert rel_err(c, gemm_ref(a, b)) <= 1e-2
+
+
 def test_gemm_ref_identity_closed_form():
     a = seeded_normal((64, 64), 9, 0.1)
     assert torch.equal(gemm_ref(a, torch.eye(64, dtype=torch.bfloat16)), a.float())

@@ -84,7 +84,9 @@ def _fused(variant: str) -> bool:
 def splitk_count(m: int, n: int, k: int, num_cus: int = 256) -> int:
     """Number of K slices for the split-K kernel: enough 128x128 tiles x
     slices to cover the CUs, with every slice a whole number of 64-deep
-    K steps.  1 means no split."""
+    K steps.  1 means no split (also for an empty product)."""
+    if m <= 0 or n <= 0 or k <= 0:
+        return 1
     tiles = math.ceil(m / 128) * math.ceil(n / 128)
     best = 1
     for s in range(2, 17):
@@ -143,6 +145,8 @@ def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None, v
         raise ValueError(f"gemm: shapes {tuple(a.shape)} @ {tuple(b.shape)} do not chain")
     m, k = a.shape
     n = b.shape[1]
+    if k == 0:
+        raise ValueError("gemm_split_k: K must be positive (api.gemm takes K = 0)")
     splits = splits or splitk_count(m, n, k)
     if k % (64 * splits) or n % 8 or not a.is_contiguous() or not b.is_contiguous():
         raise ValueError(f"gemm_split_k: K={k} must split into {splits} multiples of 64, N % 8 == 0, "
@@ -167,6 +171,8 @@ def gemm_split_k(a, b, out=None, splits: Optional[int] = None, workspace=None, v
         raise ValueError("gemm_split_k: a, b, out and workspace must be on one GPU")
     if any(t.data_ptr() % 16 for t in (a, b, out, workspace)):
         raise ValueError("gemm_split_k: a, b, out and workspace must be 16-byte aligned")
+    if m == 0 or n == 0:
+        return out
     gemm_fn, reduce_fn = _splitk_functions(variant or SPLITK_GEMM_VARIANT)
     stream = torch.cuda.current_stream(a.device).cuda_stream
     if reduce_fn is None:   # the slices are summed inside the GEMM kernel
@@ -205,6 +211,8 @@ def gemm_split_k_noalloc(a, b, out, splits: Optional[int] = None, stream=None):
         raise ValueError(f"gemm: shapes {tuple(a.shape)} @ {tuple(b.shape)} do not chain")
     m, k = a.shape
     n = b.shape[1]
+    if k == 0:
+        raise ValueError("gemm_split_k_noalloc: K must be positive (api.gemm takes K = 0)")
     splits = splits or splitk_count(m, n, k)
     for name, t, shape in (("a", a, (m, k)), ("b", b, (k, n)), ("out", out, (m, n))):
         if (not isinstance(t, torch.Tensor) or tuple(t.shape) != shape or t.dtype != torch.bfloat16
@@ -212,6 +220,8 @@ def gemm_split_k_noalloc(a, b, out, splits: Optional[int] = None, stream=None):
             raise ValueError(f"gemm_split_k_noalloc: {name} must be a contiguous bf16 {list(shape)} tensor")
     if not a.is_cuda or b.device != a.device or out.device != a.device:
         raise ValueError("gemm_split_k_noalloc: a, b and out must be on one GPU")
+    if m == 0 or n == 0:
+        return out
     gemm_fn, reduce_fn = _splitk_functions(SPLITK_TWO_LAUNCH_VARIANT)
     if stream is None:
         stream = torch.cuda.current_stream(a.device).cuda_stream
@@ -239,7 +249,9 @@ def gemm(a, b, out=None, variant: Optional[str] = None, workspace=None):
 
     The variant follows ``gemm_variant``: 256x256 tiles by default, smaller
     tiles for outputs with fewer tiles than CUs, split-K for M <= 128 and
-    long K (``workspace`` as in ``gemm_split_k``).
+    long K (``workspace`` as in ``gemm_split_k``).  An empty output (M or
+    N = 0) launches nothing; K = 0 gives zeros (the kernel's loop runs no
+    step and its tile loads read the zero page).
     """
     import torch
 
@@ -378,6 +390,8 @@ def _group_reduce(partials, out, splits: int) -> None:
 
     if not out.is_contiguous() or out.dtype.itemsize != 2:
         raise ValueError("attention_backward: dk / dv must be contiguous bf16")
+    if out.numel() == 0:
+        return
     n = out.shape[-2] * out.shape[-1]
     groups = out.numel() // n
     if n % 8 or partials.numel() != groups * splits * n:

@@ -330,7 +330,9 @@ class KernelHandle:
                 if vector:   # fp32 L x 1 vectors move 4 bytes per lane
                     if x.data_ptr() % 4:
                         raise ValueError(f"{v.name}: must be 4-byte aligned")
-                elif v.name in self._loaded_globals or shape[3] > 1:
+                elif (v.name in self._loaded_globals or shape[3] > 1) and x.numel():
+                    # (an empty tensor is never read or written: every tile of it
+                    # lies outside it, and loads of such tiles read the zero page)
                     if x.data_ptr() % 16 or (strides[2] * esz) % 16 or (shape[3] * esz) % 16:
                         raise ValueError(f"{v.name}: rows must be 16-byte aligned and a multiple of 16 bytes "
                                          "(the tile-load granule)")
@@ -346,7 +348,11 @@ class KernelHandle:
                     raise ValueError(f"{v.name}={x} does not fit in int32")
                 setattr(packed, v.name, x)
         cfg = self.lowerer.launch_config(self.kernel, {k: s for k, s in shapes.items()})
-        return packed, cfg, device
+        # every output empty (e.g. attention over S = 0): the launch would write nothing
+        empty = all(args[v.name].numel() == 0 for v in self.kernel.outputs
+                    if isinstance(v.type, GlobalType)) and any(isinstance(v.type, GlobalType)
+                                                               for v in self.kernel.outputs)
+        return packed, cfg, device, empty
 
     def _signature(self, args: Dict[str, object]):
         """Hashable summary of the arguments that fixes the packed struct, or None."""
@@ -374,13 +380,15 @@ class KernelHandle:
                 if len(self._pack_cache) >= 64:
                     self._pack_cache.clear()
                 self._pack_cache[key] = hit
-        packed, cfg, device = hit
+        packed, cfg, device, empty = hit
+        gx, gy, gz = cfg.grid
+        if empty or not (gx and gy and gz):
+            return   # an empty problem: no output element to write, or no workgroup
         self.load()
         if stream is None:
             stream = torch.cuda.current_stream(device).cuda_stream
         elif hasattr(stream, "cuda_stream"):
             stream = stream.cuda_stream
-        gx, gy, gz = cfg.grid
         bx, by, bz = cfg.block
         check(library().wir_launch(self._function, gx, gy, gz, bx, by, bz, cfg.dyn_lds,
                                    ctypes.c_void_p(stream), ctypes.byref(packed), ctypes.sizeof(packed)),
@@ -436,6 +444,8 @@ class RawKernel:
                stream=None) -> None:
         import torch
 
+        if not all(grid):
+            return   # no workgroups: nothing to launch
         self._load()
         if stream is None:
             stream = torch.cuda.current_stream().cuda_stream
