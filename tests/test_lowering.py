@@ -400,3 +400,22 @@ def test_per_ring_gemm_lowering_merges_ring_waits():
     assert "wir::wait_vm_barrier<" not in loop.replace("wir::wait_vm_barrier<8>();", "")
     assert "wir_drain += 1;" in src and "(wir_drain % 2)" in src and "(wir_drain % 3)" in src
     assert "const int v_i_d0_1 = wir_drain + 1;" in src
+
+
+@pytest.mark.parametrize("name", ["mha_d128", "mha_d64_causal"])
+def test_lazy_attention_loop_sits_inside_the_first_tile_guard(name):
+    """The peeled first tile, the loop and the last PV share one
+    ``if (tiles > start)`` guard, so the loop is entered only through the
+    peeled tile, whose MFMAs already wait for the register-hoisted Q: the
+    compiler then puts no vmcnt(0) for Q inside the loop (it would also wait
+    for the ring DMAs this wave has in flight)."""
+    src = kernels.lowerer(name).lower(kernels.VARIANTS[name]())
+    body = src[src.rindex('extern "C"'):].split("\n")
+    guards = [i for i, l in enumerate(body) if l.strip().startswith("if (") and l.rstrip().endswith(") > 0) {")]
+    loop = next(i for i, l in enumerate(body) if l.strip() == "for (;;) {")
+    assert len(guards) == 1 and guards[0] < loop
+    indent = len(body[guards[0]]) - len(body[guards[0]].lstrip())
+    close = next(i for i in range(guards[0] + 1, len(body))
+                 if body[i].strip() == "}" and len(body[i]) - len(body[i].lstrip()) == indent)
+    assert close > loop
+    assert any("mma_rAB" in l for l in body[loop:close] if "const int v_i" not in l)

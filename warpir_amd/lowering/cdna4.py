@@ -1342,26 +1342,34 @@ class CDNA4Lowerer:
             out.append(f"{pad}}}")
             return
         start = op.start
+        # One guard around the peeled first tile, the loop and the last PV:
+        # the loop is then entered only through the first tile's block, whose
+        # MFMAs already wait for the register-hoisted global fragments, so the
+        # compiler sees them complete at the loop head and puts no vmcnt(0)
+        # (which would also wait for this wave's ring DMAs) inside the loop.
+        q2 = q + "  "
         out.append(f"{q}if (({stop}) > {start}) {{")
-        out.append(f"{q}  const int {iv} = {start};")
-        self._emit_ops(pre, out, depth + 2)
-        self._emit_exact(body[fused_at], out, depth + 2)   # the running max starts at -inf
-        out.append(f"{q}}}")
-        out.append(f"{q}int {iv} = ({start}) + 1;")
-        out.append(f"{q}for (;;) {{")
-        out.append(f"{q}  bool wir_exact = false;")
-        out.append(f"{q}  for (; {iv} < {stop}; ++{iv}) {{")
-        shifted_post(depth + 3)      # PV of the previous iteration
+        out.append(f"{q2}{{")
+        out.append(f"{q2}  const int {iv} = {start};")
         self._emit_ops(pre, out, depth + 3)
-        fast_call(depth + 3)
-        out.append(f"{q}  }}")
-        out.append(f"{q}  if (!wir_exact) break;")
-        self._emit_exact(body[fused_at], out, depth + 2)
-        out.append(f"{q}  ++{iv};")
-        out.append(f"{q}}}")
-        out.append(f"{q}if (({stop}) > {start}) {{")
-        out.append(f"{q}  const int {iv} = ({stop});")
-        shifted_post(depth + 2)      # PV of the last iteration
+        self._emit_exact(body[fused_at], out, depth + 3)   # the running max starts at -inf
+        out.append(f"{q2}}}")
+        out.append(f"{q2}int {iv} = ({start}) + 1;")
+        out.append(f"{q2}for (;;) {{")
+        out.append(f"{q2}  bool wir_exact = false;")
+        out.append(f"{q2}  for (; {iv} < {stop}; ++{iv}) {{")
+        shifted_post(depth + 4)      # PV of the previous iteration
+        self._emit_ops(pre, out, depth + 4)
+        fast_call(depth + 4)
+        out.append(f"{q2}  }}")
+        out.append(f"{q2}  if (!wir_exact) break;")
+        self._emit_exact(body[fused_at], out, depth + 3)
+        out.append(f"{q2}  ++{iv};")
+        out.append(f"{q2}}}")
+        out.append(f"{q2}{{")
+        out.append(f"{q2}  const int {iv} = ({stop});")
+        shifted_post(depth + 3)      # PV of the last iteration
+        out.append(f"{q2}}}")
         out.append(f"{q}}}")
         out.append(f"{pad}}}")
 
@@ -1620,52 +1628,60 @@ class CDNA4Lowerer:
             m_barrier(d)
 
         # the first iteration (no PV yet) is peeled so the loop body's PV is
-        # unconditional and O keeps one register assignment around the loop
+        # unconditional and O keeps one register assignment around the loop.
+        # One guard holds the peeled iteration, the loop and the last M phase:
+        # the loop is entered only through the peeled iteration, whose QK
+        # MFMAs already wait for the register-hoisted Q, so the compiler puts
+        # no vmcnt(0) for Q in the loop (it would also wait for the ring DMAs
+        # this wave issued in its last V phase).
+        q2 = q + "  "
         out.append(f"{q}if (({stop}) > {start}) {{")
-        out.append(f"{q}  const int {iv} = {start};")
-        self._emit_op(qk, out, depth + 2)
-        m_barrier(depth + 2)
-        v_loads(depth + 2)
+        out.append(f"{q2}{{")
+        out.append(f"{q2}  const int {iv} = {start};")
+        self._emit_op(qk, out, depth + 3)
+        m_barrier(depth + 3)
+        v_loads(depth + 3)
         self._lazy_exact_only = True    # the first tile's running max is -inf
-        v_tail(softmax, depth + 2)
+        v_tail(softmax, depth + 3)
         self._lazy_exact_only = False
-        out.append(f"{q}}}")
+        out.append(f"{q2}}}")
         if fused_at is None:
-            out.append(f"{q}for (int {iv} = ({start}) + 1; {iv} < {stop}; ++{iv}) {{")
-            m_phase(depth + 2)
-            v_loads(depth + 2)
-            v_tail(softmax, depth + 2)
-            out.append(f"{q}}}")
+            out.append(f"{q2}for (int {iv} = ({start}) + 1; {iv} < {stop}; ++{iv}) {{")
+            m_phase(depth + 3)
+            v_loads(depth + 3)
+            v_tail(softmax, depth + 3)
+            out.append(f"{q2}}}")
         else:
             # A lazy softmax leaves the inner loop for its exact path (the
             # first tile was peeled above; later ones rarely rise above the
             # slack), so the inner loop touches O only through its MFMAs.
             fz = self._softmax_fused[id(softmax[fused_at])]
             pre, post = softmax[:fused_at], softmax[fused_at + 1:]
-            out.append(f"{q}int {iv} = ({start}) + 1;")
-            out.append(f"{q}for (;;) {{")
-            out.append(f"{q}  bool wir_exact = false;")
-            out.append(f"{q}  for (; {iv} < {stop}; ++{iv}) {{")
-            m_phase(depth + 3)
-            v_loads(depth + 3)
-            self._emit_ops(pre, out, depth + 3)
-            out.append(f"{q}    if (!{self._fast_call(fz)}) {{")
-            out.append(f"{q}      wir_exact = true;")
-            out.append(f"{q}      break;")
-            out.append(f"{q}    }}")
+            out.append(f"{q2}int {iv} = ({start}) + 1;")
+            out.append(f"{q2}for (;;) {{")
+            out.append(f"{q2}  bool wir_exact = false;")
+            out.append(f"{q2}  for (; {iv} < {stop}; ++{iv}) {{")
+            m_phase(depth + 4)
+            v_loads(depth + 4)
+            self._emit_ops(pre, out, depth + 4)
+            out.append(f"{q2}    if (!{self._fast_call(fz)}) {{")
+            out.append(f"{q2}      wir_exact = true;")
+            out.append(f"{q2}      break;")
+            out.append(f"{q2}    }}")
             for src, dst in (("m_in", "m_out"), ("l_in", "l_out"), ("o_in", "o_out")):
                 self._var_override[self.resolve(fz[dst].name)] = self._var(fz[src])
+            v_tail(post, depth + 4)
+            out.append(f"{q2}  }}")
+            out.append(f"{q2}  if (!wir_exact) break;")
+            self._emit_exact(softmax[fused_at], out, depth + 3)   # the step's exact half
             v_tail(post, depth + 3)
-            out.append(f"{q}  }}")
-            out.append(f"{q}  if (!wir_exact) break;")
-            self._emit_exact(softmax[fused_at], out, depth + 2)   # the step's exact half
-            v_tail(post, depth + 2)
-            out.append(f"{q}  ++{iv};")
-            out.append(f"{q}}}")
+            out.append(f"{q2}  ++{iv};")
+            out.append(f"{q2}}}")
         # the last M phase: PV of the last iteration
-        out.append(f"{q}if (({stop}) > {start}) {{")
-        out.append(f"{q}  const int {iv} = ({stop});")
-        emit_pv(out, depth + 2)
+        out.append(f"{q2}{{")
+        out.append(f"{q2}  const int {iv} = ({stop});")
+        emit_pv(out, depth + 3)
+        out.append(f"{q2}}}")
         out.append(f"{q}}}")
         if not one:
             out.append(f"{q}if (wir_grp == 0) wir::wait_vm_barrier<0>();   // pairs with group B's extra V phase")
