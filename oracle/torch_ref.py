@@ -85,6 +85,37 @@ def attention_bwd_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, do: tor
     return tuple(torch.stack(a).reshape(*lead, *a[0].shape) for a in outs)
 
 
+def attention_bwd_ref_bf16(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                           do: torch.Tensor, scale: Optional[float] = None, causal: bool = False,
+                           round_operands: bool = True):
+    """``(dQ, dK, dV)`` with the reference backward's bf16 MMA operands
+    (``kernel_examples/attention/mha_h100.cu:418-448``, dQ ``:132``): P = exp(S - LSE)
+    rounded to bf16 for ``dV = P^T dO`` (``:436, :443``); ``dS = P (dP - D)`` times the
+    softmax scale, rounded to bf16 for ``dK = dS^T Q`` and ``dQ = dS K`` (``:438-448``);
+    ``D = rowsum(dO * O)`` from the given (stored) O.  fp32 elsewhere, on the inputs' device,
+    per leading index.  ``round_operands=False`` is the exact gradient (equal to
+    ``attention_bwd_ref`` when ``o`` is the exact output)."""
+    scale = scale if scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    rnd = (lambda t: t.to(torch.bfloat16).float()) if round_operands else (lambda t: t)
+    lead = q.shape[:-2]
+    qf, kf, vf, of, dof = (t.float().reshape(-1, *t.shape[-2:]) for t in (q, k, v, o, do))
+    outs = ([], [], [])
+    for n in range(qf.shape[0]):
+        s = (qf[n] @ kf[n].t().contiguous()) * scale
+        if causal:
+            rows, cols = s.shape
+            s = s.masked_fill(torch.ones(rows, cols, dtype=torch.bool, device=s.device).triu(1), float("-inf"))
+        p = torch.softmax(s, dim=-1)
+        dv = rnd(p).t().contiguous() @ dof[n]
+        dp = dof[n] @ vf[n].t().contiguous()
+        d = (dof[n] * of[n]).sum(-1, keepdim=True)
+        ds = rnd(p * (dp - d) * scale)
+        outs[0].append(ds @ kf[n])
+        outs[1].append(ds.t().contiguous() @ qf[n])
+        outs[2].append(dv)
+    return tuple(torch.stack(a).reshape(*lead, *a[0].shape) for a in outs)
+
+
 def rel_err(out: torch.Tensor, ref: torch.Tensor) -> float:
     """``max|out - ref| / max|ref|`` -- the acceptance metric (bar: 1e-2)."""
     out, ref = out.float(), ref.float()

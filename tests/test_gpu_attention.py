@@ -210,6 +210,35 @@ def test_grouped_query_attention(gpu, b, hq, hkv, s, d, causal):
         assert err <= TOL, (name, err)
 
 
+@pytest.mark.parametrize("b,hq,hkv,s,d,causal", [(2, 2, 2, 512, 128, False), (2, 3, 3, 640, 64, True),
+                                                 (1, 4, 2, 384, 128, True), (3, 1, 1, 704, 128, False)])
+def test_backward_with_sharp_softmax(gpu, b, hq, hkv, s, d, causal):
+    """Keys scaled by 3 make the softmax sharp, where the bf16 MMA operands of
+    a FlashAttention backward (P for dV, dS for dQ and dK) set the error: the
+    gradients stay within 1e-2 of a reference with the reference backward's
+    own bf16 roundings (``attention_bwd_ref_bf16``), and within 2e-2 of the
+    exact fp32 gradient (which that rounded reference also reaches, so the
+    exact bar is the operands', not the kernels')."""
+    from oracle.torch_ref import attention_bwd_ref, attention_bwd_ref_bf16
+    announce(f"backward sharp softmax B={b} Hq={hq} Hkv={hkv} S={s} D={d} causal={causal}")
+    hr = hq // hkv
+    q, do = seeded_normal((b, hq, s, d), 41), seeded_normal((b, hq, s, d), 44)
+    k = (seeded_normal((b, hkv, s, d), 42).float() * 3).to(torch.bfloat16)
+    v = seeded_normal((b, hkv, s, d), 43)
+    o, lse = api.attention_forward(q.cuda(), k.cuda(), v.cuda(), causal=causal)
+    dq, dk, dv = api.attention_backward(q.cuda(), k.cuda(), v.cuda(), o, lse, do.cuda(), causal=causal)
+    torch.cuda.synchronize()
+    kx, vx = k.repeat_interleave(hr, 1).cuda(), v.repeat_interleave(hr, 1).cuda()
+    rounded = list(attention_bwd_ref_bf16(q.cuda(), kx, vx, o, do.cuda(), causal=causal))
+    exact = list(attention_bwd_ref(q.cuda(), kx, vx, do.cuda(), causal=causal))
+    for refs in (rounded, exact):   # per key/value head: the sum over its query heads
+        for j in (1, 2):
+            refs[j] = refs[j].view(b, hkv, hr, s, d).sum(2)
+    for name, got, r_rounded, r_exact in zip(("dQ", "dK", "dV"), (dq, dk, dv), rounded, exact):
+        assert rel_err(got, r_rounded) <= TOL, (name, rel_err(got, r_rounded))
+        assert rel_err(got, r_exact) <= 2 * TOL, (name, rel_err(got, r_exact))
+
+
 def test_grouped_query_rejects_bad_head_counts(gpu):
     q = torch.zeros(1, 6, 128, 128, dtype=torch.bfloat16, device="cuda")
     k = torch.zeros(1, 4, 128, 128, dtype=torch.bfloat16, device="cuda")
