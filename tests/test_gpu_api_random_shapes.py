@@ -126,3 +126,27 @@ def test_attention_empty_shapes(gpu, b, hq, hkv, s, d, causal):
     torch.cuda.synchronize()
     assert o.shape == q.shape and tuple(lse.shape) == (b, hq, s)
     assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+
+
+@pytest.mark.parametrize("b,s,h,d,causal", [(2, 256, 4, 128, False), (1, 384, 3, 64, True), (2, 192, 2, 128, True)])
+def test_attention_on_transposed_views_of_packed_qkv(gpu, b, s, h, d, causal):
+    """Q, K, V as ``[B, H, S, D]`` views of one packed ``[B, S, 3, H, D]`` tensor
+    (the layout a QKV projection produces): the kernels take the row, head and
+    batch strides as given, forward and backward, and O comes out in the same
+    dimension order."""
+    announce(f"api.attention packed-QKV views B={b} S={s} H={h} D={d} causal={causal}")
+    torch.manual_seed(b * 100 + s + h + d)
+    base = torch.randn(b, s, 3, h, d, device="cuda").to(torch.bfloat16)
+    q, k, v = (base[:, :, i].transpose(1, 2) for i in range(3))
+    assert not q.is_contiguous()
+    o, lse = api.attention_forward(q, k, v, causal=causal)
+    do = torch.randn(b, s, h, d, device="cuda").to(torch.bfloat16).transpose(1, 2)
+    dq, dk, dv = api.attention_backward(q, k, v, o, lse, do, causal=causal)
+    torch.cuda.synchronize()
+    ref, ref_lse = attention_ref(q.contiguous(), k.contiguous(), v.contiguous(), causal=causal)
+    assert o.stride() == (s * h * d, d, h * d, 1)   # empty_like keeps the [B, S, H, D] order, compacted
+    assert rel_err(o, ref) <= TOL
+    assert (lse - ref_lse).abs().max().item() <= 1e-3 * ref_lse.abs().max().item() + 1e-3
+    refs = attention_bwd_ref(q.contiguous(), k.contiguous(), v.contiguous(), do.contiguous(), causal=causal)
+    for name, got, r in zip(("dQ", "dK", "dV"), (dq, dk, dv), refs):
+        assert rel_err(got, r) <= TOL, (name, rel_err(got, r))
