@@ -70,13 +70,18 @@ def test_final_store_is_staged_through_lds():
     assert "store_tile_staged" not in plain and "wir::store_tile(" in plain
     # the attention output is staged; its fp32 LSE column vector is stored directly
     fa = CDNA4Lowerer().lower(kernels.kernel("mha_d128"))
-    assert "store_tile_staged(globals.O" in fa and "store_vec(globals.L" in fa
+    assert "store_tile_staged<true>(globals.O" in fa and "store_vec(globals.L" in fa
+    # the staged stores carry the non-temporal hint unless the target turns it off
+    assert "store_tile_staged<true>(" in tail
+    cached = CDNA4Lowerer(CDNA4Target(nontemporal_stores=False)).lower(kernels.kernel("gemm_256_k64"))
+    cached = cached[cached.rindex('extern "C" __global__'):]
+    assert "wir::store_tile_staged(" in cached and "store_tile_staged<true>" not in cached
     # the staging area is the K/V ring, into which the loop's last prefetch may still be landing:
     # every wave drains its DMAs (vmcnt 0) before the barrier that hands the LDS over
     for name in ("mha_d128", "mha_d64_causal", "mha_d128_w4", "mha_d128_ovl", "mha_bwd_dq_d128", "mha_bwd_dkdv_d128"):
         src = kernels.lowerer(name).lower(kernels.kernel(name))
         body = src[src.rindex('extern "C" __global__'):]
-        pre = body[: body.index("wir::store_tile_staged(")]
+        pre = body[: body.index("wir::store_tile_staged")]
         last_sync = max(pre.rfind("wir::barrier()"), pre.rfind("wir::wait_vm_barrier<"))
         assert pre[last_sync:].startswith("wir::wait_vm_barrier<0>();  // ring buffers dead"), name
 

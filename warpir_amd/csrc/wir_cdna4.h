@@ -1647,7 +1647,11 @@ __device__ __forceinline__ void reduce_slices(const gl<float>& part, const gl<bf
 // staged form writes the bf16 tile to LDS row-major (16-byte chunks XOR-
 // swizzled by row) and reads it back as whole rows, so each store
 // instruction writes C*2 contiguous bytes per row and 16 bytes per lane.
-template <int MS, int R, int C>
+// NT: the 16-byte stores carry the non-temporal hint.  The kernel never
+// reads its output back, and when every workgroup stores its tile at the
+// same time (equal-work grids), streaming the writes past the caches
+// shortens that burst.
+template <bool NT = false, int MS, int R, int C>
 __device__ __forceinline__ void store_tile_staged(const gl<bf16>& g, const RTile<MS, R, C>& t, int b, int d,
                                                   int row0, int col0, char* stage) {
   constexpr int CPR = C / 8;   // 16-byte chunks per row
@@ -1684,7 +1688,10 @@ __device__ __forceinline__ void store_tile_staged(const gl<bf16>& g, const RTile
     if (grow >= g.r) continue;
     bf16* p = base + (long long)grow * g.sr + gcol;
     if (vec_ok && gcol + 8 <= g.c) {
-      *(bf16x8*)p = v;
+      if (NT)
+        __builtin_nontemporal_store(v, (bf16x8*)p);
+      else
+        *(bf16x8*)p = v;
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j)

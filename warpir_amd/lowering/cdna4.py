@@ -97,6 +97,9 @@ class CDNA4Target:
     mve: bool = True
     # Final bf16 stores of register tiles go through LDS as whole rows.
     staged_stores: bool = True
+    # Those staged stores carry the non-temporal hint (wir::store_tile_staged<true>):
+    # measured +1.5% on GEMM 8192^3, +0.2-0.4% on the attention forwards.
+    nontemporal_stores: bool = True
     # Wave group (0 or 1) that issues each load stream (named by its ring,
     # e.g. "k", "v") in the 8-wavefront attention ping-pong.  None: take it
     # from the warp assigner's solution for the kernel (passes.warp_assigner).
@@ -1142,7 +1145,8 @@ class CDNA4Lowerer:
                 out.append(f"{pad}wir::wait_vm_barrier<0>();  // ring buffers dead: LDS becomes per-wave staging")
                 self._stage_barrier_done = True
             out.extend(self._consumer_only(
-                [f"{pad}wir::store_tile_staged({g}, {self._var(op.source)}, {b}, {d}, "
+                [f"{pad}wir::store_tile_staged{'<true>' if self.target.nontemporal_stores else ''}"
+                 f"({g}, {self._var(op.source)}, {b}, {d}, "
                  f"({rt}) * {sub.rows} + wave_row0, ({ct}) * {sub.cols} + wave_col0, "
                  f"smem + wir_wave * {self._staged[id(op)]});"], pad))
         elif isinstance(st, RegTileType):
