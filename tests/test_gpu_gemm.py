@@ -243,3 +243,21 @@ def test_split_k_fused_on_two_streams(gpu):
     torch.cuda.synchronize()
     assert all(torch.equal(o, ref) for o in outs)
     assert (a.device.index, s1.cuda_stream) in api._arrivals and (a.device.index, s2.cuda_stream) in api._arrivals
+
+
+def test_grid_outrunning_an_operand_reads_zeros(gpu):
+    """A launch whose C tile grid is taller than A: the in-bounds
+    specialisation's run-time conditions fail, so the kernel takes the
+    checked body and A's missing rows read as zeros (C's lower half is 0).
+    A is a view of the first half of a taller buffer, so even a wrong proof
+    would read valid memory; it would show as nonzero rows."""
+    announce("gemm_256_k64 grid taller than A")
+    k, n = 512, 256
+    big = seeded_normal((512, k), 51, 0.1).cuda()
+    a = big[:256]
+    b = seeded_normal((k, n), 52, 0.1).cuda()
+    c = torch.full((512, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+    kernels.handle("gemm_256_k64")(A=a, B=b, N=k, C_global=c)
+    torch.cuda.synchronize()
+    assert rel_err(c[:256], gemm_ref(a, b)) <= TOL
+    assert torch.equal(c[256:].float().cpu(), torch.zeros(256, n))

@@ -424,3 +424,48 @@ def test_lazy_attention_loop_sits_inside_the_first_tile_guard(name):
                  if body[i].strip() == "}" and len(body[i]) - len(body[i].lstrip()) == indent)
     assert close > loop
     assert any("mma_rAB" in l for l in body[loop:close] if "const int v_i" not in l)
+
+
+def _in_bounds_conditions(name):
+    src = kernels.lowerer(name).lower(kernels.kernel(name))
+    body = src[src.rindex('extern "C" __global__'):]
+    line = next(l for l in body.split("\n") if "const bool wir_aligned =" in l)
+    conds = line.split("=", 1)[1].rstrip(";").split(" && ")
+    return body, [c.strip() for c in conds if "Loader<" not in c]
+
+
+def _holds(conds, extents, grid, n):
+    env = dict(nx_=grid[0], ny_=grid[1], nz_=grid[2])
+    ok = True
+    for c in conds:
+        expr = c.replace("globals.N", str(n)).replace("/", "//")
+        for g, (b, d, r, col) in extents.items():
+            for k, v in (("b", b), ("d", d), ("r", r), ("c", col)):
+                expr = expr.replace(f"globals.{g}.{k}", str(v))
+        ok = ok and eval(expr, {}, env)   # noqa: S307 - integers and comparisons only
+    return ok
+
+
+def test_in_bounds_specialisation_only_where_every_tile_load_is_proved_inside():
+    """The reference buffer form with one ring depth drops the zero-page
+    selects (WIR_INB) under run-time conditions that put every tile it loads
+    inside its tensor: the grid's tile extent within each tensor, the loop's
+    tile count within K, and the prologue's tiles present.  The attention
+    prefetch form and per-ring depths keep the selects."""
+    body, conds = _in_bounds_conditions("gemm_256_k64")
+    assert "constexpr bool WIR_INB = WIR_AL && true;" in body
+    for name in ("mha_d128", "mha_d64_causal", api_splitk_variant()):
+        other, _ = _in_bounds_conditions(name)
+        assert "constexpr bool WIR_INB = WIR_AL && false;" in other, name
+    ext = lambda m, n, k: {"A": (1, 1, m, k), "B": (1, 1, k, n)}   # noqa: E731
+    assert _holds(conds, ext(8192, 8192, 8192), (32, 32, 1), 8192)
+    assert _holds(conds, ext(256, 256, 64), (1, 1, 1), 64)
+    assert not _holds(conds, ext(256, 512, 8192), (2, 2, 1), 8192)    # C grid twice A's rows
+    assert not _holds(conds, ext(512, 256, 8192), (2, 2, 1), 8192)    # ... or twice B's columns
+    assert not _holds(conds, ext(256, 256, 4096), (1, 1, 1), 8192)    # loop longer than K
+    assert not _holds(conds, ext(256, 256, 0), (1, 1, 1), 0)          # no prologue tile
+
+
+def api_splitk_variant():
+    from warpir_amd import api
+    return api.SPLITK_GEMM_VARIANT

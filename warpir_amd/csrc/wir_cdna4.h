@@ -208,13 +208,16 @@ struct Loader {
   // pitch fits the 32-bit offset form): a tile is either wholly inside or
   // wholly outside the tensor, so issue() is branch-free -- outside tiles
   // read the zero page at offset 0.  Otherwise tiles straddling an edge are
-  // loaded lane by lane with bounds checks.
-  template <bool ALIGNED>
+  // loaded lane by lane with bounds checks.  INB (with ALIGNED): the kernel
+  // has proved that every tile it loads lies inside the tensor, so neither
+  // the tile base nor a lane's offset selects the zero page.
+  template <bool ALIGNED, bool INB = false>
   static __device__ __forceinline__ Src prep(const gl<bf16>& g, int b, int d, int row0, int col0) {
+    static_assert(ALIGNED || !INB, "the in-bounds form is a case of the aligned one");
     const bool bd_ok = (unsigned)b < (unsigned)g.b && (unsigned)d < (unsigned)g.d;
     const bf16* bd = g.data + (long long)b * g.sb + (long long)d * g.sd;
     if (ALIGNED) {
-      const bool inb = bd_ok && (unsigned)row0 < (unsigned)g.r && (unsigned)col0 < (unsigned)g.c;
+      const bool inb = INB || (bd_ok && (unsigned)row0 < (unsigned)g.r && (unsigned)col0 < (unsigned)g.c);
       const bf16* t = inb ? bd + (long long)row0 * g.sr + col0 : (const bf16*)zero_page;
       return Src{t, inb, row0, col0};
     }
@@ -224,13 +227,13 @@ struct Loader {
   }
 
   // Issue this wave's j-th DMA instruction of the tile.
-  template <bool ALIGNED>
+  template <bool ALIGNED, bool INB = false>
   static __device__ __forceinline__ void issue(int j, char* tile_base, const gl<bf16>& g, const Src& s, int wave) {
     int row, c;
     place(wave, j, row, c);
     const unsigned dst = lds_addr(tile_base + (wave + j * NW) * 1024);
     if (ALIGNED) {
-      const unsigned voff = s.inb ? (unsigned)(row * (int)g.sr + c * 8) * 2u : 0u;
+      const unsigned voff = (INB || s.inb) ? (unsigned)(row * (int)g.sr + c * 8) * 2u : 0u;
       dma16_s(s.base, voff, dst);
       return;
     }
@@ -244,12 +247,12 @@ struct Loader {
     }
   }
 
-  template <bool ALIGNED>
+  template <bool ALIGNED, bool INB = false>
   static __device__ __forceinline__ void load(char* tile_base, const gl<bf16>& g, int b, int d, int row0,
                                               int col0, int wave) {
-    const Src src = prep<ALIGNED>(g, b, d, row0, col0);
+    const Src src = prep<ALIGNED, INB>(g, b, d, row0, col0);
 #pragma unroll
-    for (int j = 0; j < INSTR_PER_WAVE; ++j) issue<ALIGNED>(j, tile_base, g, src, wave);
+    for (int j = 0; j < INSTR_PER_WAVE; ++j) issue<ALIGNED, INB>(j, tile_base, g, src, wave);
   }
 
   // Whether `g` qualifies for the kernel's ALIGNED specialisation.
@@ -269,7 +272,7 @@ struct VecLoader {
   static constexpr int PER = N / NW;
   static_assert(N % NW == 0 && PER <= 64, "vector must split into at most 64 elements per wavefront");
 
-  template <bool ALIGNED>
+  template <bool ALIGNED, bool INB = false>   // (every vector load checks its rows)
   static __device__ __forceinline__ void load(char* tile_base, const gl<float>& g, int b, int d, int row0, int wave) {
     const int lane = lane_id();
     const int r = row0 + wave * PER + lane;

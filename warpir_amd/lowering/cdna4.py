@@ -846,7 +846,7 @@ class CDNA4Lowerer:
             src = op.source
             sub = src.type.sub_tile_type
             b, d, rt, ct = (self._int(c) for c in op.coords)
-            call = f"{self._load_call(op, 'load<WIR_AL>(', ptr, key)});"
+            call = f"{self._load_call(op, 'load<WIR_AL, WIR_INB>(', ptr, key)});"
             if self._ws:
                 who = self._ws_issuer(op.buf.name) if isinstance(op, TMALoadBufOp) else "wir_producer"
                 w(f"{pad}if ({who}) {call}")
@@ -888,14 +888,14 @@ class CDNA4Lowerer:
                     sub = ld.source.type.sub_tile_type
                     bb, dd, rt, ct = (self._int(c) for c in ld.coords)
                     self._aligned_checks.add((self.stile(lkey), _cname(ld.source.name)[2:]))
-                    w(f"{pad}const auto src{n_ld}_ = {loader}::prep<WIR_AL>({g}, {bb}, {dd}, ({rt}) * {sub.rows}, "
+                    w(f"{pad}const auto src{n_ld}_ = {loader}::prep<WIR_AL, WIR_INB>({g}, {bb}, {dd}, ({rt}) * {sub.rows}, "
                       f"({ct}) * {sub.cols});")
                     if self._ws and self.resolve(ld.buf.name) in self._ws_producer_streams:
-                        pcalls.append(f"if (q >= {ptotal} && q < {ptotal + n}) {loader}::issue<WIR_AL>(q - {ptotal}, "
+                        pcalls.append(f"if (q >= {ptotal} && q < {ptotal + n}) {loader}::issue<WIR_AL, WIR_INB>(q - {ptotal}, "
                                       f"{lptr}, {g}, src{n_ld}_, wir_wave);")
                         ptotal += n
                         continue
-                    calls.append(f"if (q >= {total} && q < {total + n}) {loader}::issue<WIR_AL>(q - {total}, "
+                    calls.append(f"if (q >= {total} && q < {total + n}) {loader}::issue<WIR_AL, WIR_INB>(q - {total}, "
                                  f"{lptr}, {g}, src{n_ld}_, wir_wave);")
                     total += n
                 if self._ws:
@@ -1063,9 +1063,9 @@ class CDNA4Lowerer:
                 sub = ld.source.type.sub_tile_type
                 bb, dd, rt, ct = (self._int(c) for c in ld.coords)
                 self._aligned_checks.add((self.stile(lkey), _cname(ld.source.name)[2:]))
-                out.append(f"{pad}const auto src{n_ld}_ = {loader}::prep<WIR_AL>({g}, {bb}, {dd}, ({rt}) * {sub.rows}, "
+                out.append(f"{pad}const auto src{n_ld}_ = {loader}::prep<WIR_AL, WIR_INB>({g}, {bb}, {dd}, ({rt}) * {sub.rows}, "
                            f"({ct}) * {sub.cols});")
-                calls.append(f"if (q >= {total} && q < {total + n}) {loader}::issue<WIR_AL>(q - {total}, "
+                calls.append(f"if (q >= {total} && q < {total + n}) {loader}::issue<WIR_AL, WIR_INB>(q - {total}, "
                              f"{lptr}, {g}, src{n_ld}_, wir_wave & 3);")
                 total += n
             out.append(f"{pad}{name}.step<{vm}, {total}>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int q) {{")
@@ -1521,7 +1521,7 @@ class CDNA4Lowerer:
             self._aligned_checks.add((self.stile(key), _cname(src.name)[2:]))
             pd = "  " * d
             return [f"{pd}{{ const int {aff} = {tile};",
-                    f"{pd}  wir::Loader<{self.stile(key)}, 4>::load<WIR_AL>((smem + {self.lds_off[key]} + "
+                    f"{pd}  wir::Loader<{self.stile(key)}, 4>::load<WIR_AL, WIR_INB>((smem + {self.lds_off[key]} + "
                     f"(({aff}) % {S}) * {stride}), globals.{_cname(src.name)[2:]}, {b}, {dd}, ({aff}) * {sub.rows}, "
                     f"({ct}) * {sub.cols}, wir_gw); }}"], per
 
@@ -1967,8 +1967,8 @@ class CDNA4Lowerer:
             r_ops(dst, d + 1)
             _, kc = src(kl, f"({j}) + 2")
             _, vc = src(vl, f"({j}) + 1")
-            dst.append(f"{p2}const auto wir_ks = {kload}::prep<WIR_AL>({kg}, {kc});")
-            dst.append(f"{p2}const auto wir_vs = {vload}::prep<WIR_AL>({vg}, {vc});")
+            dst.append(f"{p2}const auto wir_ks = {kload}::prep<WIR_AL, WIR_INB>({kg}, {kc});")
+            dst.append(f"{p2}const auto wir_vs = {vload}::prep<WIR_AL, WIR_INB>({vg}, {vc});")
             dst.append(f"{p2}for (int r_ = 0; r_ < {rb_n}; ++r_) wir_rs[r_] = 0.f;")
             dst.append(f"{p2}wir::mma_ABt_frags_slots<{ms}, {st.rows}, {st.cols}, {kstile}, {hf_ks}>"
                        f"({nxt}, {hf_var}, {kptr((par + 1) % 2)}, wave_col0, [&](auto t_) {{")
@@ -1977,9 +1977,9 @@ class CDNA4Lowerer:
                        f"P1 = ((T + 1) * {n_pairs} + WIR_NS - 1) / WIR_NS;")
             dst.append(f"{p2}  wir::e_pairs<P0, P1>({cur}, {p_var}, wir_rs, wir_ef);")
             dst.append(f"{p2}  if constexpr (T % 2 == 0 && T / 2 < {kper}) "
-                       f"{kload}::issue<WIR_AL>(T / 2, {kptr(par)}, {kg}, wir_ks, wir_wave);")
+                       f"{kload}::issue<WIR_AL, WIR_INB>(T / 2, {kptr(par)}, {kg}, wir_ks, wir_wave);")
             dst.append(f"{p2}  if constexpr (T % 2 == 1 && T / 2 < {vper}) "
-                       f"{vload}::issue<WIR_AL>(T / 2, {vptr((par + 1) % 2)}, {vg}, wir_vs, wir_wave);")
+                       f"{vload}::issue<WIR_AL, WIR_INB>(T / 2, {vptr((par + 1) % 2)}, {vg}, wir_vs, wir_wave);")
             dst.append(f"{p2}}});")
             dst.append(f"{p2}wir::mma_rAB_slots<{ms}, {a_t.rows}, {a_t.cols}, {res_t.cols}, {vstile}>"
                        f"({o_var}, {p_var}, {vptr(par)}, wave_col0, [&](auto t_) {{")
@@ -2058,7 +2058,7 @@ class CDNA4Lowerer:
         out.append(f"{p1}if (wir_n > 0) {{")
         p2 = p1 + "  "
         _, kc1 = src(kl, "1")
-        out.append(f"{p2}{kload}::load<WIR_AL>({kptr(1)}, {kg}, {kc1}, wir_wave);")
+        out.append(f"{p2}{kload}::load<WIR_AL, WIR_INB>({kptr(1)}, {kg}, {kc1}, wir_wave);")
         out.append(f"{p2}wir::wait_vm_barrier<{kper}>();")
         qk_plain(out, depth + 2, "wir_sa", 0)
         m_ops(out, depth + 2, "0", "wir_sa", False)
@@ -2281,10 +2281,18 @@ class CDNA4Lowerer:
         ]
         checks = " && ".join(f"wir::Loader<{t}, {self.geo.nw}>::aligned(globals.{g})"
                              for t, g in sorted(self._aligned_checks)) or "true"
+        inb = self._in_bounds_checks(kernel)
+        if inb:
+            # with these the aligned body needs no zero-page selects (WIR_INB): every tile it
+            # loads lies inside its tensor; a launch that fails them takes the checked body
+            checks += "".join(f" && {c}" for c in inb)
         src += [
             f"  const bool wir_aligned = {checks};",
             "  auto wir_body = [&](auto wir_tag) {",
             "  constexpr bool WIR_AL = decltype(wir_tag)::value;",
+            f"  constexpr bool WIR_INB = WIR_AL && {'true' if inb else 'false'};  "
+            f"// aligned tiles all inside the tensors",
+            "  (void)WIR_INB;",
             "  int wir_drain = 0;",
             "  (void)wave_row0; (void)wave_col0; (void)wir_drain;",
             *decls,
@@ -2294,6 +2302,56 @@ class CDNA4Lowerer:
                 "  else wir_body(wir::bool_tag<false>{});",
                 "}", ""]
         return "\n".join(src + body + tail)
+
+    def _in_bounds_checks(self, kernel: Kernel) -> List[str]:
+        """Run-time conditions under which every tile the kernel loads lies
+        inside its tensor, or ``[]`` when the kernel's form gives no such
+        proof.  The proof covers the reference buffer form with one depth
+        for every ring (MMAs on ring slots): the prologue loads tiles
+        ``0 .. start-1`` and iteration ``i`` tile ``i``, and every tile
+        coordinate is a constant, a grid index or the loop index.  Each
+        coordinate's largest value plus one, times its tile extent, must
+        fit the tensor's extent (``nx_`` / ``ny_`` / ``nz_`` for a grid
+        index, the loop's tile count for the loop index), and each loop must
+        have at least its prologue's ``start`` tiles.  The attention
+        prefetch form (slot views: it prefetches past the loop's end) and
+        per-ring depths (drain steps load past the end) rely on the zero
+        page instead."""
+        ops = list(_walk(kernel.body))
+        if (not any(isinstance(o, MMABufOp) for o in ops)
+                or any(isinstance(o, (SlotViewOp, DrainIndexOp, TMALoadOp)) for o in ops)):
+            return []
+        conds: List[str] = []
+        tiles_of: Dict[str, str] = {}
+        for op in kernel.body:
+            if not isinstance(op, ForOp):
+                continue
+            if not isinstance(op.start, int) or not isinstance(op.stop, Value) or op.stop not in kernel.inputs:
+                return []
+            tiles = f"globals.{_cname(op.stop.name)[2:]}"
+            if op.tile_size:
+                tiles = f"(({tiles}) + {op.tile_size - 1}) / {op.tile_size}"
+            tiles_of[op.induction_var.name] = tiles
+            conds.append(f"(({tiles}) >= {op.start})")
+        grid = {"blockIdx.x": "nx_", "blockIdx.y": "ny_", "blockIdx.z": "nz_"}
+        for op in ops:
+            if not isinstance(op, TMALoadBufOp):
+                continue
+            g = f"globals.{_cname(op.source.name)[2:]}"
+            sub = op.source.type.sub_tile_type
+            for c, unit, dim in zip(op.coords, (1, 1, sub.rows, sub.cols), "bdrc"):
+                if isinstance(c, int):
+                    count = str(c + 1)
+                elif isinstance(c, Value) and c.name in grid:
+                    count = grid[c.name]
+                elif isinstance(c, Value) and c.name in tiles_of:
+                    count = f"({tiles_of[c.name]})"
+                else:
+                    return []
+                cond = f"(({count}) * {unit} <= {g}.{dim})"
+                if cond not in conds:
+                    conds.append(cond)
+        return conds
 
     def _wave_tile(self) -> RegTileType:
         """The register tile shape that sets the wavefront slices: the first
