@@ -450,11 +450,12 @@ def test_in_bounds_specialisation_only_where_every_tile_load_is_proved_inside():
     """The reference buffer form with one ring depth drops the zero-page
     selects (WIR_INB) under run-time conditions that put every tile it loads
     inside its tensor: the grid's tile extent within each tensor, the loop's
-    tile count within K, and the prologue's tiles present.  The attention
-    prefetch form and per-ring depths keep the selects."""
+    tile count within K, and the prologue's tiles present.  The lazy
+    attention prefetch form (config 5's loop prefetches past its end) and
+    per-ring depths keep the selects."""
     body, conds = _in_bounds_conditions("gemm_256_k64")
     assert "constexpr bool WIR_INB = WIR_AL && true;" in body
-    for name in ("mha_d128", "mha_d64_causal", api_splitk_variant()):
+    for name in ("mha_d64_causal", api_splitk_variant()):
         other, _ = _in_bounds_conditions(name)
         assert "constexpr bool WIR_INB = WIR_AL && false;" in other, name
     ext = lambda m, n, k: {"A": (1, 1, m, k), "B": (1, 1, k, n)}   # noqa: E731
@@ -464,6 +465,32 @@ def test_in_bounds_specialisation_only_where_every_tile_load_is_proved_inside():
     assert not _holds(conds, ext(512, 256, 8192), (2, 2, 1), 8192)    # ... or twice B's columns
     assert not _holds(conds, ext(256, 256, 4096), (1, 1, 1), 8192)    # loop longer than K
     assert not _holds(conds, ext(256, 256, 0), (1, 1, 1), 0)          # no prologue tile
+
+
+def test_pingpong_attention_loads_its_own_prologue_and_proves_it_in_bounds():
+    """The 8-wave ping-pong issues its first K and V tiles itself, split
+    between its wave groups, so the aligned body skips the prefetch form's
+    prologue loads (the plain loop of unaligned tensors still issues them).
+    Its ring loads past the loop's end are skipped, so the in-bounds form
+    holds when the grid fits Q's batch and heads in K and V, the loop's tiles
+    fit K and V, and the unguarded prologue tiles (0 .. 2: K and V 0 .. 1,
+    group B's first V tile 2) are there."""
+    body, conds = _in_bounds_conditions("mha_d128")
+    assert "constexpr bool WIR_INB = WIR_AL && true;" in body
+    loads = [ln for ln in body.split("\n") if "::load<WIR_AL, WIR_INB>(" in ln]
+    prologue = [ln for ln in loads if ln.lstrip().startswith("if constexpr (!WIR_AL)")]
+    assert len(prologue) == 6                       # K and V tiles 0 .. 2 of the 4-slot rings
+    assert all("Loader<wir::STile<64, 128, 0>, 8>" in ln or "Loader<wir::STile<64, 128, 1>, 8>" in ln
+               for ln in prologue)
+    assert any(", 4>::load<" in ln for ln in loads)  # the ping-pong's own, four waves a group
+    ext = lambda b, h, s, d: {"K": (b, h, s, d), "V": (b, h, s, d)}   # noqa: E731
+    assert _holds(conds, ext(16, 16, 4096, 128), (16, 16, 16), 4096)
+    assert _holds(conds, ext(1, 1, 192, 128), (1, 1, 1), 192)        # exactly the prologue's tiles
+    assert not _holds(conds, ext(1, 1, 128, 128), (1, 1, 1), 128)    # the first V phase's tile 2 outside
+    assert not _holds(conds, ext(16, 16, 2048, 128), (16, 16, 16), 4096)   # loop longer than K
+    assert not _holds(conds, ext(8, 16, 4096, 128), (16, 16, 16), 4096)    # grid's batches past K's
+    assert not _holds(conds, ext(16, 8, 4096, 128), (16, 16, 16), 4096)    # ... or its heads
+    assert not _holds(conds, ext(16, 16, 4096, 64), (16, 16, 16), 4096)    # head dim below the tile
 
 
 def api_splitk_variant():

@@ -155,5 +155,13 @@ def test_generated_source_matches_the_model():
     assert "for (int wir_t = 0; wir_t < (0) + 3; ++wir_t)" in u2 and "% 5) * 16384" in u2
     d = loop("mha_d128")
     assert "group B's first V phase" in d and "wir_t < (0) + 2;" in d
+    # the model loads each tile once: the prefetch form's own prologue loads run only in the
+    # plain loop's body (tensors that are not tile-aligned), never before the ping-pong
+    for name in ("mha_d128", "mha_d128_u2"):
+        src = kernels.lowerer(name).lower(kernels.kernel(name))
+        body = src[src.rindex('extern "C" __global__'):]
+        before = body[:body.index("if constexpr (!WIR_AL) {")]
+        assert not [ln for ln in before.split("\n") if "::load<" in ln
+                    and not ln.lstrip().startswith("if constexpr (!WIR_AL) ")], name
     assert d.count(f"if (wir_grp == 1) wir::wait_vm_barrier_after<4>((v_i) + 2 < {stop});") == 2
     assert d.count(f"if ((v_i) + 3 < {stop})") == 2 and d.count(f"if ((v_i) + 2 < {stop})") == 2

@@ -208,9 +208,28 @@ class CDNA4Lowerer:
                     self._match_lazy_softmax(loop.body)
             if self.target.fold_softmax_scale:
                 self._plan_score_folds(kernel)
+        self._plan_pingpong_loops(kernel)
         body: List[str] = []
         self._emit_ops(kernel.body, body, 1)
         return self._assemble(kernel, body)
+
+    def _plan_pingpong_loops(self, kernel: Kernel) -> None:
+        """Record the top-level loops that take the attention ping-pong form,
+        and the prologue loads in front of each into its K and V rings: the
+        ping-pong issues those tiles itself (split between its wave groups),
+        so its aligned body skips them."""
+        prev: List[Op] = []
+        for op in kernel.body:
+            if not isinstance(op, ForOp):
+                prev.append(op)
+                continue
+            form = self._pingpong_form(op)
+            if form is not None:
+                self._pp_forms[id(op)] = form
+                rings = {self.resolve(form[0][k].buf.name) for k in ("k_load", "v_load")}
+                self._pp_prologue |= {id(o) for o in prev
+                                      if isinstance(o, TMALoadBufOp) and self.resolve(o.buf.name) in rings}
+            prev = []
 
     def launch_config(self, kernel: Kernel, tensors: Dict[str, Sequence[int]]) -> LaunchConfig:
         """Grid / block for concrete output shapes (``tensors``: name -> shape)."""
@@ -337,6 +356,8 @@ class CDNA4Lowerer:
         self._lazy_exact_only = False                # fused groups emit only the exact half
         self._score_folds: Dict[int, dict] = {}      # id(QK MMA) -> fold of its lazy-softmax group
         self._fold_live = False                      # inside a fused loop whose ScoreBias is declared
+        self._pp_forms: Dict[int, tuple] = {}        # id(top-level loop) -> its attention ping-pong form
+        self._pp_prologue: set = set()               # ids of prologue loads the ping-pong issues itself
 
     def _build_aliases(self, ops) -> None:
         """iter_arg init / loop results / yielded values -> block arg (``lowering.py:87-100``)."""
@@ -850,6 +871,8 @@ class CDNA4Lowerer:
             if self._ws:
                 who = self._ws_issuer(op.buf.name) if isinstance(op, TMALoadBufOp) else "wir_producer"
                 w(f"{pad}if ({who}) {call}")
+            elif id(op) in self._pp_prologue:
+                w(f"{pad}if constexpr (!WIR_AL) {call}   // the ping-pong loads its own prologue")
             else:
                 w(f"{pad}{call}")
             return
@@ -1440,6 +1463,28 @@ class CDNA4Lowerer:
         return dict(S=S, qk=qk, pv=pv, softmax=softmax, k_load=k_load, v_load=v_load, affine=affine[0],
                     yld=yld)
 
+    def _pingpong_form(self, loop: ForOp):
+        """``(plan, swap, one, every)`` when the attention ping-pong emitter
+        takes *loop* (its plan, the wave group of the K stream, the
+        one-barrier form, the iterations per barrier), else None."""
+        one = self.target.pingpong_one_barrier
+        every = self.target.pingpong_barrier_every if one else 1
+        if every not in (1, 2):
+            raise LoweringError(f"pingpong_barrier_every must be 1 or 2, not {every}")
+        plan = self._attention_pingpong_plan(loop)
+        if plan is None or plan["S"] < (4 if every == 1 else 5):
+            return None
+
+        def per(ld) -> int:   # DMAs per wave of one tile, four waves issuing
+            t = ld.buf.type.tile_type
+            return t.rows * t.cols * 2 // 1024 // 4
+        if per(plan["k_load"]) != per(plan["v_load"]):
+            return None
+        swap = self._pingpong_group_swap(plan)
+        if swap is None:
+            return None
+        return plan, swap, one, every
+
     def _pingpong_group_swap(self, plan) -> Optional[int]:
         """Which physical wave group (0: waves 0-3, 1: waves 4-7) issues the K
         stream -- the role that runs its MFMA phase first -- as the warp
@@ -1486,16 +1531,10 @@ class CDNA4Lowerer:
         issued in interval t - 2 and read in interval t + 1; the slot a load
         writes was last read two intervals (K) or one interval (V) before.
         """
-        plan = self._attention_pingpong_plan(loop)
-        one = self.target.pingpong_one_barrier
-        every = self.target.pingpong_barrier_every if one else 1
-        if every not in (1, 2):
-            raise LoweringError(f"pingpong_barrier_every must be 1 or 2, not {every}")
-        if plan is None or plan["S"] < (4 if every == 1 else 5):
+        form = self._pp_forms.get(id(loop))
+        if form is None:
             return False
-        swap = self._pingpong_group_swap(plan)
-        if swap is None:
-            return False
+        plan, swap, one, every = form
         pad = "  " * depth
         p1 = pad + "  "
         S, qk, pv = plan["S"], plan["qk"], plan["pv"]
@@ -1527,8 +1566,6 @@ class CDNA4Lowerer:
 
         k_ld, v_ld = plan["k_load"], plan["v_load"]
         per = dma(k_ld, "0", 0)[1]
-        if dma(v_ld, "0", 0)[1] != per:
-            return False
 
         npre = self.target.pingpong_v_prefetch
         pa_t, pr_t = pv.a.type, pv.result.type
@@ -2304,53 +2341,80 @@ class CDNA4Lowerer:
         return "\n".join(src + body + tail)
 
     def _in_bounds_checks(self, kernel: Kernel) -> List[str]:
-        """Run-time conditions under which every tile the kernel loads lies
-        inside its tensor, or ``[]`` when the kernel's form gives no such
-        proof.  The proof covers the reference buffer form with one depth
-        for every ring (MMAs on ring slots): the prologue loads tiles
-        ``0 .. start-1`` and iteration ``i`` tile ``i``, and every tile
-        coordinate is a constant, a grid index or the loop index.  Each
-        coordinate's largest value plus one, times its tile extent, must
-        fit the tensor's extent (``nx_`` / ``ny_`` / ``nz_`` for a grid
-        index, the loop's tile count for the loop index), and each loop must
-        have at least its prologue's ``start`` tiles.  The attention
-        prefetch form (slot views: it prefetches past the loop's end) and
-        per-ring depths (drain steps load past the end) rely on the zero
-        page instead."""
+        """Run-time conditions under which every tile the aligned body loads
+        lies inside its tensor, or ``[]`` when the kernel's form gives no
+        such proof.  Two forms carry one:
+
+        - the reference buffer form with one depth for every ring (MMAs on
+          ring slots): the prologue loads tiles ``0 .. start-1`` and
+          iteration ``i`` tile ``i``;
+        - the attention ping-pong (every top-level loop in that form): its
+          prologue loads tiles ``start .. start+P-1`` of K and V (P = ring
+          slots - 2, plus the one V tile of group B's first phase with a
+          barrier every iteration) and its ring loads are skipped past the
+          loop's end.
+
+        Every tile coordinate is a constant, a grid index or the loop's tile.
+        Each coordinate's largest value plus one, times its tile extent, must
+        fit the tensor's extent (``nx_`` / ``ny_`` / ``nz_`` for a grid index,
+        the loop's tile count for the loop's tile, and for the ping-pong also
+        ``start + P``), and a buffer-form loop must have at least its
+        prologue's ``start`` tiles.  Other prefetch forms (slot views: they
+        prefetch past the loop's end) and per-ring depths (drain steps load
+        past the end) rely on the zero page instead.  Register-hoisted tiles
+        are loaded with their own bounds checks and need no condition."""
         ops = list(_walk(kernel.body))
-        if (not any(isinstance(o, MMABufOp) for o in ops)
-                or any(isinstance(o, (SlotViewOp, DrainIndexOp, TMALoadOp)) for o in ops)):
+        if any(isinstance(o, DrainIndexOp) or (isinstance(o, TMALoadOp)
+                                               and self.resolve(o.result.name) not in self._register_tiles)
+               for o in ops):
+            return []
+        loops = [op for op in kernel.body if isinstance(op, ForOp)]
+        pingpong = bool(loops) and all(id(op) in self._pp_forms for op in loops)
+        if not pingpong and (not any(isinstance(o, MMABufOp) for o in ops)
+                             or any(isinstance(o, SlotViewOp) for o in ops)):
             return []
         conds: List[str] = []
         tiles_of: Dict[str, str] = {}
-        for op in kernel.body:
-            if not isinstance(op, ForOp):
-                continue
+        rows_of: Dict[int, List[str]] = {}    # id(ring load) -> tile counts its row coordinate reaches
+        for op in loops:
             if not isinstance(op.start, int) or not isinstance(op.stop, Value) or op.stop not in kernel.inputs:
                 return []
             tiles = f"globals.{_cname(op.stop.name)[2:]}"
             if op.tile_size:
                 tiles = f"(({tiles}) + {op.tile_size - 1}) / {op.tile_size}"
-            tiles_of[op.induction_var.name] = tiles
-            conds.append(f"(({tiles}) >= {op.start})")
+            if pingpong:
+                plan, _swap, _one, every = self._pp_forms[id(op)]
+                npro = plan["S"] - 2 + (1 if every == 1 else 0)
+                for ld in (plan["k_load"], plan["v_load"]):
+                    rows_of[id(ld)] = [f"({tiles})", str(op.start + npro)]
+            else:
+                tiles_of[op.induction_var.name] = tiles
+                conds.append(f"(({tiles}) >= {op.start})")
         grid = {"blockIdx.x": "nx_", "blockIdx.y": "ny_", "blockIdx.z": "nz_"}
         for op in ops:
             if not isinstance(op, TMALoadBufOp):
                 continue
+            if pingpong and id(op) not in rows_of:
+                if id(op) in self._pp_prologue:
+                    continue          # not issued by the aligned body
+                return []
             g = f"globals.{_cname(op.source.name)[2:]}"
             sub = op.source.type.sub_tile_type
-            for c, unit, dim in zip(op.coords, (1, 1, sub.rows, sub.cols), "bdrc"):
-                if isinstance(c, int):
-                    count = str(c + 1)
+            for pos, (c, unit, dim) in enumerate(zip(op.coords, (1, 1, sub.rows, sub.cols), "bdrc")):
+                if pingpong and pos == 2:
+                    counts = rows_of[id(op)]
+                elif isinstance(c, int):
+                    counts = [str(c + 1)]
                 elif isinstance(c, Value) and c.name in grid:
-                    count = grid[c.name]
+                    counts = [grid[c.name]]
                 elif isinstance(c, Value) and c.name in tiles_of:
-                    count = f"({tiles_of[c.name]})"
+                    counts = [f"({tiles_of[c.name]})"]
                 else:
                     return []
-                cond = f"(({count}) * {unit} <= {g}.{dim})"
-                if cond not in conds:
-                    conds.append(cond)
+                for count in counts:
+                    cond = f"(({count}) * {unit} <= {g}.{dim})"
+                    if cond not in conds:
+                        conds.append(cond)
         return conds
 
     def _wave_tile(self) -> RegTileType:
