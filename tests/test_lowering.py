@@ -455,9 +455,8 @@ def test_in_bounds_specialisation_only_where_every_tile_load_is_proved_inside():
     per-ring depths keep the selects."""
     body, conds = _in_bounds_conditions("gemm_256_k64")
     assert "constexpr bool WIR_INB = WIR_AL && true;" in body
-    for name in ("mha_d64_causal", api_splitk_variant()):
-        other, _ = _in_bounds_conditions(name)
-        assert "constexpr bool WIR_INB = WIR_AL && false;" in other, name
+    other, _ = _in_bounds_conditions("mha_d64_causal")
+    assert "constexpr bool WIR_INB = WIR_AL && false;" in other
     ext = lambda m, n, k: {"A": (1, 1, m, k), "B": (1, 1, k, n)}   # noqa: E731
     assert _holds(conds, ext(8192, 8192, 8192), (32, 32, 1), 8192)
     assert _holds(conds, ext(256, 256, 64), (1, 1, 1), 64)
@@ -491,6 +490,70 @@ def test_pingpong_attention_loads_its_own_prologue_and_proves_it_in_bounds():
     assert not _holds(conds, ext(8, 16, 4096, 128), (16, 16, 16), 4096)    # grid's batches past K's
     assert not _holds(conds, ext(16, 8, 4096, 128), (16, 16, 16), 4096)    # ... or its heads
     assert not _holds(conds, ext(16, 16, 4096, 64), (16, 16, 16), 4096)    # head dim below the tile
+
+
+def _tile_loads(kernel, tiles, grid):
+    """Every tile load of a buffer-form kernel as (tensor, coordinates, tile
+    extents), interpreted from the IR for a loop of ``tiles`` tiles and the
+    largest program index of ``grid``: the loop runs from its start to
+    ``tiles - 1``, and a drain index is the count of buffered MMAs run so far
+    plus its offset."""
+    from warpir_amd.ir.ops import DrainIndexOp, ForOp, IntAffineOp, MMABufOp, TMALoadBufOp
+    env = {"blockIdx.x": grid[0] - 1, "blockIdx.y": grid[1] - 1, "blockIdx.z": grid[2] - 1}
+    mmas, loads = [0], []
+
+    def val(x):
+        return x if isinstance(x, int) else env[x.name]
+
+    def run(ops):
+        for op in ops:
+            if isinstance(op, TMALoadBufOp):
+                sub = op.source.type.sub_tile_type
+                loads.append((op.source.name, tuple(val(c) for c in op.coords), (1, 1, sub.rows, sub.cols)))
+            elif isinstance(op, MMABufOp):
+                mmas[0] += 1
+            elif isinstance(op, DrainIndexOp):
+                env[op.result.name] = mmas[0] + op.offset
+            elif isinstance(op, IntAffineOp):
+                env[op.result.name] = val(op.input) * op.mul + op.add
+            elif isinstance(op, ForOp):
+                for i in range(op.start, tiles):
+                    env[op.induction_var.name] = i
+                    run(op.body)
+    run(kernel.body)
+    return loads
+
+
+@pytest.mark.parametrize("name", ["gemm_256_k64", "gemm_128x32_k64", "gemm_128_splitk_k128_b3",
+                                  "gemm_128_splitk_s5"])
+def test_in_bounds_conditions_cover_every_tile_load(name):
+    """Wherever the emitted conditions hold, every tile that the kernel's IR
+    loads (prologue, loop, drain steps with their drain indices, per-ring
+    shifts) lies inside its tensor; and the sweep does reach launches whose
+    loads leave a tensor, each of which the conditions reject.  Extents are
+    tile multiples (the aligned body's domain); the loop's tiles, the K
+    extent, the grid and the slice count vary."""
+    kernel = kernels.kernel(name)
+    _, conds = _in_bounds_conditions(name)
+    assert conds
+    tm, tn = 256 if "256" in name else 128, {"gemm_256_k64": 256, "gemm_128x32_k64": 32}.get(name, 128)
+    tk = kernels.lowerer(name).lower(kernel) and next(
+        o.tile_size for o in kernel.body if type(o).__name__ == "ForOp")
+    seen_outside = 0
+    for tiles in range(0, 7):
+        ks = sorted({max(tiles - 1, 0), tiles, tiles + 1})
+        for ka, kb in ((ka, kb) for ka in ks for kb in ks):
+            for slices in (1, 2):
+                for grid in ((1, 1, 1), (2, 1, 1), (1, 2, 1), (1, 1, slices), (1, 1, slices + 1)):
+                    ext = {"A": (1, slices, tm, ka * tk), "B": (1, slices, kb * tk, tn)}
+                    outside = []
+                    for src, coords, unit in _tile_loads(kernel, tiles, grid):
+                        if any(c < 0 or (c + 1) * u > e for c, u, e in zip(coords, unit, ext[src])):
+                            outside.append((src, coords))
+                    holds = _holds(conds, ext, grid, tiles * tk)
+                    assert not (holds and outside), (tiles, ka, kb, slices, grid, outside)
+                    seen_outside += bool(outside)
+    assert seen_outside
 
 
 def api_splitk_variant():

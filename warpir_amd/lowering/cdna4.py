@@ -2345,28 +2345,32 @@ class CDNA4Lowerer:
         lies inside its tensor, or ``[]`` when the kernel's form gives no
         such proof.  Two forms carry one:
 
-        - the reference buffer form with one depth for every ring (MMAs on
-          ring slots): the prologue loads tiles ``0 .. start-1`` and
-          iteration ``i`` tile ``i``;
+        - the reference buffer form (MMAs on ring slots): the prologue loads
+          tiles ``0 .. start-1``; iteration ``i`` loads tile ``i - k`` of a
+          ring whose loads run ``k`` stages behind the first (``k = 0`` with
+          one depth for every ring); a drain step loads tile ``drain + o``,
+          the MMA counter plus the step's offset, which with one loop of at
+          least ``start`` tiles is ``tiles - start + j + o`` in the drain's
+          ``j``-th step;
         - the attention ping-pong (every top-level loop in that form): its
           prologue loads tiles ``start .. start+P-1`` of K and V (P = ring
           slots - 2, plus the one V tile of group B's first phase with a
           barrier every iteration) and its ring loads are skipped past the
           loop's end.
 
-        Every tile coordinate is a constant, a grid index or the loop's tile.
-        Each coordinate's largest value plus one, times its tile extent, must
-        fit the tensor's extent (``nx_`` / ``ny_`` / ``nz_`` for a grid index,
-        the loop's tile count for the loop's tile, and for the ping-pong also
-        ``start + P``), and a buffer-form loop must have at least its
-        prologue's ``start`` tiles.  Other prefetch forms (slot views: they
-        prefetch past the loop's end) and per-ring depths (drain steps load
-        past the end) rely on the zero page instead.  Register-hoisted tiles
-        are loaded with their own bounds checks and need no condition."""
+        Every tile coordinate is a constant, a grid index, the loop's tile
+        (shifted by a constant) or a drain index.  Each coordinate's largest
+        value plus one, times its tile extent, must fit the tensor's extent
+        (``nx_`` / ``ny_`` / ``nz_`` for a grid index, the loop's tile count
+        plus the shift for the loop's tile, and for the ping-pong also
+        ``start + P``); a buffer-form loop must have at least its prologue's
+        ``start`` tiles, and no coordinate may be negative.  The lazy
+        attention prefetch form (slot views outside the ping-pong: it
+        prefetches past the loop's end) relies on the zero page instead.
+        Register-hoisted tiles are loaded with their own bounds checks and
+        need no condition."""
         ops = list(_walk(kernel.body))
-        if any(isinstance(o, DrainIndexOp) or (isinstance(o, TMALoadOp)
-                                               and self.resolve(o.result.name) not in self._register_tiles)
-               for o in ops):
+        if any(isinstance(o, TMALoadOp) and self.resolve(o.result.name) not in self._register_tiles for o in ops):
             return []
         loops = [op for op in kernel.body if isinstance(op, ForOp)]
         pingpong = bool(loops) and all(id(op) in self._pp_forms for op in loops)
@@ -2374,8 +2378,8 @@ class CDNA4Lowerer:
                              or any(isinstance(o, SlotViewOp) for o in ops)):
             return []
         conds: List[str] = []
-        tiles_of: Dict[str, str] = {}
-        rows_of: Dict[int, List[str]] = {}    # id(ring load) -> tile counts its row coordinate reaches
+        counts_of: Dict[str, List[str]] = {}  # integer value -> tile counts its coordinate reaches
+        rows_of: Dict[int, List[str]] = {}    # id(ping-pong ring load) -> tile counts of its row coordinate
         for op in loops:
             if not isinstance(op.start, int) or not isinstance(op.stop, Value) or op.stop not in kernel.inputs:
                 return []
@@ -2387,9 +2391,30 @@ class CDNA4Lowerer:
                 npro = plan["S"] - 2 + (1 if every == 1 else 0)
                 for ld in (plan["k_load"], plan["v_load"]):
                     rows_of[id(ld)] = [f"({tiles})", str(op.start + npro)]
-            else:
-                tiles_of[op.induction_var.name] = tiles
-                conds.append(f"(({tiles}) >= {op.start})")
+                continue
+            conds.append(f"(({tiles}) >= {op.start})")
+            iv = op.induction_var.name
+            counts_of[iv] = [f"({tiles})"]
+            for o in op.body:
+                if isinstance(o, IntAffineOp) and isinstance(o.input, Value) and o.input.name == iv:
+                    if o.mul != 1 or op.start + o.add < 0:
+                        return []
+                    counts_of[o.result.name] = [f"({tiles}) + {o.add}" if o.add else f"({tiles})"]
+        if not pingpong:
+            # drain indices: wir_drain counts the buffered MMAs, one per loop iteration and one
+            # per drain step, so only a kernel with a single loop gives them a closed form
+            loop, j = None, 0
+            for op in kernel.body:
+                if isinstance(op, ForOp):
+                    loop, j = op, 0
+                elif isinstance(op, MMABufOp):
+                    j += 1
+                elif isinstance(op, DrainIndexOp):
+                    if loop is None or len(loops) != 1 or j + op.offset < 0:
+                        return []
+                    tiles = counts_of[loop.induction_var.name][0]
+                    extra = j + op.offset + 1 - loop.start
+                    counts_of[op.result.name] = [f"{tiles} + {extra}" if extra else tiles]
         grid = {"blockIdx.x": "nx_", "blockIdx.y": "ny_", "blockIdx.z": "nz_"}
         for op in ops:
             if not isinstance(op, TMALoadBufOp):
@@ -2404,11 +2429,13 @@ class CDNA4Lowerer:
                 if pingpong and pos == 2:
                     counts = rows_of[id(op)]
                 elif isinstance(c, int):
+                    if c < 0:
+                        return []
                     counts = [str(c + 1)]
                 elif isinstance(c, Value) and c.name in grid:
                     counts = [grid[c.name]]
-                elif isinstance(c, Value) and c.name in tiles_of:
-                    counts = [f"({tiles_of[c.name]})"]
+                elif isinstance(c, Value) and c.name in counts_of:
+                    counts = counts_of[c.name]
                 else:
                     return []
                 for count in counts:
