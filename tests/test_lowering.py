@@ -399,7 +399,7 @@ def test_per_ring_gemm_lowering_merges_ring_waits():
     flight, and the drain counter counts MMAs (a drain_index reads it) and is reduced per ring."""
     name = "gemm_128_splitk_k128_b3"
     src = kernels.lowerer(name).lower(kernels.kernel(name))
-    loop = src[src.index("for (; wir_base_i + 6 <="):src.index("pipe0.finish")]
+    loop = src[src.index("for (; WIR_AL && wir_base_i + 6 <="):src.index("pipe0.finish")]
     assert loop.count("const int v_i = wir_base_i + ") == 6
     assert loop.count("wir::wait_vm_barrier<8>();") == 7   # six copies and the remainder loop
     assert "wir::wait_vm_barrier<" not in loop.replace("wir::wait_vm_barrier<8>();", "")

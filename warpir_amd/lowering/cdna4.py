@@ -1278,7 +1278,9 @@ class CDNA4Lowerer:
             return
         base = f"wir_base_{iv[2:]}"
         out.append(f"{pad}int {base} = {op.start};")
-        out.append(f"{pad}for (; {base} + {m} <= ({stop}); {base} += {m}) {{")
+        # only the aligned body unrolls: the checked body's per-chunk bounds state times m copies
+        # spilled (gemm_256_k64: 11 VGPRs, 43 SGPRs), and it runs every trip in the remainder loop
+        out.append(f"{pad}for (; WIR_AL && {base} + {m} <= ({stop}); {base} += {m}) {{")
         for u in range(m):
             self._slot_const[ivn] = (op.start + u) % m
             out.append(f"{pad}  {{")
