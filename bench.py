@@ -41,8 +41,9 @@ METRIC = "bf16 TFLOP/s + % MFMA peak: GEMM 8192³ and FA-fwd B16 H16 S4096 D128"
 def _time_launches(launch, steps: int, warmup: int, stream, per_launch: bool = False):
     """Mean ms per launch over ``steps`` back-to-back launches (one event pair
     around all of them) and the wall-clock mean; with ``per_launch``, also the
-    median of ``steps`` launches each bracketed by its own event pair (the
-    reference's method, tests/test_modal_gpu.py:126-152).  Returns
+    median of ``steps`` launches each bracketed by its own event pair and
+    followed by a device synchronisation (the reference's method,
+    tests/test_modal_gpu.py:126-152).  Returns
     ``(mean_ms, wall_ms, median_ms or None)``."""
     import torch
 
@@ -67,7 +68,7 @@ def _time_launches(launch, steps: int, warmup: int, stream, per_launch: bool = F
             a.record(stream)
             launch()
             b.record(stream)
-        torch.cuda.synchronize()
+            torch.cuda.synchronize()
         median = statistics.median(a.elapsed_ms(b) for a, b in pairs)
     return mean, wall * 1e3 / steps, median
 

@@ -33,7 +33,7 @@ def test_reference_attention_ir(gpu, n):
 
 @pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_vp4", "mha_d128_vp8", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp_swapped", "mha_d128_w4",
                                      "mha_d128_online", "mha_d128_ovl", "mha_d128_s5", "mha_d128_pp2b",
-                                     "mha_d128_fold", "mha_d128_u2"])
+                                     "mha_d128_fold", "mha_d128_u2", "mha_d128_mr", "mha_d128_dma_sc1"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 1, 64)])
 def test_mha_d128(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")
@@ -68,7 +68,7 @@ def test_mha_d128_causal(gpu, b, h, s):
 
 
 @pytest.mark.parametrize("variant", ["mha_d64_causal", "mha_d64_causal_ssa", "mha_d64_causal_online", "mha_d64_causal_ovl",
-                                     "mha_d64_causal_pp", "mha_d64_causal_fold"])
+                                     "mha_d64_causal_pp", "mha_d64_causal_fold", "mha_d64_causal_mr"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 2, 512), (1, 2, 1024), (1, 1, 192)])
 def test_mha_d64_causal(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")
@@ -83,7 +83,8 @@ def test_mha_d64_causal(gpu, variant, b, h, s):
 @pytest.mark.parametrize("variant,d,causal", [("mha_d128", 128, False), ("mha_d128_w4", 128, False),
                                               ("mha_d128_u2", 128, False),
                                               ("mha_d64_causal", 64, True), ("mha_d128_ovl", 128, False),
-                                              ("mha_d64_causal_ovl", 64, True), ("mha_d64_causal_pp", 64, True)])
+                                              ("mha_d64_causal_ovl", 64, True), ("mha_d64_causal_pp", 64, True),
+                                              ("mha_d128_mr", 128, False), ("mha_d64_causal_mr", 64, True)])
 def test_mha_lazy_rescale_with_growing_scores(gpu, variant, d, causal):
     """Keys grow along the sequence, so the running max moves by more than
     the slack on later tiles and the rescale path runs too."""

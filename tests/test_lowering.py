@@ -559,3 +559,49 @@ def test_in_bounds_conditions_cover_every_tile_load(name):
 def api_splitk_variant():
     from warpir_amd import api
     return api.SPLITK_GEMM_VARIANT
+
+
+def test_dma_cache_policy_option():
+    """CDNA4Target.dma_cache_policy: the modifiers reach the tile DMAs through a define ahead of
+    the tile library (canonical order), the default emits none, and unknown or repeated words
+    are rejected."""
+    k = kernels.kernel("gemm_256_k64")
+    assert '#define WIR_DMA_CPOL " ' not in CDNA4Lowerer().lower(k)
+    src = CDNA4Lowerer(CDNA4Target(dma_cache_policy="nt sc1")).lower(k)
+    assert src.index('#define WIR_DMA_CPOL " sc1 nt"') < src.index("#ifndef WIR_DMA_CPOL")
+    for bad in ("sc2", "nt nt", "glc"):
+        with pytest.raises(ValueError):
+            CDNA4Lowerer(CDNA4Target(dma_cache_policy=bad)).lower(k)
+
+
+def test_rowsum_mfma_option_emits_matrix_core_sums():
+    """CDNA4Target.rowsum_mfma: the speculative softmax half becomes lazy_softmax_fast_mr."""
+    name = "mha_d64_causal"
+    base = kernels.lowerer(name).lower(kernels.kernel(name))
+    mr = CDNA4Lowerer(CDNA4Target(rowsum_mfma=True)).lower(kernels.kernel(name))
+    body = lambda s: s[s.rindex('extern "C" __global__'):]  # noqa: E731
+    assert "lazy_softmax_fast(" in body(base) and "lazy_softmax_fast_mr(" not in body(base)
+    assert "lazy_softmax_fast_mr(" in body(mr) and "lazy_softmax_fast(" not in body(mr)
+
+
+def test_rowsum_selector_sums_a_rows_two_half_lanes():
+    """The layout argument of wir::rowsum_selector, checked on a model of v_mfma_f32_16x16x32_bf16
+    (A lane l: row l%16, k 8*(l/16)+j; B lane l: column l%16, the same k; C register i of lane l:
+    row 4*(l/16)+i, column l%16): with P's 8 values per lane as B, every C register of lane l is
+    the sum of lanes l%32 and l%32+32, i.e. its own row's sum in the lane = row layout."""
+    src = open(os.path.join(os.path.dirname(kernels.__file__), "csrc", "wir_cdna4.h")).read()
+    expr = re.search(r"const bf16 e = (.*) \? \(bf16\)1\.0f", src).group(1)
+    sel = [1.0 if eval(expr.replace("==", " == "), {"l": lane}) else 0.0 for lane in range(64)]
+    g = torch.Generator().manual_seed(0)
+    bvals = torch.rand(64, 8, generator=g, dtype=torch.float64)
+    a = torch.zeros(16, 32, dtype=torch.float64)
+    b = torch.zeros(32, 16, dtype=torch.float64)
+    for lane in range(64):
+        for j in range(8):
+            a[lane % 16, 8 * (lane // 16) + j] = sel[lane]
+            b[8 * (lane // 16) + j, lane % 16] = bvals[lane, j]
+    c = a @ b
+    for lane in range(64):
+        want = bvals[lane % 32].sum() + bvals[lane % 32 + 32].sum()
+        for i in range(4):
+            assert abs(c[4 * (lane // 16) + i, lane % 16] - want) < 1e-12, (lane, i)

@@ -151,16 +151,22 @@ struct STile {
 // ds_read and inserts s_waitcnt vmcnt(0) in front of it, which would
 // serialise every ring stage.  Completion is instead tracked by the
 // lowering itself (wait_vm_barrier<N> with N from its schedule analysis).
+//
+// WIR_DMA_CPOL: cache-policy modifiers appended to the tile DMAs (" sc0",
+// " sc1", " nt" or a combination; empty for the default policy).
+#ifndef WIR_DMA_CPOL
+#define WIR_DMA_CPOL ""
+#endif
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 // Uniform 64-bit base + per-lane 32-bit byte offset (the saddr form).
 __device__ __forceinline__ void dma16_s(const void* gbase, unsigned voff, unsigned lds_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" WIR_DMA_CPOL
                :: "v"(voff), "s"(gbase), "s"(lds_addr) : "memory", "m0");
 }
 // Per-lane 64-bit address.
 __device__ __forceinline__ void dma16_v(const void* gaddr, unsigned lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" WIR_DMA_CPOL
                :: "v"(gaddr), "s"(lds_addr) : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -1324,6 +1330,80 @@ template <int MS, int R, int C, int DO>
 __device__ __forceinline__ void lazy_softmax(const RTile<MS, R, C>& s, RVec<MS, R>& m, RVec<MS, R>& l,
                                              RTile<MS, R, DO>& o, BTile<MS, R, C>& pb, float c, float slack) {
   if (lazy_softmax_fast(s, m, l, pb, c, slack)) return;
+  lazy_softmax_exact(s, m, l, o, pb, c, slack);
+}
+
+// ---------------------------------------------------------------------------
+// Row sums on the matrix core.  A 32-row P tile (lane = row: lane l holds
+// row l%32, lanes l and l+32 complementary keys) is summed per row by
+// 16x16x32 MFMAs that take two of its 4-element groups (8 bf16 per lane)
+// as the B operand, against a 0/1 A operand.  The MFMA reads B lane L as
+// column L%16 of k block L/16; with A[m][k] = 1 exactly when the parities
+// of m/4 and k/8 agree, C row m sums the k blocks of its parity, so C
+// register i of lane l (row 4*(l/16)+i, column l%16) is the sum over
+// lanes {l%32, l%32+32}: every C register of a lane holds its own row's sum
+// of the 16 probabilities in those two groups.  Four such MFMAs cover a
+// 64-key tile, in place of 32 fp32 adds and a cross-lane reduction per lane.
+__device__ __forceinline__ bf16x8 rowsum_selector() {
+  const int l = lane_id();
+  const bf16 e = ((((l & 15) >> 2) ^ (l >> 4)) & 1) == 0 ? (bf16)1.0f : (bf16)0.0f;
+  bf16x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = e;
+  return v;
+}
+
+// lazy_softmax_fast with the row sums of the bf16 probabilities from the
+// matrix core (rowsum_selector).  The guard is checked on those sums: all
+// terms are non-negative and the MFMA adds them exactly from bf16 products,
+// so each bf16(p) is at most its row's sum, and a sum at most
+// 2^(slack*c) * (1 - 2^-8) bounds every p (at most 2^-9 above its bf16) below
+// 2^(slack*c): no score exceeds m + slack, exactly as in lazy_softmax_fast.
+// A full-row sum is at least a lane's partial sum, so the guard passes less
+// often than lazy_softmax_fast's (the exact half then runs, which computes
+// the same step).  l accumulates sums of the rounded probabilities that the
+// PV MFMAs multiply, in place of the fp32 ones (at most 2^-9 relative per
+// term).  32-row fragments (MS = 32) only.
+template <int MS, int R, int C>
+__device__ __forceinline__ bool lazy_softmax_fast_mr(const RTile<MS, R, C>& s, const RVec<MS, R>& m, RVec<MS, R>& l,
+                                                     BTile<MS, R, C>& pb, float c, float slack) {
+  static_assert(MS == 32, "matrix-core row sums take the 32x32 fragment layout");
+  constexpr int RB = R / MS, CB = C / MS, G = BTile<MS, R, C>::G;
+  static_assert((CB * G) % 2 == 0, "the key tile must fill whole 16x16x32 MFMAs");
+  const float guard = __builtin_amdgcn_exp2f(slack * c) * (1.0f - 1.0f / 256.0f);
+  const bf16x8 sel = rowsum_selector();
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        bf16x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (bf16)__builtin_amdgcn_exp2f(__builtin_fmaf(s.f[cb][rb][4 * g + j], c, -m.v[rb] * c));
+        pb.f[cb][rb][g] = v;
+      }
+  float sum[RB];
+  bool ok = true;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < CB * G; t += 2)
+      acc = MF<16>::mma(sel, cat(pb.f[t / G][rb][t % G], pb.f[(t + 1) / G][rb][(t + 1) % G]), acc);
+    sum[rb] = acc[0];
+    ok = ok && (sum[rb] <= guard);  // false for inf and NaN
+  }
+  if (__builtin_amdgcn_ballot_w64(!ok) != 0) return false;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) l.v[rb] += sum[rb];
+  return true;
+}
+
+template <int MS, int R, int C, int DO>
+__device__ __forceinline__ void lazy_softmax_mr(const RTile<MS, R, C>& s, RVec<MS, R>& m, RVec<MS, R>& l,
+                                                RTile<MS, R, DO>& o, BTile<MS, R, C>& pb, float c, float slack) {
+  if (lazy_softmax_fast_mr(s, m, l, pb, c, slack)) return;
   lazy_softmax_exact(s, m, l, o, pb, c, slack);
 }
 

@@ -246,6 +246,16 @@ TARGETS: Dict[str, dict] = {
                             "wave_groups": {"a": 1, "b": 1}},
     "mha_d64_causal_ovl": {"lazy_softmax": False},
 }
+# the lazy softmax's row sums on the matrix core (CDNA4Target.rowsum_mfma; config 5 within 0.3-0.7%
+# of the default, the config-4 ping-pong 5% slower)
+for _base in ("mha_d128", "mha_d64_causal"):
+    VARIANTS[f"{_base}_mr"] = VARIANTS[_base]
+    TARGETS[f"{_base}_mr"] = {"rowsum_mfma": True}
+# device-scope cache policy on the tile DMAs (CDNA4Target.dma_cache_policy) of the two headline
+# kernels (measured equal to the default policy; "nt" slower)
+for _base in ("gemm_256_k64", "mha_d128"):
+    VARIANTS[f"{_base}_dma_sc1"] = VARIANTS[_base]
+    TARGETS[f"{_base}_dma_sc1"] = {"dma_cache_policy": "sc1"}
 
 # The D=128 dK/dV kernels hold dK, dV and the score tiles in more than 256 registers.  With
 # the MFMAs' VGPR form the S and dP tiles stay in arch VGPRs (no v_accvgpr_read per score

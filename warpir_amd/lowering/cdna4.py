@@ -144,6 +144,17 @@ class CDNA4Target:
     # every barrier; gfx950 has no setmaxnreg, so both get the same register
     # allocation (two waves per SIMD: at most 256 per lane).
     warp_specialize: bool = False
+    # Cache-policy bits on the tile loads' global_load_lds instructions: "" (the
+    # default policy), or any of "sc0", "sc1", "nt" joined by spaces (gfx950's
+    # scope and non-temporal bits).  The tiles are read once per workgroup, so
+    # nothing on the path re-reads them from the CU's L1.
+    dma_cache_policy: str = ""
+    # The lazy softmax's speculative half sums each row's bf16 probabilities
+    # on the matrix core (wir::lazy_softmax_fast_mr: four 16x16x32 MFMAs per
+    # 64-key tile against a 0/1 operand) instead of 32 fp32 adds and a
+    # cross-lane reduction per lane; its guard tests those sums.  32-row
+    # fragments only; not with fold_softmax_scale.
+    rowsum_mfma: bool = False
 
 
 @dataclass
@@ -788,7 +799,8 @@ class CDNA4Lowerer:
             guard = 2.0 ** (float(fz["slack"]) * float(fz["c"]))
             return (f"wir::lazy_softmax_fast_b({self._var(fz['s'])}, {self._var(fz['l_in'])}, "
                     f"{self._var(fz['p'])}, {_flt(guard)})")
-        return (f"wir::lazy_softmax_fast({self._var(fz['s'])}, {self._var(fz['m_in'])}, "
+        mr = "_mr" if self.target.rowsum_mfma else ""
+        return (f"wir::lazy_softmax_fast{mr}({self._var(fz['s'])}, {self._var(fz['m_in'])}, "
                 f"{self._var(fz['l_in'])}, {self._var(fz['p'])}, {_flt(fz['c'])}, {_flt(fz['slack'])})")
 
     def _emit_lazy_softmax(self, plan, out: List[str], depth: int) -> None:
@@ -802,6 +814,8 @@ class CDNA4Lowerer:
         # -inf) or has just failed (a loop's exit to its exact path), only the exact half runs
         fn = "lazy_softmax_exact" if self._lazy_exact_only else "lazy_softmax"
         folded = self._fold_live and plan.get("fold")
+        if self.target.rowsum_mfma and not folded and not self._lazy_exact_only:
+            fn += "_mr"
         out.append(f"{pad}wir::{fn}{'_b' if folded else ''}({self._var(plan['s'])}, {self._var(plan['m_in'])}, "
                    f"{self._var(plan['l_in'])}, {self._var(plan['o_in'])}, {self._var(plan['p'])}, "
                    f"{_flt(plan['c'])}, {_flt(plan['slack'])}{', wir_sb' if folded else ''});")
@@ -2300,6 +2314,8 @@ class CDNA4Lowerer:
         src = [
             *([f"{HIPCC_FLAGS_MARKER} -mllvm -amdgpu-mfma-vgpr-form=1"] if self.target.mfma_vgpr_form else []),
             "// Generated by warpir_amd.lowering.CDNA4Lowerer for gfx950 -- do not edit.",
+            *([f'#define WIR_DMA_CPOL " {_dma_cpol(self.target.dma_cache_policy)}"']
+              if self.target.dma_cache_policy else []),
             _header_text(),
             "",
             f"struct {kernel.name}_globals {{",
@@ -2679,6 +2695,14 @@ def _pid_code(dims: int, target: CDNA4Target, reverse_x: bool) -> List[str]:
 
 
 _HEADER_CACHE: Dict[str, str] = {}
+
+
+def _dma_cpol(policy: str) -> str:
+    """The cache-policy modifiers of CDNA4Target.dma_cache_policy, checked."""
+    words = policy.split()
+    if not words or any(w not in ("sc0", "sc1", "nt") for w in words) or len(set(words)) != len(words):
+        raise ValueError(f"dma_cache_policy: expected distinct words from sc0, sc1, nt; got {policy!r}")
+    return " ".join(w for w in ("sc0", "sc1", "nt") if w in words)
 
 
 def _header_text() -> str:
