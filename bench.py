@@ -445,11 +445,12 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
     gemms = [x for x in names if x.startswith("gemm_") and "splitk" not in x]
     sks = [x for x in names if x.startswith("gemm_") and "splitk" in x]
     dqs = [x for x in names if x.startswith("mha_bwd_dq_d128") and not x.endswith(("_causal", "_gqa"))]
+    dkdvs = [x for x in names if x.startswith("mha_bwd_dkdv_d128") and "causal" not in x and "gqa" not in x]
     fas = [x for x in names if x.startswith("mha_d128") and "causal" not in x and "gqa" not in x]
     c5s = [x for x in names if x.startswith("mha_d64_causal") and not x.endswith("_ssa")]
-    untimed = [x for x in names if x not in gemms + sks + dqs + fas + c5s]
+    untimed = [x for x in names if x not in gemms + sks + dqs + dkdvs + fas + c5s]
     if untimed:
-        raise ValueError(f"--compare times GEMM 8192^3, split-K at M=128 N=K=8192, FA forward and dQ at "
+        raise ValueError(f"--compare times GEMM 8192^3, split-K at M=128 N=K=8192, FA forward, dQ and dK/dV at "
                          f"the config-4 shape and causal FA forward at the config-5 shape; not "
                          f"{', '.join(untimed)}")
     stream = torch.cuda.current_stream().cuda_stream
@@ -510,8 +511,8 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
                          "tflops": api.attention_flops(bsz, heads, seq, d, causal=True) / (ms * 1e-3) / 1e12,
                          "shape": [bsz, heads, seq, d], "options": kernels.TARGETS.get(name, {})}
         del q, k, v, o, lse
-    if dqs and not fas:
-        fas = ["mha_d128"]   # the dQ kernels read the forward's O and LSE
+    if (dqs or dkdvs) and not fas:
+        fas = ["mha_d128"]   # the backward kernels read the forward's O and LSE
     if not fas:
         return out
     bsz, heads, seq, d = 16, 16, 4096, 128
@@ -533,7 +534,8 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
     # backward dQ kernel: 3 of the S x S x D products, over the forward's O and LSE
     do = seeded_normal((bsz, heads, seq, d), 3).cuda()
     dvec = torch.empty(bsz, heads, seq, dtype=torch.float32, device="cuda")
-    kernels.handle("mha_bwd_prep_d128")(O=o, dO=do, L=lse, Dv=dvec, L2=torch.empty_like(lse))
+    lse2 = torch.empty_like(lse)
+    kernels.handle("mha_bwd_prep_d128")(O=o, dO=do, L=lse, Dv=dvec, L2=lse2)
     dq = torch.empty_like(q)
     for _ in range(reps):
         for name in dqs:
@@ -548,6 +550,17 @@ def bench_compare(steps: int, warmup: int, names=None, reps: int = 1):
                                                 "Dv": tuple(dvec.shape), "dQ": tuple(dq.shape)})
         out[name] = {"ms": ms, "ms_reps": timed[name], "tflops": 1.5 * flops / (ms * 1e-3) / 1e12,
                      "options": kernels.TARGETS.get(name, {}), "grid": list(lc.grid), "block": lc.block[0]}
+    # backward dK/dV kernel: 4 of the S x S x D products
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    for _ in range(reps):
+        for name in dkdvs:
+            h = kernels.handle(name)
+            timed[name].append(_time_launches(lambda: h(Q=q, K=k, V=v, dO=do, L2=lse2, Dv=dvec, N=seq, dK=dk,  # noqa: B023
+                                                        dV=dv), steps, warmup, stream)[0])
+    for name in dkdvs:
+        ms = statistics.median(timed[name])
+        out[name] = {"ms": ms, "ms_reps": timed[name], "tflops": 2.0 * flops / (ms * 1e-3) / 1e12,
+                     "options": kernels.TARGETS.get(name, {})}
     return out
 
 

@@ -588,12 +588,15 @@ struct MMAPipeAB {
   // half of the tile's MFMAs: bunched DMA issue stalls the issuing wave
   // (measured: 2764 -> 2416 cycles per 256x256x64 step with one DMA every
   // second MFMA), and issuing them later leaves too little time for them to
-  // land before the next barrier.  sched_barrier fences pin the order.
-  template <int NLOAD, class LoadFn>
+  // land before the next barrier.  With WHOLE the loads spread over all the
+  // tile's MFMAs instead: for rings whose later loads have a step more to
+  // land (a deeper ring on the operand issued last), so the CU's address
+  // unit sees half the DMA rate.  sched_barrier fences pin the order.
+  template <int NLOAD, bool WHOLE = false, class LoadFn>
   __device__ __forceinline__ void run(RTile<MS, R, C>& acc, char* a_base, int a_row0, char* b_base, int b_col0,
                                       LoadFn loads) {
     constexpr int PEND = (KS - 1) & 1;
-    constexpr int HALF = (NMMA * KS) / 2;
+    constexpr int HALF = WHOLE ? NMMA * KS : (NMMA * KS) / 2;
     constexpr int EVERY = NLOAD > 0 && HALF / NLOAD > 1 ? HALF / NLOAD : 1;
     int nl = 0;
     __builtin_amdgcn_sched_barrier(0);
@@ -973,6 +976,66 @@ __device__ __forceinline__ void mma_rAB_slots(RTile<MS, R, C>& acc, const BTile<
     __builtin_amdgcn_sched_barrier(0);
     slot(ic<t>{});
     __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Element-wise tile ops restricted to register groups [G0, G1): group q is
+// the 4 C registers 4g..4g+3 of block (cb, rb), numbered (cb, rb, g).  A
+// chain of element-wise ops may run group by group, each MFMA slot of an
+// independent MMA (mma_*_slots) carrying its share, since every element of
+// the chain depends only on the same element of its inputs (and on its row
+// or column value).
+template <int G0, int G1, int MS, int R, int C, class F>
+__device__ __forceinline__ void each_group(F&& f) {
+  constexpr int RB = R / MS, GPB = MF<MS>::CREGS / 4;
+  static_assert(0 <= G0 && G0 <= G1 && G1 <= (C / MS) * RB * GPB, "register group range out of the tile");
+#pragma unroll
+  for (int q = G0; q < G1; ++q) f(q / (RB * GPB), (q / GPB) % RB, q % GPB);
+}
+
+template <int G0, int G1, int MS, int R, int C, class F>
+__device__ __forceinline__ void map_part(RTile<MS, R, C>& out, const RTile<MS, R, C>& in, F fn) {
+  each_group<G0, G1, MS, R, C>([&](int cb, int rb, int g) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out.f[cb][rb][4 * g + j] = fn(in.f[cb][rb][4 * g + j], rb);
+  });
+}
+
+template <int G0, int G1, int MS, int R, int C, class F>
+__device__ __forceinline__ void map2_part(RTile<MS, R, C>& out, const RTile<MS, R, C>& a, const RTile<MS, R, C>& b,
+                                          F fn) {
+  each_group<G0, G1, MS, R, C>([&](int cb, int rb, int g) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out.f[cb][rb][4 * g + j] = fn(a.f[cb][rb][4 * g + j], b.f[cb][rb][4 * g + j]);
+  });
+}
+
+template <int G0, int G1, int MS, int R, int C, class F>
+__device__ __forceinline__ void col_apply_part(RTile<MS, R, C>& out, const RTile<MS, R, C>& t, const CVec<MS, C>& v,
+                                               F fn) {
+  each_group<G0, G1, MS, R, C>([&](int cb, int rb, int g) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out.f[cb][rb][4 * g + j] = fn(t.f[cb][rb][4 * g + j], v.v[cb][4 * g + j]);
+  });
+}
+
+template <int G0, int G1, int MS, int R, int C, class F>
+__device__ __forceinline__ void row_apply_part(RTile<MS, R, C>& out, const RTile<MS, R, C>& t, const RVec<MS, R>& v,
+                                               F fn) {
+  each_group<G0, G1, MS, R, C>([&](int cb, int rb, int g) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out.f[cb][rb][4 * g + j] = fn(t.f[cb][rb][4 * g + j], v.v[rb]);
+  });
+}
+
+template <int G0, int G1, int MS, int R, int C>
+__device__ __forceinline__ void to_bf16_part(BTile<MS, R, C>& out, const RTile<MS, R, C>& in) {
+  each_group<G0, G1, MS, R, C>([&](int cb, int rb, int g) {
+    bf16x4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (bf16)in.f[cb][rb][4 * g + j];
+    out.f[cb][rb][g] = v;
   });
 }
 

@@ -80,6 +80,10 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     "gemm_256x128_ws_k32": lambda: _gemm_mi355x(32, block_n=128, wave_n=64, load_units=12),
     "gemm_256x128_ws_all": lambda: _gemm_mi355x(64, block_n=128, wave_n=64),
     "gemm_256x128": lambda: _gemm_mi355x(64, block_n=128, wave_n=64),
+    # 256x256x64 with rings per operand from kernel_pass (B priced as the long stream: B 3 slots
+    # loaded two steps ahead, A 2 slots, 160 KiB); _sw with B's DMAs in each step's second half
+    "gemm_256_k64_b3": lambda: _gemm_mi355x(64, lds_budget=160 * 1024, hbm_sources=("B",)),
+    "gemm_256_k64_b3sw": lambda: _gemm_mi355x(64, lds_budget=160 * 1024, hbm_sources=("B",)),
     # The reference's single-head attention IR (tests/attention_baseline.py:46-186).
     "attn_ref_ssa": lambda: build_attention_kernel(),
     # Multi-head FlashAttention forward, [B, H, S, D] with LSE: SSA form (loads
@@ -245,6 +249,7 @@ TARGETS: Dict[str, dict] = {
     "gemm_256x128_ws_all": {"warp_specialize": True, "rotate_mma": False, "mve": False,
                             "wave_groups": {"a": 1, "b": 1}},
     "mha_d64_causal_ovl": {"lazy_softmax": False},
+    "gemm_256_k64_b3sw": {"dma_spread_whole": True},
 }
 # the lazy softmax's row sums on the matrix core (CDNA4Target.rowsum_mfma; config 5 within 0.3-0.7%
 # of the default, the config-4 ping-pong 5% slower)
@@ -264,6 +269,10 @@ for _base in ("gemm_256_k64", "mha_d128"):
 for _name in ("mha_bwd_dkdv_d128", "mha_bwd_dkdv_d128_causal", "mha_bwd_dkdv_d128_gqa",
               "mha_bwd_dkdv_d128_causal_gqa"):
     TARGETS[_name] = {"mfma_vgpr_form": True}
+# the D=128 dK/dV kernel with its element-wise chains in the MFMA slots of the MMAs after them
+# (CDNA4Target.slot_fusion: P^T in dP^T's MFMAs, dS^T in dV's)
+VARIANTS["mha_bwd_dkdv_d128_sf"] = VARIANTS["mha_bwd_dkdv_d128"]
+TARGETS["mha_bwd_dkdv_d128_sf"] = {"mfma_vgpr_form": True, "slot_fusion": True}
 
 
 def lowerer(name: str):

@@ -155,6 +155,18 @@ class CDNA4Target:
     # cross-lane reduction per lane; its guard tests those sums.  32-row
     # fragments only; not with fold_softmax_scale.
     rowsum_mfma: bool = False
+    # Rotated MMA pipelines: spread the step's DMAs over all its MFMAs
+    # (MMAPipeAB::run<N, true>) instead of the first half, the first-loaded
+    # operand's in the first half and the other's in the second.  Meant for
+    # rings whose wait leaves the newest batch in flight (a deeper ring on
+    # the operand loaded last), where those loads have a step more to land.
+    dma_spread_whole: bool = False
+    # Element-wise register-tile ops that directly precede an MMA emitted from
+    # register operands (hoisted fragments, or a bf16 register A) and that the
+    # MMA does not depend on run inside that MMA's MFMA stream, one group of
+    # 4 registers per MFMA slot (wir::*_part in mma_*_slots), so a single
+    # wavefront per SIMD issues them under its own MFMAs.
+    slot_fusion: bool = False
 
 
 @dataclass
@@ -362,6 +374,8 @@ class CDNA4Lowerer:
         self._var_override: Dict[str, str] = {}  # resolved value name -> C++ variable
         self._ws = False                          # warp-specialised form (producer / consumer waves)
         self._softmax_fused: Dict[int, object] = {}  # id(op) -> fused lazy-softmax plan, or "skip"
+        self._slot_work: Dict[int, tuple] = {}       # id(MMA) -> (moved ops, register groups, slots form)
+        self._slot_skip: set = set()                 # ids of ops emitted in an MMA's slots
         self._no_fusion = False                      # emit the fused groups' ops one by one
         self._overlapped = False                     # an attention loop took the overlapped ("mixed") form
         self._lazy_exact_only = False                # fused groups emit only the exact half
@@ -826,8 +840,113 @@ class CDNA4Lowerer:
         self._emit_op(op, out, depth)
         self._lazy_exact_only = False
 
+    # element-wise register-tile ops a slot-fused MMA can carry, and the helpers they lower to
+    _SLOT_OPS = (MulScalarOp, Exp2Op, SubOp, MulOp, AddOp, SubRowOp, SubColOp, CopyOp)
+    _SLOT_CALL = re.compile(r"^\s*wir::(map|map2|col_apply|row_apply|to_bf16)\((.*)\);$")
+
+    def _slot_form(self, op: Op) -> Optional[Tuple[str, int]]:
+        """(helper, MFMA slot count) of an MMA that mma_*_slots can emit, or None."""
+        if not isinstance(op, MMAOp) or self.geo.ms != 32:
+            return None
+        ms, res_t = self.geo.ms, op.result.type
+        if op.transpose_b:
+            hoisted = self._hoisted.get(self.resolve(op.a.name))
+            if hoisted is None or (self._fold_live and id(op) in self._score_folds):
+                return None
+            return "mma_ABt_frags_slots", hoisted[1] * (res_t.cols // ms)
+        a_t = op.a.type
+        if (self._is_shared(op.a) or self._lds_key(op.a) is not None or not isinstance(a_t, RegTileType)
+                or a_t.data_type != GPUType.bf16):
+            return None
+        groups = (a_t.cols // ms) * 4   # 4-register groups of a along k
+        return "mma_rAB_slots", (groups // 2) * (res_t.cols // ms)
+
+    def _slot_calls(self, op: Op) -> Optional[List[str]]:
+        """The element-wise op as wir::*_part calls over register groups
+        [WIR_G0, WIR_G1), or None when it is not one this fusion carries."""
+        if not isinstance(op, self._SLOT_OPS) or not isinstance(op.result.type, RegTileType):
+            return None
+        if isinstance(op, CopyOp) and not (isinstance(op.input.type, RegTileType)
+                                           and op.input.type.data_type == GPUType.fp32
+                                           and op.result.type.data_type == GPUType.bf16):
+            return None
+        tmp: List[str] = []
+        skipped = id(op) in self._slot_skip
+        self._slot_skip.discard(id(op))
+        try:
+            self._emit_op(op, tmp, 0)
+        finally:
+            if skipped:
+                self._slot_skip.add(id(op))
+        calls = []
+        for line in tmp:
+            m = self._SLOT_CALL.match(line)
+            if m is None:
+                return None
+            calls.append(f"wir::{m.group(1)}_part<WIR_G0, WIR_G1>({m.group(2)});")
+        return calls
+
+    def _plan_slot_fusion(self, ops: List[Op]) -> None:
+        """CDNA4Target.slot_fusion: each slot-capable MMA takes into its MFMA
+        slots the element-wise ops it does not depend on (transitively) from
+        the contiguous run of element-wise ops and fills right before it, and
+        then those right after it (up to the next other op) whose inputs all
+        exist before it or come from ops it already took.  Ops that stay
+        before the MMA may not read a moved op's result, and every moved op
+        has the same register-tile shape (the group partition)."""
+        def reads(o):
+            return {self.resolve(v.name) for v in _op_values(o) if v is not getattr(o, "result", None)}
+
+        for idx, mma in enumerate(ops):
+            form = self._slot_form(mma)
+            if form is None or id(mma) in self._slot_work:
+                continue
+            run = []
+            j = idx - 1
+            while j >= 0 and (isinstance(ops[j], ZeroOp) or isinstance(ops[j], self._SLOT_OPS)):
+                if id(ops[j]) not in self._slot_skip:   # (ops an earlier MMA took are not in the run)
+                    run.append(ops[j])
+                j -= 1
+            need = reads(mma)
+            moved = []
+            for o in run:   # nearest first
+                if self.resolve(o.result.name) in need or isinstance(o, ZeroOp) or self._slot_calls(o) is None:
+                    need |= reads(o)
+                else:
+                    moved.append(o)
+            changed = True
+            while changed:   # an op that stays must not read a moved result
+                changed = False
+                stay_reads = set().union(*(reads(o) for o in run if o not in moved)) if run else set()
+                for o in list(moved):
+                    if self.resolve(o.result.name) in stay_reads:
+                        moved.remove(o)
+                        changed = True
+            moved.sort(key=ops.index)
+            # ops after the MMA whose inputs exist before it (or come from ops it took)
+            before = {self.resolve(o.result.name) for o in ops[:idx] if isinstance(getattr(o, "result", None), Value)
+                      and o not in moved}
+            later_moved = []
+            k = idx + 1
+            while k < len(ops) and isinstance(ops[k], self._SLOT_OPS):
+                o = ops[k]
+                avail = before | {self.resolve(m.result.name) for m in moved + later_moved}
+                if reads(o) <= avail and self._slot_calls(o) is not None:
+                    later_moved.append(o)
+                k += 1
+            moved += later_moved
+            shapes = {(o.result.type.rows, o.result.type.cols) for o in moved}
+            if not moved or len(shapes) != 1:
+                continue
+            rows, cols = shapes.pop()
+            self._slot_work[id(mma)] = (moved, (rows // 32) * (cols // 32) * 4, form)
+            for o in moved:
+                self._slot_skip.add(id(o))
+
     def _emit_ops(self, ops, out: List[str], depth: int) -> None:
         ops = list(ops)
+        if self.target.slot_fusion:
+            self._plan_slot_fusion(ops)
         for k, op in enumerate(ops):
             if (isinstance(op, WaitBufOp) and k + 1 < len(ops) and isinstance(ops[k + 1], WaitBufOp)
                     and id(op) not in self._pp_ops and id(ops[k + 1]) not in self._pp_ops):
@@ -847,6 +966,8 @@ class CDNA4Lowerer:
             if fused != "skip":
                 self._emit_lazy_softmax(fused, out, depth)
             return
+        if id(op) in self._slot_skip:
+            return   # emitted in the MFMA slots of the MMA after it
         if isinstance(op, (AllocSharedOp, YieldOp, PipelineStageOp)):
             # a pipeline_stage mark is realised by the loop emitters that take
             # its placement; elsewhere the loop runs in program order
@@ -950,7 +1071,8 @@ class CDNA4Lowerer:
                     w(f"{pad}  }});")
                     w(f"{pad}}}")
                 else:
-                    w(f"{pad}{pipe}.run<{total}>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int q) {{")
+                    whole = ", true" if self.target.dma_spread_whole else ""
+                    w(f"{pad}{pipe}.run<{total}{whole}>({acc}, {a_ptr}, wave_row0, {b_ptr}, wave_col0, [&](int q) {{")
                     for c in calls:
                         w(f"{pad}  {c}")
                     w(f"{pad}}});")
@@ -1138,6 +1260,26 @@ class CDNA4Lowerer:
         res_t = op.result.type
         res = self._var(op.result)
         b_ptr, b_key = self._tile_ptr(op.b)
+        if id(op) in self._slot_work:
+            moved, ngroups, (helper, nslots) = self._slot_work[id(op)]
+            calls = [c for o in moved for c in self._slot_calls(o)]
+            if op.transpose_b:
+                frags, ks = self._hoisted[self.resolve(op.a.name)]
+                head = (f"wir::{helper}<{ms}, {res_t.rows}, {res_t.cols}, {self.stile(b_key)}, {ks}>"
+                        f"({res}, {frags}, {b_ptr}, wave_col0, [&](auto wir_t) {{")
+            else:
+                acc = self._var(op.accum)
+                if acc != res:
+                    out.append(f"{pad}{res} = {acc};")
+                a_t = op.a.type
+                head = (f"wir::{helper}<{ms}, {a_t.rows}, {a_t.cols}, {res_t.cols}, {self.stile(b_key)}>"
+                        f"({res}, {self._var(op.a)}, {b_ptr}, wave_col0, [&](auto wir_t) {{")
+            out.append(f"{pad}{head}   // {len(moved)} element-wise ops in the MFMA slots")
+            out.append(f"{pad}  constexpr int WIR_G0 = decltype(wir_t)::value * {ngroups} / {nslots};")
+            out.append(f"{pad}  constexpr int WIR_G1 = (decltype(wir_t)::value + 1) * {ngroups} / {nslots};")
+            out.extend(f"{pad}  {c}" for c in calls)
+            out.append(f"{pad}}});")
+            return
         if op.transpose_b:
             hoisted = self._hoisted.get(self.resolve(op.a.name))
             if hoisted is not None:
