@@ -33,7 +33,7 @@ def test_reference_attention_ir(gpu, n):
 
 @pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_vp4", "mha_d128_vp8", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp_swapped", "mha_d128_w4",
                                      "mha_d128_online", "mha_d128_ovl", "mha_d128_s5", "mha_d128_pp2b",
-                                     "mha_d128_fold", "mha_d128_u2", "mha_d128_mr", "mha_d128_dma_sc1"])
+                                     "mha_d128_fold", "mha_d128_u2", "mha_d128_mr", "mha_d128_dma_sc1", "mha_d128_sb"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 1, 64)])
 def test_mha_d128(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")
@@ -84,7 +84,8 @@ def test_mha_d64_causal(gpu, variant, b, h, s):
                                               ("mha_d128_u2", 128, False),
                                               ("mha_d64_causal", 64, True), ("mha_d128_ovl", 128, False),
                                               ("mha_d64_causal_ovl", 64, True), ("mha_d64_causal_pp", 64, True),
-                                              ("mha_d128_mr", 128, False), ("mha_d64_causal_mr", 64, True)])
+                                              ("mha_d128_mr", 128, False), ("mha_d64_causal_mr", 64, True),
+                                              ("mha_d128_sb", 128, False)])
 def test_mha_lazy_rescale_with_growing_scores(gpu, variant, d, causal):
     """Keys grow along the sequence, so the running max moves by more than
     the slack on later tiles and the rescale path runs too."""
@@ -137,7 +138,7 @@ def test_mha_full_size_sampled(gpu):
 @pytest.mark.parametrize("variant,causal,shape", [
     (None, True, (8, 32, 8192, 64)), (None, False, (16, 16, 4096, 128)), (None, True, (16, 16, 4096, 128)),
     ("mha_d128_online", False, (16, 16, 4096, 128)), ("mha_d128_ovl", False, (16, 16, 4096, 128)),
-    ("mha_d128_u2", False, (16, 16, 4096, 128)),
+    ("mha_d128_u2", False, (16, 16, 4096, 128)), ("mha_d128_sb", False, (16, 16, 4096, 128)),
     ("mha_d64_causal_ovl", True, (8, 32, 8192, 64)), ("mha_d64_causal_pp", True, (8, 32, 8192, 64))])
 def test_mha_repeated_launches_bitwise_stable(gpu, variant, causal, shape):
     """Configs 5 and 4 at full size (default kernels and the ping-pong / overlapped
@@ -370,3 +371,19 @@ def test_dkdv_slot_fusion_bitwise(gpu, b, h, s):
     _, rk, rv = attention_bwd_ref(q.cpu(), k.cpu(), v.cpu(), do.cpu())
     assert rel_err(outs[1][0].cpu().float(), rk) <= TOL
     assert rel_err(outs[1][1].cpu().float(), rv) <= TOL
+
+
+@pytest.mark.parametrize("shape", [(16, 16, 4096, 128), (2, 3, 320, 128), (1, 2, 192, 128)])
+def test_split_barrier_pingpong_equals_default(gpu, shape):
+    """mha_d128_sb moves only group B's barrier (between its PV and QK MMAs), so every wave
+    computes the same operations in the same order as mha_d128: O agrees bit for bit.  The LSE
+    epilogue (c*m + log2(l)) may be contracted into one fma in one build and not the other (HIP
+    contracts by default), so the LSE agrees to a few ulps."""
+    announce(f"mha_d128_sb vs mha_d128 {shape}")
+    q, k, v = (seeded_normal(shape, sd) for sd in (50, 51, 52))
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    o0, l0 = api.attention_forward(qd, kd, vd, variant="mha_d128")
+    o1, l1 = api.attention_forward(qd, kd, vd, variant="mha_d128_sb")
+    torch.cuda.synchronize()
+    assert torch.equal(o0, o1)
+    assert ((l0 - l1).abs() <= 4e-7 * l0.abs() + 1e-7).all(), (l0 - l1).abs().max().item()

@@ -68,6 +68,42 @@ def schedule(S: int, every: int, n: int, dv=None, b_cond_off=None, a_cond_off=No
     return ev
 
 
+def schedule_split(S: int, n: int, dv=None, b_cond_off=None):
+    """The split-barrier form (``CDNA4Target.pingpong_split_barrier``): group B
+    passes its barrier after the rotated PV(i-1) instead of after QK(i), its V
+    tiles are loaded S - 2 ahead like A's K tiles, there is no extra first V
+    load, and B's last barrier follows the last PV."""
+    dist = S - 2
+    dv = dist if dv is None else dv
+    b_cond_off = dv if b_cond_off is None else b_cond_off
+    ev = {"A": [], "B": []}
+    for t in range(dist):
+        ev["A"].append(("load", "k", t))
+        ev["B"].append(("load", "v", t))
+    for g in "AB":
+        ev[g].append(("barrier", 1))
+    for i in range(n):
+        for g in "AB":
+            if i > 0:
+                ev[g].append(("read", "v", i - 1))
+        if i > 0:   # B's latest batch: V tile i - 1 + dv
+            ev["B"].append(("barrier", 1 if (i - 1) + b_cond_off < n else 0))
+        for g in "AB":
+            ev[g].append(("read", "k", i))
+        if i + dist < n:
+            ev["A"].append(("load", "k", i + dist))
+        if i + dv < n:
+            ev["B"].append(("load", "v", i + dv))
+        ev["A"].append(("barrier", 1 if i + dist < n else 0))
+    if n > 0:
+        for g in "AB":
+            ev[g].append(("read", "v", n - 1))
+        ev["B"].append(("barrier", 1 if (n - 1) + b_cond_off < n else 0))
+    for g in "AB":
+        ev[g].append(("barrier", 0))
+    return ev
+
+
 def violations(S: int, ev, n: int):
     out = []
     nb = {g: sum(1 for e in ev[g] if e[0] == "barrier") for g in ev}
@@ -165,3 +201,36 @@ def test_generated_source_matches_the_model():
                     and not ln.lstrip().startswith("if constexpr (!WIR_AL) ")], name
     assert d.count(f"if (wir_grp == 1) wir::wait_vm_barrier_after<4>((v_i) + 2 < {stop});") == 2
     assert d.count(f"if ((v_i) + 3 < {stop})") == 2 and d.count(f"if ((v_i) + 2 < {stop})") == 2
+
+
+@pytest.mark.parametrize("S", [4, 5])
+def test_split_barrier_protocol_is_race_free(S):
+    for n in range(0, 14):
+        assert violations(S, schedule_split(S, n), n) == [], (S, n)
+
+
+def test_split_barrier_planted_mistakes_are_caught():
+    # three slots: a V load overwrites the slot that group A's next PV still reads
+    assert any(violations(3, schedule_split(3, n), n) for n in range(2, 10))
+    # V one tile further ahead (the unsplit form's distance) on a 4-slot ring
+    assert any("WAR" in v for n in range(3, 10) for v in violations(4, schedule_split(4, n, dv=3), n))
+    # B's drain condition one tile short keeps a batch in flight that the next PV reads
+    assert any("RAW" in v for n in range(2, 10) for v in violations(4, schedule_split(4, n, b_cond_off=1), n))
+
+
+def test_split_barrier_source_matches_the_model():
+    """mha_d128_sb: no extra first V load, K and V both two tiles ahead, B's barrier right after
+    the rotated PV (in the loop, and after the last PV) covering V tile i + 1, A's after the
+    softmax covering K tile i + 2, and no barrier for B after the QK MMA."""
+    src = kernels.lowerer("mha_d128_sb").lower(kernels.kernel("mha_d128_sb"))
+    body = src[src.rindex('extern "C" __global__'):]
+    d = body[body.index("const int wir_grp ="):body.index("ring buffers dead")]
+    stop = "((globals.N) + 63) / 64"
+    assert "group B's first V phase" not in d and "wir_t < (0) + 2;" in d
+    b_bar = f"if (wir_grp == 1) wir::wait_vm_barrier_after<4>((v_i) + 1 < {stop});"
+    assert d.count(b_bar) == 2
+    assert d.count(f"if (wir_grp == 0) wir::wait_vm_barrier_after<4>((v_i) + 2 < {stop});") == 3
+    assert d.count(f"if ((v_i) + 2 < {stop})") == 4 and f"(v_i) + 3 < {stop}" not in d
+    # each B barrier directly follows a PV MMA
+    for part in d.split(b_bar)[:-1]:
+        assert part.rstrip().split("\n")[-1].lstrip().startswith("wir::mma_rAB<")

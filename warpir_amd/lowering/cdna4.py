@@ -119,6 +119,14 @@ class CDNA4Target:
     # V tiles S - 2 ahead, and each barrier still leaves the wave's newest
     # batch in flight).  1 keeps a barrier every iteration.
     pingpong_barrier_every: int = 1
+    # With the one-barrier ping-pong (a barrier every iteration): group B
+    # passes its barrier between the rotated PV and the QK MMA instead of
+    # after the QK, so between two barriers A runs PV(i-1), QK(i), softmax(i)
+    # and B runs QK(i), softmax(i), PV(i): the groups sit a third of an
+    # iteration apart instead of half, and at each interval's start both
+    # waves of a SIMD issue MFMAs (one's LDS operand latency under the
+    # other's MFMAs).  B's V tiles are then loaded S - 2 ahead, like A's K.
+    pingpong_split_barrier: bool = False
     # Attention ping-pong: B operands of the next PV MMA (V tile fragments,
     # in mma_rAB's order) each wave reads at the end of its VALU phase, when
     # its LDS reads are otherwise idle, so its MFMA phase reads that many
@@ -1629,6 +1637,9 @@ class CDNA4Lowerer:
         every = self.target.pingpong_barrier_every if one else 1
         if every not in (1, 2):
             raise LoweringError(f"pingpong_barrier_every must be 1 or 2, not {every}")
+        if self.target.pingpong_split_barrier and not (one and every == 1):
+            raise LoweringError("pingpong_split_barrier takes the one-barrier ping-pong with a barrier "
+                                "every iteration")
         plan = self._attention_pingpong_plan(loop)
         if plan is None or plan["S"] < (4 if every == 1 else 5):
             return None
@@ -1701,7 +1712,8 @@ class CDNA4Lowerer:
         # iteration it loads V tile i + S - 1; with one every second iteration
         # tile i + S - 2, so that the slot's previous tile was read in an
         # earlier barrier interval.
-        dv = dist + 1 if every == 1 else dist
+        split = self.target.pingpong_split_barrier
+        dv = dist + 1 if every == 1 and not split else dist
         iv = self._var(loop.induction_var)
         ivn = self.resolve(loop.induction_var.name)
         start = loop.start
@@ -1774,7 +1786,7 @@ class CDNA4Lowerer:
         out.append(f"{q}  }}")
         out.append(f"{q}}}")
         out.append(f"{q}wir::wait_vm_barrier<{per}>();")
-        if every == 1:
+        if every == 1 and not split:
             out.append(f"{q}if (wir_grp == 1) {{   // group B's first V phase: its first ring load only")
             out.extend(dma(v_ld, f"({start}) + {dist}", depth + 2)[0])
             if not one:
@@ -1788,8 +1800,14 @@ class CDNA4Lowerer:
         # wave's latest batch was skipped drains all its loads instead (the
         # batch before is then the newest).  A's batch of V(i) is K tile
         # i + dist, B's batch of V(i) is V tile i + dist + 1.
+        def pv_barrier(d: int) -> None:   # split form: B's barrier after the rotated PV(i-1)
+            if split:   # B's latest batch: from its V(i-1), V tile i - 1 + dv
+                out.append(f"{'  ' * d}if (wir_grp == 1) wir::wait_vm_barrier_after<{per}>(({iv}) + {dv - 1} < {stop});")
+
         def m_barrier(d: int) -> None:   # end of an M phase
             pd = "  " * d
+            if split:
+                return
             if one:   # B's latest batch: from its V(i-1), V tile i - 1 + dv
                 out.append(f"{pd}if (wir_grp == 1{odd}) wir::wait_vm_barrier_after<{per}>(({iv}) + {dv - 1} < {stop});")
             else:
@@ -1822,6 +1840,7 @@ class CDNA4Lowerer:
 
         def m_phase(d: int) -> None:
             emit_pv(out, d)
+            pv_barrier(d)
             out.append(f"{'  ' * d}__builtin_amdgcn_sched_barrier(0);")
             self._emit_op(qk, out, d)
             m_barrier(d)
@@ -1880,6 +1899,7 @@ class CDNA4Lowerer:
         out.append(f"{q2}{{")
         out.append(f"{q2}  const int {iv} = ({stop});")
         emit_pv(out, depth + 3)
+        pv_barrier(depth + 3)
         out.append(f"{q2}}}")
         out.append(f"{q}}}")
         if not one:
@@ -2548,7 +2568,7 @@ class CDNA4Lowerer:
                 tiles = f"(({tiles}) + {op.tile_size - 1}) / {op.tile_size}"
             if pingpong:
                 plan, _swap, _one, every = self._pp_forms[id(op)]
-                npro = plan["S"] - 2 + (1 if every == 1 else 0)
+                npro = plan["S"] - 2 + (1 if every == 1 and not self.target.pingpong_split_barrier else 0)
                 for ld in (plan["k_load"], plan["v_load"]):
                     rows_of[id(ld)] = [f"({tiles})", str(op.start + npro)]
                 continue
