@@ -183,20 +183,23 @@ def test_split_k_kernel_variants_agree(gpu):
     assert rel_err(c128.cpu(), gemm_ref(a.cpu(), b.cpu())) <= TOL
 
 
+@pytest.mark.parametrize("variant", ["gemm_128_splitk_k128_b3", "gemm_128_splitk_k64_b7", "gemm_128_splitk_k64_b7sw",
+                                     "gemm_128_splitk_k32_b14", "gemm_128_splitk_k32_b14sw"])
 @pytest.mark.parametrize("m,n,k,splits", [(128, 8192, 8192, 4), (128, 1024, 512, 4), (128, 1024, 1024, 4),
                                           (96, 384, 384, 2), (128, 256, 8256, 3), (300, 520, 2048, 4)])
-def test_split_k_per_ring_depth_agrees(gpu, m, n, k, splits):
-    """The per-operand ring form (B three slots loaded two tiles ahead, A two slots one tile
-    ahead, kernel_pass with B as the HBM stream) against the uniform two-slot kernel: the same
-    MFMAs in the same k order, so bitwise equal -- also for slices of one or two 128-deep steps,
+def test_split_k_per_ring_depth_agrees(gpu, m, n, k, splits, variant):
+    """The per-operand ring forms (kernel_pass with B as the HBM stream: B three slots loaded two
+    tiles ahead and A two at K=128, B 7 / A 3 at K=64, B 14 / A 6 at K=32, with and without the
+    whole-step DMA spread) against the uniform two-slot kernel: the same MFMAs in the same k order,
+    so bitwise equal -- also for slices of one or two 128-deep steps,
     where the drain consumes prologue slots and its drain_index load reads past the slice."""
     from warpir_amd import api
 
-    announce(f"split-K per-ring depths {m}x{n}x{k} splits={splits}")
+    announce(f"split-K per-ring depths {variant} {m}x{n}x{k} splits={splits}")
     a = seeded_normal((m, k), 92, 0.1).cuda()
     b = seeded_normal((k, n), 93, 0.1).cuda()
     ref = api.gemm_split_k(a, b, splits=splits, variant="gemm_128_splitk_k128")
-    c = api.gemm_split_k(a, b, splits=splits, variant="gemm_128_splitk_k128_b3")
+    c = api.gemm_split_k(a, b, splits=splits, variant=variant)
     torch.cuda.synchronize()
     assert torch.equal(c, ref)
     assert rel_err(c.cpu(), gemm_ref(a.cpu(), b.cpu())) <= TOL

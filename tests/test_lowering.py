@@ -334,7 +334,7 @@ def test_gemm_variant_selection():
     assert api.gemm_variant(2048, 2048) == "gemm_128_k64"      # 64 tiles of 256x256
     assert api.gemm_variant(128, 8192) == "gemm_128x32_k64"          # K unknown: no split
     assert api.gemm_variant(256, 8192) == "gemm_128x64_k64"
-    assert api.gemm_variant(64, 8192, 8192) == api.SPLITK_GEMM_VARIANT == "gemm_128_splitk_k128_b3"
+    assert api.gemm_variant(64, 8192, 8192) == api.SPLITK_GEMM_VARIANT == "gemm_128_splitk_k64_b7"
     assert api.gemm_variant(128, 8192, 8192) == api.SPLITK_GEMM_VARIANT
     assert api.gemm_variant(64, 8192, 100) == "gemm_128x32_k64"   # K too short to split
     for v in ("gemm_256_k64", "gemm_128_k64", "gemm_128x32_k64"):
@@ -525,7 +525,7 @@ def _tile_loads(kernel, tiles, grid):
 
 
 @pytest.mark.parametrize("name", ["gemm_256_k64", "gemm_128x32_k64", "gemm_128_splitk_k128_b3",
-                                  "gemm_128_splitk_s5"])
+                                  "gemm_128_splitk_s5", "gemm_128_splitk_k64_b7", "gemm_256_k64_b3"])
 def test_in_bounds_conditions_cover_every_tile_load(name):
     """Wherever the emitted conditions hold, every tile that the kernel's IR
     loads (prologue, loop, drain steps with their drain indices, per-ring

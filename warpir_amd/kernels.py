@@ -61,6 +61,16 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # rings per operand (B three slots, loaded two tiles ahead; A two slots, one tile ahead)
     "gemm_128_splitk_k128_b3": lambda: _gemm_mi355x(128, block_m=128, block_n=128, wave_m=64, wave_n=64,
                                                     lds_budget=160 * 1024, split_k=True, hbm_sources=("B",)),
+    # shallower K steps, so kernel_pass's per-operand rings go deeper in the same 160 KiB (K=64:
+    # B 7 slots, A 3; K=32: B 14, A 6); _sw spreads each step's DMAs over all its MFMAs
+    "gemm_128_splitk_k64_b7": lambda: _gemm_mi355x(64, block_m=128, block_n=128, wave_m=64, wave_n=64,
+                                                   lds_budget=160 * 1024, split_k=True, hbm_sources=("B",)),
+    "gemm_128_splitk_k64_b7sw": lambda: _gemm_mi355x(64, block_m=128, block_n=128, wave_m=64, wave_n=64,
+                                                     lds_budget=160 * 1024, split_k=True, hbm_sources=("B",)),
+    "gemm_128_splitk_k32_b14": lambda: _gemm_mi355x(32, block_m=128, block_n=128, wave_m=64, wave_n=64,
+                                                    lds_budget=160 * 1024, split_k=True, hbm_sources=("B",)),
+    "gemm_128_splitk_k32_b14sw": lambda: _gemm_mi355x(32, block_m=128, block_n=128, wave_m=64, wave_n=64,
+                                                      lds_budget=160 * 1024, split_k=True, hbm_sources=("B",)),
     # the same rings with the slices summed in the kernel: the last slice to store an output tile
     # adds the fp32 partials in slice order and writes the bf16 tile (reduce_slices)
     "gemm_128_splitk_fused": lambda: _gemm_mi355x(128, block_m=128, block_n=128, wave_m=64, wave_n=64,
@@ -254,6 +264,8 @@ TARGETS: Dict[str, dict] = {
                             "wave_groups": {"a": 1, "b": 1}},
     "mha_d64_causal_ovl": {"lazy_softmax": False},
     "gemm_256_k64_b3sw": {"dma_spread_whole": True},
+    "gemm_128_splitk_k64_b7sw": {"dma_spread_whole": True},
+    "gemm_128_splitk_k32_b14sw": {"dma_spread_whole": True},
 }
 # the lazy softmax's row sums on the matrix core (CDNA4Target.rowsum_mfma; config 5 within 0.3-0.7%
 # of the default, the config-4 ping-pong 5% slower)
