@@ -821,6 +821,8 @@ class CDNA4Lowerer:
             guard = 2.0 ** (float(fz["slack"]) * float(fz["c"]))
             return (f"wir::lazy_softmax_fast_b({self._var(fz['s'])}, {self._var(fz['l_in'])}, "
                     f"{self._var(fz['p'])}, {_flt(guard)})")
+        if self.target.rowsum_mfma and self.geo.ms != 32:
+            raise LoweringError("rowsum_mfma takes the 32x32 MFMA fragment layout")
         mr = "_mr" if self.target.rowsum_mfma else ""
         return (f"wir::lazy_softmax_fast{mr}({self._var(fz['s'])}, {self._var(fz['m_in'])}, "
                 f"{self._var(fz['l_in'])}, {self._var(fz['p'])}, {_flt(fz['c'])}, {_flt(fz['slack'])})")
@@ -837,6 +839,8 @@ class CDNA4Lowerer:
         fn = "lazy_softmax_exact" if self._lazy_exact_only else "lazy_softmax"
         folded = self._fold_live and plan.get("fold")
         if self.target.rowsum_mfma and not folded and not self._lazy_exact_only:
+            if self.geo.ms != 32:
+                raise LoweringError("rowsum_mfma takes the 32x32 MFMA fragment layout")
             fn += "_mr"
         out.append(f"{pad}wir::{fn}{'_b' if folded else ''}({self._var(plan['s'])}, {self._var(plan['m_in'])}, "
                    f"{self._var(plan['l_in'])}, {self._var(plan['o_in'])}, {self._var(plan['p'])}, "
@@ -943,6 +947,9 @@ class CDNA4Lowerer:
                     later_moved.append(o)
                 k += 1
             moved += later_moved
+            # a moved op writes its result while the MMA runs: never into a variable the MMA reads
+            mma_vars = {self._var(v) for v in _op_values(mma) if v is not mma.result}
+            moved = [o for o in moved if self._var(o.result) not in mma_vars]
             shapes = {(o.result.type.rows, o.result.type.cols) for o in moved}
             if not moved or len(shapes) != 1:
                 continue
