@@ -605,3 +605,24 @@ def test_rowsum_selector_sums_a_rows_two_half_lanes():
         want = bvals[lane % 32].sum() + bvals[lane % 32 + 32].sum()
         for i in range(4):
             assert abs(c[4 * (lane // 16) + i, lane % 16] - want) < 1e-12, (lane, i)
+
+
+def test_persistent_programs_launch_and_tile_walk():
+    """CDNA4Target.persistent: the grid is min(tiles, programs) on x, the kernel takes its tile
+    counts from the output tensor, and each program walks tiles blockIdx.x + k * gridDim.x
+    through the same XCD remap as the one-workgroup-per-tile form, a barrier between tiles."""
+    k = kernels.kernel("mha_d128")
+    shapes = {"Q": (16, 16, 4096, 128), "K": (16, 16, 4096, 128), "V": (16, 16, 4096, 128),
+              "O": (16, 16, 4096, 128), "L": (16, 16, 4096)}
+    assert CDNA4Lowerer().launch_config(k, shapes).grid == (16, 16, 16)
+    lw = CDNA4Lowerer(CDNA4Target(persistent=256))
+    assert lw.launch_config(k, shapes).grid == (256, 1, 1)
+    small = {n: (1, 2, 512, 128) for n in "QKVO"}
+    small["L"] = (1, 2, 512)
+    assert lw.launch_config(k, small).grid == (4, 1, 1)
+    src = lw.lower(k)
+    body = src[src.rindex('extern "C" __global__'):]
+    assert "const int nx_ = max(((globals.O.r) + 255) / 256, ((globals.L.r) + 255) / 256), ny_ = max(globals.O.d, globals.L.d)" in body
+    assert "for (int wir_blk = blockIdx.x; wir_blk < wir_nblk; wir_blk += gridDim.x) {" in body
+    assert "const int lid_ = wir::remap_xcd(wir_blk, wir_nblk);" in body
+    assert body.count("wir::barrier();   // the tile's LDS") == 1

@@ -175,6 +175,13 @@ class CDNA4Target:
     # 4 registers per MFMA slot (wir::*_part in mma_*_slots), so a single
     # wavefront per SIMD issues them under its own MFMAs.
     slot_fusion: bool = False
+    # Persistent programs: launch min(tiles, persistent) workgroups, each
+    # walking output tiles blockIdx.x, blockIdx.x + gridDim.x, ... (the tile
+    # extents come from the output tensor, the tile -> program-id map is the
+    # XCD remap of the tile index, so a tile keeps its XCD when the count is a
+    # multiple of 8).  The body runs once per tile, a workgroup barrier
+    # between tiles.  0: one workgroup per tile.
+    persistent: int = 0
 
 
 @dataclass
@@ -277,7 +284,34 @@ class CDNA4Lowerer:
                 if isinstance(c, Value) and c.name in BUILTINS:
                     axis = BUILTINS.index(c.name)
                     grid[axis] = max(grid[axis], _ceil_div(shape[pos], units[pos]))
+        if self.target.persistent:
+            total = grid[0] * grid[1] * grid[2]
+            grid = [max(1, min(total, self.target.persistent)), 1, 1]
         return LaunchConfig(grid=tuple(grid), block=(self.num_threads, 1, 1), dyn_lds=0)
+
+    def _tile_extents(self, kernel: Kernel) -> List[str]:
+        """C++ expressions of the output-tile counts along blockIdx.x, .y, .z,
+        from the stored globals' extents (the persistent form's grid does not
+        carry them)."""
+        fields = ("b", "d", "r", "c")
+        ext: List[List[str]] = [[], [], []]
+        for op in _walk(kernel.body):
+            if not isinstance(op, TMAStoreOp):
+                continue
+            sub = op.dest.type.sub_tile_type
+            units = (1, 1, sub.rows, sub.cols)
+            for pos, c in enumerate(op.coords):
+                if isinstance(c, Value) and c.name in BUILTINS:
+                    e = f"globals.{_cname(op.dest.name)[2:]}.{fields[pos]}"
+                    ext[BUILTINS.index(c.name)].append(e if units[pos] == 1 else
+                                                       f"(({e}) + {units[pos] - 1}) / {units[pos]}")
+        out = []
+        for es in ext:
+            expr = "1"
+            for e in es:
+                expr = e if expr == "1" else f"max({expr}, {e})"
+            out.append(expr)
+        return out
 
     @property
     def num_threads(self) -> int:
@@ -2479,7 +2513,18 @@ class CDNA4Lowerer:
             wpe = 2 if self._overlapped else max(2, min(wpe, by_lds))
         self.waves_per_simd = wpe
         nt = self.num_threads
-        pid = _pid_code(dims, self.target, reverse_x=causal_x)
+        if self.target.persistent:
+            if self._ws:
+                raise LoweringError("persistent programs do not take the warp-specialised form")
+            pid = _persistent_pid_code(self._tile_extents(kernel))
+            body = ["  for (int wir_blk = blockIdx.x; wir_blk < wir_nblk; wir_blk += gridDim.x) {",
+                    "  wir_drain = 0;",
+                    *_persistent_tile_ids(dims, self.target, reverse_x=causal_x),
+                    *body,
+                    "  wir::barrier();   // the tile's LDS (ring, staging) is free before the next tile's loads",
+                    "  }"]
+        else:
+            pid = _pid_code(dims, self.target, reverse_x=causal_x)
         src = [
             *([f"{HIPCC_FLAGS_MARKER} -mllvm -amdgpu-mfma-vgpr-form=1"] if self.target.mfma_vgpr_form else []),
             "// Generated by warpir_amd.lowering.CDNA4Lowerer for gfx950 -- do not edit.",
@@ -2860,6 +2905,30 @@ def _pid_code(dims: int, target: CDNA4Target, reverse_x: bool) -> List[str]:
     if reverse_x:
         lines.append("  pid_x = nx_ - 1 - pid_x;  // longest causal rows first")
     lines.append("  (void)pid_x; (void)pid_y; (void)pid_z;")
+    return lines
+
+
+def _persistent_pid_code(extents: List[str]) -> List[str]:
+    """Program-independent part of the persistent form: tile counts per axis
+    from the output tensor, and the mutable tile ids."""
+    return [
+        f"  const int nx_ = {extents[0]}, ny_ = {extents[1]}, nz_ = {extents[2]};",
+        "  const int wir_nblk = nx_ * ny_ * nz_;   // output tiles; this program takes every gridDim.x-th",
+        "  int pid_x = 0, pid_y = 0, pid_z = 0;",
+        "  (void)pid_x; (void)pid_y; (void)pid_z;",
+    ]
+
+
+def _persistent_tile_ids(dims: int, target: CDNA4Target, reverse_x: bool) -> List[str]:
+    """Tile ids of tile wir_blk: the mapping _pid_code gives dispatch index wir_blk."""
+    lines = [f"  {{ const int lid_ = {'wir::remap_xcd(wir_blk, wir_nblk)' if target.xcd_remap else 'wir_blk'};"]
+    if dims == 2:
+        lines.append(f"    wir::grouped_tile<{target.group_m}>(lid_, nx_, ny_, pid_x, pid_y);")
+    else:
+        lines.append("    pid_x = lid_ % nx_; pid_y = (lid_ / nx_) % ny_; pid_z = lid_ / (nx_ * ny_);")
+    if reverse_x:
+        lines.append("    pid_x = nx_ - 1 - pid_x;")
+    lines.append("  }")
     return lines
 
 
