@@ -38,6 +38,22 @@ PEAK_HBM_GBS = 8000.0
 METRIC = "bf16 TFLOP/s + % MFMA peak: GEMM 8192³ and FA-fwd B16 H16 S4096 D128"
 
 
+PREWARM_S = 0.5   # --prewarm: seconds of untimed launches before the warm-up steps
+
+
+def _prewarm(launch, seconds: float) -> None:
+    """Run ``launch`` in batches of 8 (synchronising after each) for about
+    ``seconds`` of wall time: the GPU leaves its idle clocks over the first
+    ~100 ms of sustained load, longer than a few warm-up launches take."""
+    import torch
+
+    end = time.perf_counter() + seconds
+    while time.perf_counter() < end:
+        for _ in range(8):
+            launch()
+        torch.cuda.synchronize()
+
+
 def _time_launches(launch, steps: int, warmup: int, stream, per_launch: bool = False):
     """Mean ms per launch over ``steps`` back-to-back launches (one event pair
     around all of them) and the wall-clock mean; with ``per_launch``, also the
@@ -109,6 +125,7 @@ def bench_gemm(steps, warmup, cpu: bool, median: bool = False):
     def launch():
         h(A=a, B=b, N=k, C_global=c)
 
+    _prewarm(launch, PREWARM_S)
     mean, wall_ms, med = _time_launches(launch, steps, warmup, stream, per_launch=True)
     ms = med if median else mean
     flops = 2.0 * m * n * k
@@ -163,6 +180,7 @@ def bench_fa(steps, warmup, cpu: bool, median: bool = False):
     def launch():
         h(Q=q, K=k, V=v, N=seq, O=o, L=lse)
 
+    _prewarm(launch, PREWARM_S)
     mean, wall_ms, med = _time_launches(launch, steps, warmup, stream, per_launch=True)
     ms = med if median else mean
     flops = api.attention_flops(bsz, heads, seq, d)
@@ -568,6 +586,7 @@ ONLY = ["gemm", "fa", "ceiling"] + list(EXTRA) + ["none"]   # none: only --compa
 
 
 def main() -> int:
+    global PREWARM_S
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -579,6 +598,9 @@ def main() -> int:
                     help="headline value from the median of per-launch event pairs (the reference's method) "
                          "instead of the mean over back-to-back launches")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
+    ap.add_argument("--prewarm", type=float, default=PREWARM_S, metavar="SECONDS",
+                    help="untimed launches of the GEMM and FA headline kernels for this long before their "
+                         "warm-up steps (the GPU's clocks settle over ~100 ms of load); 0 to skip")
     ap.add_argument("--compare", nargs="?", const="default", default=None, metavar="VARIANTS",
                     help="also time schedule alternatives at the headline shapes: COMPARE_GEMM, COMPARE_FA and "
                          "COMPARE_BWD_DQ, or the comma-separated kernels.VARIANTS names given")
@@ -588,6 +610,7 @@ def main() -> int:
                     help="also run a plain device copy of MIB MiB (read MIB, write MIB) three times, "
                          "the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    PREWARM_S = max(0.0, args.prewarm)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "GEMM shards by output rows and attention by (batch, head), with no communication",
@@ -645,7 +668,8 @@ def main() -> int:
         return 0
     line = {
         "metric": METRIC, "value": head["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
+        "warmup": args.warmup, "prewarm_s": PREWARM_S, "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1), GEMM x0.1)",
         "config": head["config"], "roofline": head["roofline"],
         "timing": ("median of per-launch HIP event pairs" if args.median else
