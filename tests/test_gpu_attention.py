@@ -34,7 +34,7 @@ def test_reference_attention_ir(gpu, n):
 @pytest.mark.parametrize("variant", ["mha_d128", "mha_d128_vp4", "mha_d128_vp8", "mha_d128_ssa", "mha_d128_q256", "mha_d128_pp_swapped", "mha_d128_w4",
                                      "mha_d128_online", "mha_d128_ovl", "mha_d128_s5", "mha_d128_pp2b",
                                      "mha_d128_fold", "mha_d128_u2", "mha_d128_mr", "mha_d128_dma_sc1", "mha_d128_sb",
-                                     "mha_d128_pers"])
+                                     "mha_d128_pers", "mha_d128_stream"])
 @pytest.mark.parametrize("b,h,s", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 1, 64)])
 def test_mha_d128(gpu, variant, b, h, s):
     announce(f"{variant} B={b} H={h} S={s}")
@@ -86,7 +86,7 @@ def test_mha_d64_causal(gpu, variant, b, h, s):
                                               ("mha_d64_causal", 64, True), ("mha_d128_ovl", 128, False),
                                               ("mha_d64_causal_ovl", 64, True), ("mha_d64_causal_pp", 64, True),
                                               ("mha_d128_mr", 128, False), ("mha_d64_causal_mr", 64, True),
-                                              ("mha_d128_sb", 128, False)])
+                                              ("mha_d128_sb", 128, False), ("mha_d128_stream", 128, False)])
 def test_mha_lazy_rescale_with_growing_scores(gpu, variant, d, causal):
     """Keys grow along the sequence, so the running max moves by more than
     the slack on later tiles and the rescale path runs too."""
@@ -140,7 +140,7 @@ def test_mha_full_size_sampled(gpu):
     (None, True, (8, 32, 8192, 64)), (None, False, (16, 16, 4096, 128)), (None, True, (16, 16, 4096, 128)),
     ("mha_d128_online", False, (16, 16, 4096, 128)), ("mha_d128_ovl", False, (16, 16, 4096, 128)),
     ("mha_d128_u2", False, (16, 16, 4096, 128)), ("mha_d128_sb", False, (16, 16, 4096, 128)),
-    ("mha_d128_pers", False, (16, 16, 4096, 128)),
+    ("mha_d128_pers", False, (16, 16, 4096, 128)), ("mha_d128_stream", False, (16, 16, 4096, 128)),
     ("mha_d64_causal_ovl", True, (8, 32, 8192, 64)), ("mha_d64_causal_pp", True, (8, 32, 8192, 64))])
 def test_mha_repeated_launches_bitwise_stable(gpu, variant, causal, shape):
     """Configs 5 and 4 at full size (default kernels and the ping-pong / overlapped
@@ -380,7 +380,7 @@ def test_dkdv_slot_fusion_bitwise(gpu, b, h, s):
 
 
 @pytest.mark.parametrize("shape", [(16, 16, 4096, 128), (2, 3, 320, 128), (1, 2, 192, 128), (3, 5, 2048, 128)])
-@pytest.mark.parametrize("variant", ["mha_d128_sb", "mha_d128_pers"])
+@pytest.mark.parametrize("variant", ["mha_d128_sb", "mha_d128_pers", "mha_d128_stream"])
 def test_pingpong_forms_equal_default(gpu, shape, variant):
     """mha_d128_sb moves only group B's barrier (between its PV and QK MMAs), and mha_d128_pers
     runs the same body per tile in persistent programs (256 workgroups, tiles blockIdx.x +

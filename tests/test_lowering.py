@@ -626,3 +626,21 @@ def test_persistent_programs_launch_and_tile_walk():
     assert "for (int wir_blk = blockIdx.x; wir_blk < wir_nblk; wir_blk += gridDim.x) {" in body
     assert "const int lid_ = wir::remap_xcd(wir_blk, wir_nblk);" in body
     assert body.count("wir::barrier();   // the tile's LDS") == 1
+
+
+def test_persistent_stream_form():
+    """CDNA4Target.persistent_stream on the config-4 kernel: the aligned body is one ring stream
+    (loop end wir_T, loads through each wave's cursor, the tile's first key tile peeled, O stored
+    from registers after the tile's last PV), the unaligned body walks tiles one by one; without
+    persistent programs the option is refused."""
+    k = kernels.kernel("mha_d128")
+    src = CDNA4Lowerer(CDNA4Target(persistent=256, persistent_stream=True)).lower(k)
+    body = src[src.rindex('extern "C" __global__'):]
+    al = body[body.index("if constexpr (WIR_AL) {"):body.index("} else {\n  for (int wir_blk")]
+    assert "const int wir_T = wir_cnt * wir_nt;" in al and "wir_adv();" in al
+    assert "store_tile_staged" not in al and al.count("wir::store_tile(globals.O") == 1
+    assert "wir::wait_vm_barrier_after<4>((v_i) + 2 < wir_T);" in al
+    assert "for (; v_i < wir_nb; ++v_i)" in al and "if (v_i == wir_T) break;" in al
+    assert "for (int wir_blk = blockIdx.x; wir_blk < wir_nblk; wir_blk += gridDim.x) {" in body
+    with pytest.raises(LoweringError):
+        CDNA4Lowerer(CDNA4Target(persistent_stream=True)).lower(k)

@@ -122,6 +122,9 @@ VARIANTS: Dict[str, Callable[[], Kernel]] = {
     # persistent programs: 256 workgroups walking the (query block, head) tiles
     "mha_d128_pers": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
                                   rescale_slack=LAZY_SLACK),
+    # the same with one K/V ring stream across each program's tiles (persistent_stream)
+    "mha_d128_stream": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
+                                    rescale_slack=LAZY_SLACK),
     # the same with group B's barrier between its PV and QK (groups a third of an iteration apart)
     "mha_d128_sb": lambda: _mha(128, 256, 64, 32, causal=False, lds_budget=128 * 1024, min_stages=4,
                                 rescale_slack=LAZY_SLACK),
@@ -246,6 +249,7 @@ TARGETS: Dict[str, dict] = {
     "mha_d128_u2": {"pingpong_barrier_every": 2},
     "mha_d128_sb": {"pingpong_split_barrier": True},
     "mha_d128_pers": {"persistent": 256},
+    "mha_d128_stream": {"persistent": 256, "persistent_stream": True},
     "mha_d128_vp4": {"pingpong_v_prefetch": 4},
     "mha_d128_vp8": {"pingpong_v_prefetch": 8},
     "mha_d128_fold": {"fold_softmax_scale": True},

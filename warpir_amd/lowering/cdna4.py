@@ -182,6 +182,13 @@ class CDNA4Target:
     # multiple of 8).  The body runs once per tile, a workgroup barrier
     # between tiles.  0: one workgroup per tile.
     persistent: int = 0
+    # With persistent programs and the attention ping-pong (a barrier every
+    # iteration): one K/V ring stream across the tiles a program walks, so the
+    # next tile's first K/V tiles load under the current tile's last steps and
+    # the ping-pong never drains between tiles.  At a tile boundary, after the
+    # rotated PV, each wave stores its rows of O and the LSE from registers,
+    # then loads the next tile's Q and resets its running state.
+    persistent_stream: bool = False
 
 
 @dataclass
@@ -247,9 +254,39 @@ class CDNA4Lowerer:
             if self.target.fold_softmax_scale:
                 self._plan_score_folds(kernel)
         self._plan_pingpong_loops(kernel)
+        if self.target.persistent_stream:
+            self._stream = self._stream_plan(kernel)
         body: List[str] = []
         self._emit_ops(kernel.body, body, 1)
+        if self._stream is not None:
+            self._stream_lines = self._emit_attention_stream(*self._stream)
         return self._assemble(kernel, body)
+
+    def _stream_plan(self, kernel: Kernel):
+        """(loop, ops before it, ops after it) when the kernel takes the
+        persistent stream form: persistent programs, one top-level loop in the
+        one-barrier ping-pong form with a barrier every iteration (no split
+        barrier, V prefetch or folded scale), whose K and V loads address
+        (batch, head) = (pid_z, pid_y) at key tile = the loop index, column 0."""
+        if not self.target.persistent:
+            raise LoweringError("persistent_stream takes persistent programs")
+        loops = [o for o in kernel.body if isinstance(o, ForOp)]
+        if len(loops) != 1 or id(loops[0]) not in self._pp_forms:
+            return None
+        loop = loops[0]
+        plan, _swap, one, every = self._pp_forms[id(loop)]
+        t = self.target
+        if (not one or every != 1 or t.pingpong_split_barrier or t.pingpong_v_prefetch or t.fold_softmax_scale
+                or not isinstance(loop.start, int) or loop.step != 1):
+            return None
+        aff = self.resolve(plan["affine"].result.name)
+        for ld in (plan["k_load"], plan["v_load"]):
+            b, d, rt, ct = ld.coords
+            if not (isinstance(b, Value) and b.name == "blockIdx.z" and isinstance(d, Value) and d.name == "blockIdx.y"
+                    and isinstance(rt, Value) and self.resolve(rt.name) == aff and ct == 0):
+                return None
+        idx = kernel.body.index(loop)
+        return loop, list(kernel.body[:idx]), list(kernel.body[idx + 1:])
 
     def _plan_pingpong_loops(self, kernel: Kernel) -> None:
         """Record the top-level loops that take the attention ping-pong form,
@@ -425,6 +462,8 @@ class CDNA4Lowerer:
         self._fold_live = False                      # inside a fused loop whose ScoreBias is declared
         self._pp_forms: Dict[int, tuple] = {}        # id(top-level loop) -> its attention ping-pong form
         self._pp_prologue: set = set()               # ids of prologue loads the ping-pong issues itself
+        self._stream = None                          # persistent_stream: (loop, pre ops, post ops)
+        self._stream_lines: List[str] = []
 
     def _build_aliases(self, ops) -> None:
         """iter_arg init / loop results / yielded values -> block arg (``lowering.py:87-100``)."""
@@ -1811,6 +1850,9 @@ class CDNA4Lowerer:
         self._no_fusion = True
         self._emit_loop(loop, stop, out, depth + 1, mve=False)
         self._no_fusion = False
+        if self._stream is not None and self._stream[0] is loop:
+            out.append(f"{pad}}}   // (aligned tensors: the persistent stream form)")
+            return True
         out.append(f"{pad}}} else {{")
         out.append(f"{q}const int wir_grp = (wir_wave >> 2) ^ {swap}, wir_gw = wir_wave & 3;"
                    f"  // group A (K loads) = physical wave group {swap}")
@@ -1948,6 +1990,194 @@ class CDNA4Lowerer:
         out.append(f"{pad}}}")
         self._fold_live = was_live
         return True
+
+    def _emit_attention_stream(self, loop: ForOp, pre_ops: List[Op], post_ops: List[Op]) -> List[str]:
+        """The aligned body of the persistent stream form
+        (``CDNA4Target.persistent_stream``): the one-barrier ping-pong of
+        ``_emit_attention_pingpong`` over stream index ``u`` in ``[0, T)``,
+        ``T`` = this program's tiles x key tiles per tile, where ``u`` is key
+        tile ``u % nt`` of the program's tile ``u / nt``.  Ring slot, load
+        distances and barrier conditions are the ping-pong's with the loop
+        index replaced by ``u`` and the loop end by ``T`` (so the barrier
+        protocol is the one its CPU model checks for a loop of ``T`` tiles);
+        K and V tile ``w`` read (batch, head) of tile ``w / nt``.  After the
+        rotated PV of the last key tile of a tile, each wave finishes that
+        tile (O normalised in place and stored from registers, the LSE
+        stored), switches the tile ids, loads the next tile's Q and resets
+        its running max, sum and O; the lazy softmax of the tile's first key
+        tile then takes its exact half (the max is -inf)."""
+        plan, swap, _one, _every = self._pp_forms[id(loop)]
+        S, qk, pv = plan["S"], plan["qk"], plan["pv"]
+        dist = S - 2
+        dv = dist + 1
+        iv = self._var(loop.induction_var)
+        ivn = self.resolve(loop.induction_var.name)
+        stop = self._int(loop.stop)
+        if loop.tile_size:
+            stop = f"(({stop}) + {loop.tile_size - 1}) / {loop.tile_size}"
+        out: List[str] = []
+        w = out.append
+        q = "    "
+
+        def per(ld) -> int:
+            t = ld.buf.type.tile_type
+            return t.rows * t.cols * 2 // 1024 // 4
+        k_ld, v_ld = plan["k_load"], plan["v_load"]
+        npl = per(k_ld)
+
+        def dma(ld, tile: str, d: int) -> List[str]:
+            key = self.resolve(ld.buf.name)
+            stride = _tile_bytes(self.tile_type_of(key))
+            sub = ld.source.type.sub_tile_type
+            self._aligned_checks.add((self.stile(key), _cname(ld.source.name)[2:]))
+            pd = "  " * d
+            # each wave loads stream tiles in increasing order, so a cursor (tile, key tile, batch,
+            # head of the next tile it loads) replaces dividing the stream index
+            return [f"{pd}{{ const int wir_w = {tile};",
+                    f"{pd}  wir::Loader<{self.stile(key)}, 4>::load<WIR_AL, WIR_INB>((smem + {self.lds_off[key]} + "
+                    f"((wir_w) % {S}) * {stride}), globals.{_cname(ld.source.name)[2:]}, wir_cz, wir_cy, "
+                    f"(wir_ckt) * {sub.rows}, 0, wir_gw);",
+                    f"{pd}  wir_adv(); }}"]
+
+        # the tile's first and last ops: Q load and resets, and the finish (direct stores)
+        pre: List[str] = []
+        self._emit_ops([o for o in pre_ops if not isinstance(o, TMALoadBufOp)], pre, 0)
+        decls = [ln for ln in pre if ln.lstrip().startswith("wir::RowFrags<")]
+        acts = [ln for ln in pre if ln not in decls and not ln.lstrip().startswith("if constexpr (!WIR_AL)")]
+        staged, over = dict(self._staged), dict(self._var_override)
+        for o in post_ops:
+            if isinstance(o, TMAStoreOp):
+                self._staged.pop(id(o), None)
+            if isinstance(o, DivRowOp):
+                self._var_override[self.resolve(o.result.name)] = self._var(o.tile)   # in place
+        fin: List[str] = []
+        self._emit_ops(post_ops, fin, 0)
+        self._staged, self._var_override = staged, over
+        if any("store_tile_staged" in ln or "wait_vm_barrier" in ln for ln in fin):
+            raise LoweringError("persistent_stream: the tile's finish must store from registers")
+
+        def emit(lines: List[str], d: int) -> None:
+            pd = "  " * d
+            out.extend(pd + ln.strip() if ln.strip() else ln for ln in lines)
+
+        w(f"{q}const int wir_G = gridDim.x;")
+        w(f"{q}const int wir_cnt = (int)blockIdx.x < wir_nblk ? (wir_nblk - 1 - (int)blockIdx.x) / wir_G + 1 : 0;")
+        w(f"{q}const int wir_nt = {stop};   // key tiles per output tile")
+        w(f"{q}const int wir_T = wir_cnt * wir_nt;   // this program's stream of key tiles")
+        w(f"{q}const int wir_grp = (wir_wave >> 2) ^ {swap}, wir_gw = wir_wave & 3;")
+        w(f"{q}auto wir_tile = [&](int sb) {{   // tile ids of this program's sb-th tile")
+        w(f"{q}  const int lid_ = wir::remap_xcd((int)blockIdx.x + sb * wir_G, wir_nblk);")
+        w(f"{q}  pid_x = lid_ % nx_; pid_y = (lid_ / nx_) % ny_; pid_z = lid_ / (nx_ * ny_);")
+        w(f"{q}}};")
+        w(f"{q}int wir_csb = 0, wir_ckt = 0, wir_cz = 0, wir_cy = 0;   // this wave's load cursor")
+        w(f"{q}auto wir_cur = [&]() {{")
+        w(f"{q}  const int lid_ = wir::remap_xcd((int)blockIdx.x + wir_csb * wir_G, wir_nblk);")
+        w(f"{q}  wir_cy = (lid_ / nx_) % ny_; wir_cz = lid_ / (nx_ * ny_);")
+        w(f"{q}}};")
+        w(f"{q}auto wir_adv = [&]() {{")
+        w(f"{q}  if (++wir_ckt == wir_nt) {{ wir_ckt = 0; ++wir_csb; wir_cur(); }}")
+        w(f"{q}}};")
+        w(f"{q}int wir_sb = 0, wir_nb = wir_nt;   // the tile being computed; stream index of the next one")
+        emit(decls, 2)
+        w(f"{q}if (wir_cnt > 0) {{")
+        q2 = q + "  "
+        w(f"{q2}wir_tile(0);")
+        w(f"{q2}wir_cur();")
+        emit(acts, 3)
+        w(f"{q2}for (int wir_t = 0; wir_t < {dist}; ++wir_t) {{")
+        w(f"{q2}  if (wir_t < wir_T) {{")
+        w(f"{q2}    if (wir_grp == 0) {{")
+        out.extend(dma(k_ld, "wir_t", 6))
+        w(f"{q2}    }} else {{")
+        out.extend(dma(v_ld, "wir_t", 6))
+        w(f"{q2}    }}")
+        w(f"{q2}  }}")
+        w(f"{q2}}}")
+        w(f"{q2}wir::wait_vm_barrier_after<{npl}>({dist - 1} < wir_T);")
+        w(f"{q2}if (wir_grp == 1 && {dist} < wir_T) {{   // group B's first V phase: its first ring load only")
+        out.extend(dma(v_ld, str(dist), 4))
+        w(f"{q2}}}")
+
+        def m_barrier(d: int) -> None:   # B's latest batch: V tile u - 1 + dv
+            out.append(f"{'  ' * d}if (wir_grp == 1) wir::wait_vm_barrier_after<{npl}>(({iv}) + {dv - 1} < wir_T);")
+
+        def v_barrier(d: int) -> None:   # A's latest batch: K tile u + dist
+            out.append(f"{'  ' * d}if (wir_grp == 0) wir::wait_vm_barrier_after<{npl}>(({iv}) + {dist} < wir_T);")
+
+        def v_loads(d: int) -> None:
+            qq = "  " * d
+            out.append(f"{qq}if (wir_grp == 0) {{")
+            out.append(f"{qq}  if (({iv}) + {dist} < wir_T)")
+            out.extend(dma(k_ld, f"({iv}) + {dist}", d + 2))
+            out.append(f"{qq}}} else {{")
+            out.append(f"{qq}  if (({iv}) + {dv} < wir_T)")
+            out.extend(dma(v_ld, f"({iv}) + {dv}", d + 2))
+            out.append(f"{qq}}}")
+
+        def emit_pv(d: int) -> None:
+            self._slot_shift[ivn] = -1
+            self._emit_op(pv, out, d)
+            del self._slot_shift[ivn]
+
+        def v_tail(ops, d: int) -> None:
+            self._emit_ops(ops, out, d)
+            self._emit_op(plan["yld"], out, d)
+            v_barrier(d)
+
+        softmax = plan["softmax"]
+        fused_at = next((k for k, o in enumerate(softmax) if isinstance(self._softmax_fused.get(id(o)), dict)), None)
+        if fused_at is None:
+            raise LoweringError("persistent_stream takes the lazy-softmax ping-pong")
+        fz = self._softmax_fused[id(softmax[fused_at])]
+        pre_sm, post_sm = softmax[:fused_at], softmax[fused_at + 1:]
+        # One pass of the outer loop per output tile.  The tile's first key tile is peeled: its QK
+        # is the only use of the tile's freshly loaded Q fragments that the compiler must wait
+        # for (the inner loop is entered only through it, so no vmcnt(0) lands in the inner loop,
+        # where it would also wait for the ring DMAs in flight), and its softmax takes the exact
+        # half (the running max is -inf).  The tile's last PV ends the pass, then its finish.
+        q3, q4 = q2 + "  ", q2 + "    "
+        w(f"{q2}int {iv} = 0;")
+        w(f"{q2}for (;;) {{")
+        w(f"{q3}{{")
+        self._emit_op(qk, out, 7)
+        m_barrier(7)
+        v_loads(7)
+        self._lazy_exact_only = True
+        v_tail(softmax, 7)
+        self._lazy_exact_only = False
+        w(f"{q3}}}")
+        w(f"{q3}++{iv};")
+        w(f"{q3}for (;;) {{")
+        w(f"{q4}bool wir_exact = false;")
+        w(f"{q4}for (; {iv} < wir_nb; ++{iv}) {{")
+        emit_pv(8)
+        w(f"{q4}  __builtin_amdgcn_sched_barrier(0);")
+        self._emit_op(qk, out, 8)
+        m_barrier(8)
+        v_loads(8)
+        self._emit_ops(pre_sm, out, 8)
+        w(f"{q4}  if (!{self._fast_call(fz)}) {{")
+        w(f"{q4}    wir_exact = true;")
+        w(f"{q4}    break;")
+        w(f"{q4}  }}")
+        for src, dst in (("m_in", "m_out"), ("l_in", "l_out"), ("o_in", "o_out")):
+            self._var_override[self.resolve(fz[dst].name)] = self._var(fz[src])
+        v_tail(post_sm, 8)
+        w(f"{q4}}}")
+        w(f"{q4}if (!wir_exact) break;")
+        self._emit_exact(softmax[fused_at], out, 7)
+        v_tail(post_sm, 7)
+        w(f"{q4}++{iv};")
+        w(f"{q3}}}")
+        emit_pv(6)   # the tile's last PV ({iv} == wir_nb)
+        emit(fin, 6)
+        w(f"{q3}if ({iv} == wir_T) break;")
+        w(f"{q3}wir_nb += wir_nt;")
+        w(f"{q3}wir_tile(++wir_sb);")
+        emit(acts, 6)
+        w(f"{q2}}}")
+        w(f"{q}}}")
+        return out
 
     def _attention_overlap_plan(self, loop: ForOp):
         """Match the prefetch-form attention loop for the overlapped emitter:
@@ -2523,6 +2753,10 @@ class CDNA4Lowerer:
                     *body,
                     "  wir::barrier();   // the tile's LDS (ring, staging) is free before the next tile's loads",
                     "  }"]
+            if self._stream is not None:
+                if causal_x or dims != 3:
+                    raise LoweringError("persistent_stream takes the non-causal attention forward")
+                body = ["  if constexpr (WIR_AL) {", *self._stream_lines, "  } else {", *body, "  }"]
         else:
             pid = _pid_code(dims, self.target, reverse_x=causal_x)
         src = [
