@@ -13,6 +13,33 @@
 typedef float wr_f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 wr_bf16x8 __attribute__((ext_vector_type(8)));
 
+// lo/hi += the 8 floats of each of `count` partials at p, p + stride, ...
+// in that order.  The loads of up to four partials are issued before their
+// adds (the adds stay in partial order, so the sums are those of the
+// one-at-a-time loop), so a thread waits for one memory round trip per four
+// partials instead of one per partial.
+__device__ __forceinline__ void wr_accumulate(wr_f32x4& lo, wr_f32x4& hi, const float* p, long long stride,
+                                              int count) {
+  int s = 0;
+  for (; s + 4 <= count; s += 4) {
+    wr_f32x4 a[4], b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[j] = *(const wr_f32x4*)(p + (s + j) * stride);
+      b[j] = *(const wr_f32x4*)(p + (s + j) * stride + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lo += a[j];
+      hi += b[j];
+    }
+  }
+  for (; s < count; ++s) {
+    lo += *(const wr_f32x4*)(p + s * stride);
+    hi += *(const wr_f32x4*)(p + s * stride + 4);
+  }
+}
+
 struct wr_args {
   const float* partials;   // [splits][n]
   __bf16* out;             // [n]
@@ -25,11 +52,7 @@ extern "C" __global__ void __launch_bounds__(256) wir_splitk_reduce(const wr_arg
   const long long e = ((long long)blockIdx.x * 256 + threadIdx.x) * 8;
   if (e >= args.n) return;
   wr_f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < args.splits; ++s) {
-    const float* p = args.partials + s * args.split_stride + e;
-    lo += *(const wr_f32x4*)p;
-    hi += *(const wr_f32x4*)(p + 4);
-  }
+  wr_accumulate(lo, hi, args.partials + e, args.split_stride, args.splits);
   wr_bf16x8 v;
   for (int j = 0; j < 4; ++j) {
     v[j] = (__bf16)lo[j];
@@ -58,12 +81,7 @@ extern "C" __global__ void __launch_bounds__(256) wir_group_reduce(const wg_args
   if (e >= args.n * args.groups) return;
   const long long g = e / args.n, off = e % args.n;
   wr_f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
-  const float* base = args.partials + g * args.splits * args.n + off;
-  for (int r = 0; r < args.splits; ++r) {
-    const float* p = base + r * args.n;
-    lo += *(const wr_f32x4*)p;
-    hi += *(const wr_f32x4*)(p + 4);
-  }
+  wr_accumulate(lo, hi, args.partials + g * args.splits * args.n + off, args.n, args.splits);
   wr_bf16x8 v;
   for (int j = 0; j < 4; ++j) {
     v[j] = (__bf16)lo[j];
