@@ -379,13 +379,15 @@ def test_dkdv_slot_fusion_bitwise(gpu, b, h, s):
     assert rel_err(outs[1][1].cpu().float(), rv) <= TOL
 
 
-@pytest.mark.parametrize("shape", [(16, 16, 4096, 128), (2, 3, 320, 128), (1, 2, 192, 128), (3, 5, 2048, 128)])
+@pytest.mark.parametrize("shape", [(16, 16, 4096, 128), (2, 3, 320, 128), (1, 2, 192, 128), (3, 5, 2048, 128),
+                                   (3, 25, 1024, 128)])
 @pytest.mark.parametrize("variant", ["mha_d128_sb", "mha_d128_pers", "mha_d128_stream"])
 def test_pingpong_forms_equal_default(gpu, shape, variant):
     """mha_d128_sb moves only group B's barrier (between its PV and QK MMAs), and mha_d128_pers
-    runs the same body per tile in persistent programs (256 workgroups, tiles blockIdx.x +
-    k * gridDim.x), so every wave computes the same operations in the same order as mha_d128: O
-    agrees bit for bit.  The LSE epilogue (c*m + log2(l)) may be contracted into one fma in one
+    and mha_d128_stream run the same steps per tile in persistent programs (256 workgroups, tiles
+    blockIdx.x + k * gridDim.x; 300 tiles at B3 H25 S1024 give some programs two tiles and others
+    one), so every wave computes the same operations in the same order as mha_d128: O agrees bit
+    for bit.  The LSE epilogue (c*m + log2(l)) may be contracted into one fma in one
     build and not the other (HIP contracts by default), so the LSE agrees to a few ulps."""
     announce(f"{variant} vs mha_d128 {shape}")
     q, k, v = (seeded_normal(shape, sd) for sd in (50, 51, 52))
